@@ -1,0 +1,80 @@
+"""ctypes binding of libspecmoe_mi355x.so (the C ABI in include/specmoe_mi355x.h).
+
+The library is built in-tree by ``ae_amd.build``. Loading fails loudly when it is missing:
+there is no fallback implementation of any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from .build import LIB_PATH
+
+SMX_F32, SMX_F16, SMX_BF16 = 0, 1, 2
+SMX_OK = 0
+SMX_ERR_INVALID_ARG = 1000
+SMX_ERR_UNSUPPORTED = 1001
+SMX_ERR_WORKSPACE = 1002
+SMX_ERR_MISALIGNED = 1003
+
+# (name, restype, argtypes) of every exported entry point, in header order.
+_c_void_p, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
+SIGNATURES = [
+    ("smx_version", ctypes.c_int, []),
+    ("smx_error_string", ctypes.c_char_p, [_i32]),
+    ("smx_topk_softmax", ctypes.c_int,
+     [_c_void_p, _i32, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p]),
+    ("smx_moe_align_block_size", ctypes.c_int,
+     [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    ("smx_moe_workspace_size", _sz, [_i64, _i64, _i64, _i64, _i64, _i32]),
+    ("smx_stack_fused_moe", ctypes.c_int,
+     [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
+      _c_void_p, _c_void_p, _i64, _c_void_p, _sz, _c_void_p]),
+    ("smx_fused_moe_forward", ctypes.c_int,
+     [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,
+      _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
+    ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
+]
+
+_lock = threading.Lock()
+_lib = None
+
+
+class SmxError(RuntimeError):
+    """A non-zero status from the C ABI."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed with status {code}: {msg}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded once per process)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise ImportError(
+                    f"{LIB_PATH} is missing: build it with `python -m ae_amd.build` "
+                    "(the MoE path has no fallback implementation)")
+            handle = ctypes.CDLL(LIB_PATH)
+            for name, restype, argtypes in SIGNATURES:
+                fn = getattr(handle, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _lib = handle
+    return _lib
+
+
+def check(fn: str, code: int) -> None:
+    if code != SMX_OK:
+        msg = lib().smx_error_string(code).decode()
+        raise SmxError(fn, code, msg)
+
+
+def call(fn: str, *args) -> None:
+    """Invoke entry point `fn` and raise SmxError on a non-zero status."""
+    check(fn, getattr(lib(), fn)(*args))

@@ -1,0 +1,266 @@
+// C ABI of libspecmoe_mi355x.so (declared in include/specmoe_mi355x.h).
+//
+// Host code only: argument checks, the launch plan (a pure function of the shapes, so the
+// grid never depends on routing results and nothing waits on the device), workspace layout,
+// and the stream-ordered launch sequence route -> gate/up -> down -> combine.
+#include "../../include/specmoe_mi355x.h"
+#include "smx_kernels.h"
+
+namespace {
+
+using namespace smx;
+
+constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
+constexpr size_t kAlign = 256;
+constexpr int64_t kTargetDownWaves = 8192;  // enough waves to cover 256 CUs several times
+
+// Optional measurement events (smx_set_profile_events): recorded on the launch stream
+// before routing and after each of the four kernels.
+constexpr int kProfileEvents = 5;
+hipEvent_t g_profile[kProfileEvents] = {};
+bool g_profiling = false;
+
+void mark(int i, hipStream_t s) {
+  if (g_profiling) (void)hipEventRecord(g_profile[i], s);
+}
+
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+bool valid_dtype(int dt) { return dt == kF32 || dt == kF16 || dt == kBF16; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct Plan {
+  int N = 0;
+  int max_active = 0;
+  int tok_tiles = 1;
+  int splits = 1;
+  int split_steps = 0;
+  size_t hdr = 0, act_expert = 0, act_off = 0, act_cnt = 0, sorted_f = 0, w = 0, ids = 0;
+  size_t act = 0, part = 0, total = 0;
+};
+
+// Shape limits shared by the workspace query and the entry points.
+int check_shape(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype) {
+  if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0 || !valid_dtype(dtype)) return SMX_ERR_INVALID_ARG;
+  if (k > E) return SMX_ERR_INVALID_ARG;
+  if (E > kMaxExperts || k > kMaxTopK) return SMX_ERR_UNSUPPORTED;
+  if (T * k > kMaxAssignments) return SMX_ERR_UNSUPPORTED;
+  const int64_t eb = dtype_bytes(dtype);
+  const int64_t chunk = static_cast<int64_t>(kStepBytes) * kUnroll;  // bytes per pipelined chunk
+  if ((H * eb) % chunk != 0 || (I * eb) % chunk != 0) return SMX_ERR_UNSUPPORTED;
+  if (H % (kRowTile * kDownRows) != 0 || I % kRowTile != 0) return SMX_ERR_UNSUPPORTED;
+  if (H > (1 << 20) || I > (1 << 20)) return SMX_ERR_UNSUPPORTED;
+  return SMX_OK;
+}
+
+Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype) {
+  Plan p;
+  p.N = static_cast<int>(T * k);
+  p.max_active = static_cast<int>(E < p.N ? E : p.N);
+  const int64_t tiles = (T + kTokTile - 1) / kTokTile;
+  p.tok_tiles = static_cast<int>(tiles < 1 ? 1 : (tiles > kMaxTokTiles ? kMaxTokTiles : tiles));
+  const int64_t eb = dtype_bytes(dtype);
+  const int64_t nchunks = I * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+  const int64_t units = static_cast<int64_t>(p.max_active > 0 ? p.max_active : 1) * (H / (kRowTile * kDownRows));
+  int64_t want = (kTargetDownWaves + units - 1) / units;
+  if (want < 1) want = 1;
+  int64_t s = 1;
+  for (int64_t d = 1; d <= nchunks && d <= want; ++d)
+    if (nchunks % d == 0) s = d;
+  p.splits = static_cast<int>(s);
+  p.split_steps = static_cast<int>(nchunks / s * kUnroll);
+  size_t o = 0;
+  p.hdr = o;        o = align_up(o + 64);
+  p.act_expert = o; o = align_up(o + sizeof(int32_t) * E);
+  p.act_off = o;    o = align_up(o + sizeof(int32_t) * E);
+  p.act_cnt = o;    o = align_up(o + sizeof(int32_t) * E);
+  p.sorted_f = o;   o = align_up(o + sizeof(int32_t) * p.N);
+  p.w = o;          o = align_up(o + sizeof(float) * p.N);
+  p.ids = o;        o = align_up(o + sizeof(int32_t) * p.N);
+  p.act = o;        o = align_up(o + static_cast<size_t>(eb) * p.N * I);
+  p.part = o;       o = align_up(o + sizeof(float) * static_cast<size_t>(s) * p.N * H);
+  p.total = o;
+  return p;
+}
+
+RouteBuffers carve(const Plan& p, void* ws) {
+  char* b = static_cast<char*>(ws);
+  RouteBuffers rb;
+  rb.hdr = reinterpret_cast<int32_t*>(b + p.hdr);
+  rb.act_expert = reinterpret_cast<int32_t*>(b + p.act_expert);
+  rb.act_off = reinterpret_cast<int32_t*>(b + p.act_off);
+  rb.act_cnt = reinterpret_cast<int32_t*>(b + p.act_cnt);
+  rb.sorted_f = reinterpret_cast<int32_t*>(b + p.sorted_f);
+  return rb;
+}
+
+// Shared tail of both MoE entry points: expert kernels then combine.
+int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t T, int64_t H,
+                int64_t I, int64_t E, int64_t k, const void* pool, int64_t num_slots,
+                int64_t page_elems, const int64_t* e2s, const float* w, const int32_t* ids,
+                void* ws, hipStream_t s) {
+  char* b = static_cast<char*>(ws);
+  ExpertArgs a{};
+  a.x = hidden;
+  a.pool = pool;
+  a.page_elems = page_elems;
+  a.e2s = e2s;
+  a.rb = carve(p, ws);
+  a.T = static_cast<int>(T);
+  a.H = static_cast<int>(H);
+  a.I = static_cast<int>(I);
+  a.k = static_cast<int>(k);
+  a.act = b + p.act;
+  a.part = reinterpret_cast<float*>(b + p.part);
+  a.splits = p.splits;
+  a.split_steps = p.split_steps;
+  hipError_t err = launch_gateup(dtype, a, p.max_active, p.tok_tiles, s);
+  if (err != hipSuccess) return static_cast<int>(err);
+  mark(2, s);
+  err = launch_down(dtype, a, p.max_active, p.tok_tiles, s);
+  if (err != hipSuccess) return static_cast<int>(err);
+  mark(3, s);
+  CombineArgs c{};
+  c.part = a.part;
+  c.w = w;
+  c.ids = ids;
+  c.e2s = e2s;
+  c.num_slots = num_slots;
+  c.y = out;
+  c.T = static_cast<int>(T);
+  c.H = static_cast<int>(H);
+  c.k = static_cast<int>(k);
+  c.E = static_cast<int>(E);
+  c.splits = p.splits;
+  err = launch_combine(dtype, c, s);
+  if (err != hipSuccess) return static_cast<int>(err);
+  mark(4, s);
+  return SMX_OK;
+}
+
+int check_pool(const void* hidden, const void* out, const void* pool, int64_t num_slots,
+               int64_t page_elems, const int64_t* e2s, int64_t H, int64_t* I) {
+  if (!hidden || !out || !pool || !e2s || num_slots <= 0 || page_elems <= 0) return SMX_ERR_INVALID_ARG;
+  if (page_elems % (3 * H) != 0) return SMX_ERR_INVALID_ARG;
+  *I = page_elems / (3 * H);
+  if (!aligned16(hidden) || !aligned16(out) || !aligned16(pool)) return SMX_ERR_MISALIGNED;
+  return SMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int smx_version(void) { return kVersion; }
+
+const char* smx_error_string(int code) {
+  switch (code) {
+    case SMX_OK: return "success";
+    case SMX_ERR_INVALID_ARG: return "invalid argument";
+    case SMX_ERR_UNSUPPORTED: return "shape outside the supported limits";
+    case SMX_ERR_WORKSPACE: return "workspace too small";
+    case SMX_ERR_MISALIGNED: return "tensor base not 16-byte aligned";
+    default: return hipGetErrorString(static_cast<hipError_t>(code));
+  }
+}
+
+int smx_topk_softmax(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t top_k,
+                     int renormalize, float* topk_weights, int32_t* topk_ids, void* stream) {
+  if (T < 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(logits_dtype)) return SMX_ERR_INVALID_ARG;
+  if (E > kMaxExperts || top_k > kMaxTopK || T > (int64_t{1} << 30) / top_k) return SMX_ERR_UNSUPPORTED;
+  if (T == 0) return SMX_OK;
+  if (!logits || !topk_weights || !topk_ids) return SMX_ERR_INVALID_ARG;
+  return static_cast<int>(launch_topk_softmax(logits, logits_dtype, static_cast<int>(T), static_cast<int>(E),
+                                              static_cast<int>(top_k), renormalize, topk_weights, topk_ids,
+                                              static_cast<hipStream_t>(stream)));
+}
+
+int smx_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_size,
+                             int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_tokens_post_pad,
+                             void* stream) {
+  if (numel < 0 || E <= 0 || block_size <= 0) return SMX_ERR_INVALID_ARG;
+  if (E > kMaxExperts || numel > kMaxAssignments || block_size > (1 << 16)) return SMX_ERR_UNSUPPORTED;
+  if (!sorted_ids || !expert_ids || !num_tokens_post_pad || (numel > 0 && !topk_ids)) return SMX_ERR_INVALID_ARG;
+  return static_cast<int>(launch_align(topk_ids, static_cast<int>(numel), static_cast<int>(E),
+                                       static_cast<int>(block_size), sorted_ids, expert_ids,
+                                       num_tokens_post_pad, static_cast<hipStream_t>(stream)));
+}
+
+size_t smx_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k, int dtype) {
+  if (check_shape(T, H, I, E, top_k, dtype) != SMX_OK) return 0;
+  return make_plan(T, H, I, E, top_k, dtype).total;
+}
+
+int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                        const void* pool, int64_t num_slots, int64_t page_elems,
+                        const int64_t* expert_to_slot, int64_t E,
+                        const float* topk_weights, const int32_t* topk_ids, int64_t top_k,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (H <= 0) return SMX_ERR_INVALID_ARG;
+  int64_t I = 0;
+  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, &I);
+  if (rc != SMX_OK) return rc;
+  rc = check_shape(T, H, I, E, top_k, dtype);
+  if (rc != SMX_OK) return rc;
+  if (T == 0) return SMX_OK;
+  if (!topk_weights || !topk_ids || !workspace) return SMX_ERR_INVALID_ARG;
+  const Plan p = make_plan(T, H, I, E, top_k, dtype);
+  if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mark(0, s);
+  hipError_t err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k),
+                                0, nullptr, nullptr, topk_ids, expert_to_slot, num_slots, carve(p, workspace), s);
+  if (err != hipSuccess) return static_cast<int>(err);
+  mark(1, s);
+  return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
+                     expert_to_slot, topk_weights, topk_ids, workspace, s);
+}
+
+int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                          const void* router_logits, int logits_dtype, int64_t E, int64_t top_k,
+                          int renormalize, const void* pool, int64_t num_slots, int64_t page_elems,
+                          const int64_t* expert_to_slot, float* topk_weights_out,
+                          int32_t* topk_ids_out, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (H <= 0 || !valid_dtype(logits_dtype)) return SMX_ERR_INVALID_ARG;
+  int64_t I = 0;
+  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, &I);
+  if (rc != SMX_OK) return rc;
+  rc = check_shape(T, H, I, E, top_k, dtype);
+  if (rc != SMX_OK) return rc;
+  if (T == 0) return SMX_OK;
+  if (!router_logits || !workspace) return SMX_ERR_INVALID_ARG;
+  const Plan p = make_plan(T, H, I, E, top_k, dtype);
+  if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
+  char* b = static_cast<char*>(workspace);
+  float* w = topk_weights_out ? topk_weights_out : reinterpret_cast<float*>(b + p.w);
+  int32_t* ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t*>(b + p.ids);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mark(0, s);
+  hipError_t err = launch_route(router_logits, logits_dtype, static_cast<int>(T), static_cast<int>(E),
+                                static_cast<int>(top_k), renormalize, w, ids, nullptr, expert_to_slot,
+                                num_slots, carve(p, workspace), s);
+  if (err != hipSuccess) return static_cast<int>(err);
+  mark(1, s);
+  return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
+                     expert_to_slot, w, ids, workspace, s);
+}
+
+int smx_set_profile_events(void* const* events, int count) {
+  if (events == nullptr || count == 0) {
+    g_profiling = false;
+    return SMX_OK;
+  }
+  if (count != kProfileEvents) return SMX_ERR_INVALID_ARG;
+  for (int i = 0; i < kProfileEvents; ++i) {
+    if (events[i] == nullptr) return SMX_ERR_INVALID_ARG;
+    g_profile[i] = static_cast<hipEvent_t>(events[i]);
+  }
+  g_profiling = true;
+  return SMX_OK;
+}
+
+}  // extern "C"

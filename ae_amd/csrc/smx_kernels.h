@@ -1,0 +1,71 @@
+// Internal interface between the kernel translation units and the C ABI (capi.hip).
+#pragma once
+
+#include "smx_common.h"
+
+namespace smx {
+
+// Routing limits (one workgroup sorts all assignments in LDS).
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / kWave;
+constexpr int kMaxExperts = 256;
+constexpr int kMaxExpertsPerLane = kMaxExperts / kWave;
+constexpr int kMaxAssignments = 16384;  // T * top_k
+constexpr int kMaxTopK = 16;
+
+// Expert-kernel geometry.
+constexpr int kExpertThreads = 256;                 // 4 independent waves per workgroup
+constexpr int kExpertWaves = kExpertThreads / kWave;
+constexpr int kRowTile = 16;                        // weight rows per MFMA tile
+constexpr int kTokTile = 16;                        // token columns per MFMA tile
+constexpr int kStepBytes = 64;                      // row bytes one 16-byte/lane load step covers
+constexpr int kUnroll = 4;                          // load steps per pipelined chunk
+constexpr int kDownRows = 2;                        // row tiles per wave in the down projection
+constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 tokens)
+
+struct RouteBuffers {
+  int32_t* hdr;         // [0] active experts, [1] dropped-assignment flag
+  int32_t* act_expert;  // [E] expert id of each active expert (ascending)
+  int32_t* act_off;     // [E] first sorted position of each active expert
+  int32_t* act_cnt;     // [E] assignments routed to each active expert
+  int32_t* sorted_f;    // [T*k] flat assignment index f = t*k + j at each sorted position
+};
+
+struct ExpertArgs {
+  const void* x;        // [T, H] hidden states
+  const void* pool;     // [num_slots, page_elems] expert pages
+  int64_t page_elems;
+  const int64_t* e2s;   // [E] expert -> pool slot
+  RouteBuffers rb;
+  int T, H, I, k;
+  void* act;            // [T*k, I] silu(gate)*up, row = sorted position
+  float* part;          // [splits, T*k, H] fp32 partial down projections, row = f
+  int splits;           // K splits of the down projection
+  int split_steps;      // load steps per split
+};
+
+struct CombineArgs {
+  const float* part;
+  const float* w;       // [T*k]
+  const int32_t* ids;   // [T*k]
+  const int64_t* e2s;
+  int64_t num_slots;
+  void* y;              // [T, H]
+  int T, H, k, E, splits;
+};
+
+hipError_t launch_topk_softmax(const void* logits, int ldt, int T, int E, int k, int renorm,
+                               float* w, int32_t* ids, hipStream_t s);
+hipError_t launch_align(const int32_t* ids, int N, int E, int bm, int32_t* sorted_ids,
+                        int32_t* expert_ids, int32_t* ntp, hipStream_t s);
+hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int renorm,
+                        float* w_out, int32_t* ids_out, const int32_t* ids_in,
+                        const int64_t* e2s, int64_t num_slots, const RouteBuffers& rb,
+                        hipStream_t s);
+hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_active, int tok_tiles,
+                         hipStream_t s);
+hipError_t launch_down(int dtype, const ExpertArgs& a, int max_active, int tok_tiles,
+                       hipStream_t s);
+hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s);
+
+}  // namespace smx

@@ -1,0 +1,147 @@
+"""Fused MoE operators on MI355X: the functions of specmoe/layers/fused_moe_kernel.py.
+
+``moe_align_block_size`` and ``stack_fused_moe`` keep the reference's names, arguments,
+return values and assertions; the work runs in libspecmoe_mi355x.so (HIP, gfx950).
+``fused_moe_forward`` is routing + experts in one library call, used by FusedMoE.forward.
+
+Expert pool contract (specmoe/layers/FusedMoE.py:485-505 packs it; the pool is allocated at
+specmoe/backend/execution_engine.py:1189): ``w1`` is ``[P, 3*I*H]``, each page holding
+``[W1 gate (I x H) | W3 up (I x H) | W2 down (H x I)]`` row-major, and ``indicies[e]`` (int64,
+on the GPU) names the page of expert ``e``. Only the pages of routed experts are read.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from .. import _lib
+from ._torch import dtype_code, ptr, require_gpu, stream_of, workspace
+
+
+def moe_align_block_size(topk_ids: torch.Tensor, block_size: int,
+                         num_experts: int) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Sort flat assignments by expert and pad each expert's run to a multiple of block_size.
+
+    Reference: specmoe/layers/fused_moe_kernel.py:16-85. Returns
+    ``(sorted_token_ids, expert_ids, num_tokens_post_padded)`` with the reference's sizes:
+    ``sorted_token_ids`` has ``numel + E*(block_size-1)`` entries, padding holds ``numel``;
+    ``expert_ids`` has ``cdiv(len(sorted_token_ids), block_size)`` entries, the expert of each
+    block (entries past ``num_tokens_post_padded / block_size`` are -1 here; the reference
+    leaves them unset). Within an expert, flat indices appear in ascending order.
+    """
+    require_gpu(topk_ids)
+    ids = topk_ids.contiguous()
+    if ids.dtype != torch.int32:
+        ids = ids.to(torch.int32)
+    numel = ids.numel()
+    max_num_tokens_padded = numel + num_experts * (block_size - 1)
+    sorted_ids = torch.empty((max_num_tokens_padded,), dtype=torch.int32, device=ids.device)
+    max_num_m_blocks = (max_num_tokens_padded + block_size - 1) // block_size
+    expert_ids = torch.empty((max_num_m_blocks,), dtype=torch.int32, device=ids.device)
+    num_tokens_post_pad = torch.empty((1,), dtype=torch.int32, device=ids.device)
+    _lib.call("smx_moe_align_block_size", ptr(ids), numel, num_experts, block_size,
+              ptr(sorted_ids), ptr(expert_ids), ptr(num_tokens_post_pad), stream_of(ids))
+    return sorted_ids, expert_ids, num_tokens_post_pad
+
+
+def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:
+    H = hidden_states.shape[1]
+    _, page_size = w1.shape
+    assert page_size % (3 * H) == 0, "pool page is not 3*I*H elements"
+    return H, page_size // (3 * H)
+
+
+def _as_index(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    t = t.contiguous()
+    return t if t.dtype == dtype else t.to(dtype)
+
+
+def stack_fused_moe(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    indicies: torch.Tensor,
+    gating_output: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    renormalize: bool,
+    inplace: bool = False,
+) -> torch.Tensor:
+    """MoE experts over a pooled weight cache, routing given.
+
+    Reference: specmoe/layers/fused_moe_kernel.py:253-349. ``y[t] = sum_j w[t,j] *
+    W2_e(silu(W1_e x_t) * W3_e x_t)`` with e = topk_ids[t,j] and expert e's weights in page
+    ``indicies[e]`` of ``w1``. With ``inplace`` the result is written into hidden_states
+    (the reference's ``torch.sum(..., out=hidden_states)``) and hidden_states is returned.
+    ``renormalize`` is accepted for signature parity; like the reference, the weights are
+    used as given.
+    """
+    # Check constraints (same as the reference).
+    assert hidden_states.shape[0] == gating_output.shape[0], "Number of tokens mismatch"
+    E = gating_output.shape[1]
+    assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
+    assert w1.is_contiguous(), "Expert weights1 must be contiguous"
+    assert hidden_states.dtype in [torch.float32, torch.float16, torch.bfloat16]
+    assert w1.dtype == hidden_states.dtype, "expert pool and hidden states dtypes differ"
+    require_gpu(hidden_states, w1, indicies, topk_weights, topk_ids)
+    H, I = _pool_geometry(hidden_states, w1)
+    T = hidden_states.shape[0]
+    top_k = topk_ids.shape[1]
+    out = hidden_states if inplace else torch.empty_like(hidden_states)
+    slots = _as_index(indicies, torch.int64)
+    ids = _as_index(topk_ids, torch.int32)
+    w = _as_index(topk_weights, torch.float32)
+    dt = dtype_code(hidden_states.dtype)
+    nbytes = _lib.lib().smx_moe_workspace_size(T, H, I, E, top_k, dt)
+    if nbytes == 0 and T > 0:
+        raise ValueError(f"unsupported MoE shape T={T} H={H} I={I} E={E} top_k={top_k}")
+    ws = workspace(nbytes, hidden_states.device)
+    _lib.call("smx_stack_fused_moe", ptr(hidden_states), ptr(out), dt, T, H, ptr(w1),
+              w1.shape[0], w1.shape[1], ptr(slots), E, ptr(w), ptr(ids), top_k,
+              ptr(ws), ws.numel(), stream_of(hidden_states))
+    return out
+
+
+def fused_moe_forward(
+    hidden_states: torch.Tensor,
+    router_logits: torch.Tensor,
+    w1: torch.Tensor,
+    indicies: torch.Tensor,
+    top_k: int,
+    renormalize: bool,
+    inplace: bool = True,
+    return_routing: bool = False,
+):
+    """Routing (select_experts) and stack_fused_moe in one library call.
+
+    Reference: the body of UnquantizedFusedMoEMethod.forward_cuda,
+    specmoe/layers/FusedMoE.py:155-196 (select_experts at :174, stack_fused_moe at :187,
+    inplace=True). With ``return_routing`` also returns ``(topk_weights, topk_ids)``.
+    """
+    assert hidden_states.shape[0] == router_logits.shape[0], "Number of tokens mismatch"
+    assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
+    assert w1.is_contiguous(), "Expert weights1 must be contiguous"
+    assert hidden_states.dtype in [torch.float32, torch.float16, torch.bfloat16]
+    assert w1.dtype == hidden_states.dtype, "expert pool and hidden states dtypes differ"
+    require_gpu(hidden_states, router_logits, w1, indicies)
+    H, I = _pool_geometry(hidden_states, w1)
+    T, E = router_logits.shape
+    logits = router_logits.contiguous()
+    out = hidden_states if inplace else torch.empty_like(hidden_states)
+    slots = _as_index(indicies, torch.int64)
+    dt = dtype_code(hidden_states.dtype)
+    nbytes = _lib.lib().smx_moe_workspace_size(T, H, I, E, top_k, dt)
+    if nbytes == 0 and T > 0:
+        raise ValueError(f"unsupported MoE shape T={T} H={H} I={I} E={E} top_k={top_k}")
+    ws = workspace(nbytes, hidden_states.device)
+    w = ids = None
+    if return_routing:
+        w = torch.empty((T, top_k), dtype=torch.float32, device=hidden_states.device)
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=hidden_states.device)
+    _lib.call("smx_fused_moe_forward", ptr(hidden_states), ptr(out), dt, T, H, ptr(logits),
+              dtype_code(logits.dtype), E, top_k, int(bool(renormalize)), ptr(w1), w1.shape[0],
+              w1.shape[1], ptr(slots), ptr(w), ptr(ids), ptr(ws), ws.numel(),
+              stream_of(hidden_states))
+    if return_routing:
+        return out, w, ids
+    return out

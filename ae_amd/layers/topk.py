@@ -1,0 +1,69 @@
+"""Top-k softmax routing: the `select_experts` the reference's MoE layer calls.
+
+Reference call site: specmoe/layers/FusedMoE.py:174-185, which calls
+``sglang.srt.layers.moe.topk.select_experts`` (sglang==0.4.5.post3, not vendored): an fp32
+softmax over the experts (sgl_kernel.topk_softmax), top-k selection in descending order
+with ties resolved to the lower expert index, then an optional renormalisation
+``w / w.sum(-1)``. Returns ``(topk_weights fp32 [T,k], topk_ids int32 [T,k])``.
+"""
+from __future__ import annotations
+
+from typing import Callable, Optional, Tuple
+
+import torch
+
+from .. import _lib
+from ._torch import dtype_code, ptr, require_gpu, stream_of
+
+
+def check_routing_options(use_grouped_topk: bool, topk_group: Optional[int],
+                          num_expert_group: Optional[int],
+                          custom_routing_function: Optional[Callable],
+                          correction_bias: Optional[torch.Tensor],
+                          routed_scaling_factor: Optional[float]) -> None:
+    """Reject the select_experts options this build does not implement.
+
+    Grouped top-k with a single group is plain top-k and is accepted.
+    """
+    if use_grouped_topk and not (num_expert_group in (None, 1) and topk_group in (None, 1)):
+        raise NotImplementedError("grouped top-k with more than one expert group")
+    if custom_routing_function is not None:
+        raise NotImplementedError("custom_routing_function")
+    if correction_bias is not None:
+        raise NotImplementedError("correction_bias (biased grouped top-k)")
+    if routed_scaling_factor not in (None, 1.0):
+        raise NotImplementedError("routed_scaling_factor other than 1.0")
+
+
+def select_experts(
+    hidden_states: torch.Tensor,
+    router_logits: torch.Tensor,
+    top_k: int,
+    use_grouped_topk: bool = False,
+    renormalize: bool = True,
+    topk_group: Optional[int] = None,
+    num_expert_group: Optional[int] = None,
+    custom_routing_function: Optional[Callable] = None,
+    correction_bias: Optional[torch.Tensor] = None,
+    torch_native: bool = False,
+    routed_scaling_factor: Optional[float] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    check_routing_options(use_grouped_topk, topk_group, num_expert_group,
+                          custom_routing_function, correction_bias, routed_scaling_factor)
+    if torch_native:
+        raise NotImplementedError("torch_native routing (this build routes on the GPU only)")
+    assert hidden_states.shape[0] == router_logits.shape[0], "Number of tokens mismatch"
+    require_gpu(router_logits)
+    logits = router_logits.contiguous()
+    T, E = logits.shape
+    w = torch.empty((T, top_k), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((T, top_k), dtype=torch.int32, device=logits.device)
+    _lib.call("smx_topk_softmax", ptr(logits), dtype_code(logits.dtype), T, E, top_k,
+              int(bool(renormalize)), ptr(w), ptr(ids), stream_of(logits))
+    return w, ids
+
+
+def fused_topk(hidden_states: torch.Tensor, gating_output: torch.Tensor, topk: int,
+               renormalize: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """sglang's fused_topk (the ungrouped branch select_experts dispatches to)."""
+    return select_experts(hidden_states, gating_output, topk, False, renormalize)

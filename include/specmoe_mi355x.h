@@ -1,0 +1,134 @@
+/*
+ * specmoe_mi355x.h -- C ABI of the MI355X (gfx950) MoE verify-step hot path.
+ *
+ * One shared library, libspecmoe_mi355x.so, built with hipcc --offload-arch=gfx950.
+ * Every entry point:
+ *   - takes plain device pointers and sizes (no framework types);
+ *   - is stream-ordered on the hipStream_t passed as `stream` (NULL = default stream);
+ *   - never synchronises the host and never allocates device memory: scratch space is the
+ *     caller's `workspace` (size from smx_moe_workspace_size);
+ *   - returns 0 on success, an SMX_ERR_* code (>= 1000) for a rejected argument, or the
+ *     hipError_t of a failed launch. smx_error_string() names every code.
+ *
+ * Tensors are row-major and densely packed. Element types are SMX_F32 / SMX_F16 / SMX_BF16.
+ *
+ * Expert pool ("page") layout, one page per pool slot, page_elems = 3*I*H elements:
+ *   [ W1 = gate (I x H) | W3 = up (I x H) | W2 = down (H x I) ]
+ * (reference: specmoe/layers/FusedMoE.py:485-505, the weight_loader that packs it, and
+ *  specmoe/layers/fused_moe_kernel.py:289-290, which derives I from the page size).
+ */
+#ifndef SPECMOE_MI355X_H
+#define SPECMOE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum smx_dtype { SMX_F32 = 0, SMX_F16 = 1, SMX_BF16 = 2 };
+
+enum smx_status {
+  SMX_OK = 0,
+  SMX_ERR_INVALID_ARG = 1000,     /* null pointer, negative size, top_k > E, ... */
+  SMX_ERR_UNSUPPORTED = 1001,     /* shape outside the kernels' limits (see below) */
+  SMX_ERR_WORKSPACE = 1002,       /* workspace smaller than smx_moe_workspace_size() */
+  SMX_ERR_MISALIGNED = 1003       /* a tensor base is not 16-byte aligned */
+};
+
+/* Limits: 1 <= E <= 256; 1 <= top_k <= min(E, 16); T*top_k <= 16384;
+ * H and I multiples of 128 for 16-bit types and of 64 for fp32 (a weight row is a whole
+ * number of 256-byte chunks); H, I <= 2^20. T == 0 is a no-op. Larger T*top_k or E
+ * return SMX_ERR_UNSUPPORTED. */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int smx_version(void);
+
+/* Human-readable name of a status code returned by any entry point. */
+const char* smx_error_string(int code);
+
+/*
+ * Routing: fp32 softmax over E experts, then top_k rounds of arg-max (ties go to the lower
+ * expert index), optional renormalisation w /= sum_j w.
+ * Replaces sglang.srt.layers.moe.topk.select_experts(use_grouped_topk=False) as called at
+ * specmoe/layers/FusedMoE.py:174-185 (sglang==0.4.5.post3, which dispatches to
+ * sgl_kernel.topk_softmax and renormalises in torch).
+ *   logits  [T, E] of logits_dtype
+ *   topk_weights [T, top_k] fp32 out, topk_ids [T, top_k] int32 out (descending weight).
+ */
+int smx_topk_softmax(const void* logits, int logits_dtype, int64_t T, int64_t E,
+                     int64_t top_k, int renormalize,
+                     float* topk_weights, int32_t* topk_ids, void* stream);
+
+/*
+ * Token/expert alignment in the reference's padded format.
+ * Replaces moe_align_block_size (specmoe/layers/fused_moe_kernel.py:16-85, which wraps
+ * sgl_kernel.moe_align_block_size from sgl-kernel==0.1.2).
+ *   topk_ids  [numel] int32, values in [0, E)
+ *   sorted_ids  [numel + E*(block_size-1)] int32 out: for each expert in ascending order, the
+ *               flat indices f (ascending) routed to it, then padding up to a multiple of
+ *               block_size; every padding slot holds the sentinel `numel`.
+ *   expert_ids  [ceil_div(numel + E*(block_size-1), block_size)] int32 out: the expert of each
+ *               block; blocks at and past num_tokens_post_pad/block_size hold -1.
+ *   num_tokens_post_pad [1] int32 out: sum over experts of round_up(count, block_size).
+ */
+int smx_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E,
+                             int64_t block_size, int32_t* sorted_ids, int32_t* expert_ids,
+                             int32_t* num_tokens_post_pad, void* stream);
+
+/* Bytes of workspace the two MoE entry points below need for these sizes. */
+size_t smx_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
+                              int dtype);
+
+/*
+ * The expert computation with routing already done:
+ *   y[t] = sum_j w[t,j] * W2_e (silu(W1_e x[t]) * (W3_e x[t])),  e = topk_ids[t,j],
+ * with the weights of expert e read from pool page expert_to_slot[e]. Intermediates are
+ * rounded to `dtype` at the reference's points (gate/up outputs, silu*up, each weighted
+ * down output, the final top_k sum); accumulation is fp32.
+ * Replaces stack_fused_moe (specmoe/layers/fused_moe_kernel.py:253-349).
+ *   hidden  [T, H] dtype;  out [T, H] dtype (may equal hidden: the in-place form)
+ *   pool [num_slots, page_elems] dtype; expert_to_slot [E] int64 (device)
+ *   topk_weights [T, top_k] fp32; topk_ids [T, top_k] int32 (device)
+ * Only pool pages named by expert_to_slot[e] for routed experts e are read.
+ * An id outside [0,E) or a slot outside [0,num_slots) contributes nothing to `out`.
+ */
+int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                        const void* pool, int64_t num_slots, int64_t page_elems,
+                        const int64_t* expert_to_slot, int64_t E,
+                        const float* topk_weights, const int32_t* topk_ids, int64_t top_k,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Routing plus expert computation in one call (smx_topk_softmax then smx_stack_fused_moe,
+ * with the routing and expert sort fused into one launch).
+ * Replaces FusedMoE.forward -> UnquantizedFusedMoEMethod.forward_cuda
+ * (specmoe/layers/FusedMoE.py:508-532 and :155-196).
+ *   router_logits [T, E] of logits_dtype.
+ *   topk_weights_out / topk_ids_out: optional [T, top_k] outputs (NULL to skip).
+ */
+int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                          const void* router_logits, int logits_dtype, int64_t E,
+                          int64_t top_k, int renormalize,
+                          const void* pool, int64_t num_slots, int64_t page_elems,
+                          const int64_t* expert_to_slot,
+                          float* topk_weights_out, int32_t* topk_ids_out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
+ * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
+ * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and
+ * not thread-safe: for benchmarks only.
+ * No counterpart in the reference's operator API; it plays the role of the reference's
+ * CUDA-event timing around post_attention (specmoe/backend/execution_engine.py:450-451,
+ * 740-741, 783-784), at kernel granularity.
+ */
+int smx_set_profile_events(void* const* events, int count);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPECMOE_MI355X_H */

@@ -1,0 +1,273 @@
+"""CPU oracle for SpecMoE's verify-step MoE path -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module,
+and only as the checker (or as the timed CPU restatement in the baseline). The product path
+(ae_amd) never imports it and has no CPU fallback.
+
+A plain numpy restatement of the reference's arithmetic:
+
+  routing   select_experts as called at specmoe/layers/FusedMoE.py:174-185 (sglang 0.4.5.post3
+            -> sgl_kernel.topk_softmax, not vendored): fp32 softmax, top-k with ties to the
+            lower expert index, optional w / sum(w).
+  align     moe_align_block_size, specmoe/layers/fused_moe_kernel.py:16-85 (sgl-kernel 0.1.2
+            underneath, not vendored); pinned by the docstring example at :41-54.
+  experts   stack_fused_moe, specmoe/layers/fused_moe_kernel.py:253-349: per routed
+            assignment, C1 = round(x W13^T) (:332-335, rounded at :203), C2 =
+            round(silu(C1_gate) * C1_up) (:337), C3 = round((C2 W2^T) * w) (:339-342, weight
+            applied at :197-201), y = round(sum_j C3) (:344-347). round() is to the activation
+            dtype; fp32 runs round nowhere (the reference's fp16 store of fp32 GEMM outputs,
+            :248, is not reproduced).
+  page      FusedMoE.weight_loader, specmoe/layers/FusedMoE.py:485-505: one page per expert,
+            [W1 (I x H) | W3 (I x H) | W2 (H x I)].
+
+Routing arithmetic is restated operation for operation (same exp method, same summation
+tree, correctly rounded fp32 divide), so GPU routing weights match this oracle bit for bit.
+GEMM accumulation order is not restated; outputs agree to a stated tolerance.
+
+Parity pinning (tests/test_oracle.py): the align docstring example; brute-force sorting;
+top-k against np.argsort/lexsort selection and hand-built tie cases; exp_nonpos against float64
+exp (<= 2 ulp); the expert math against a float64 textbook SwiGLU MoE built from separate
+gate/up/down matrices through the page packing. No reference test vectors exist beyond the
+align docstring example (the reference ships no tests).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32, F16, BF16 = "f32", "f16", "bf16"
+
+_f32 = np.float32
+
+
+def _c(bits: int) -> np.float32:
+    return np.array([bits], dtype=np.uint32).view(np.float32)[0]
+
+
+# ---------------------------------------------------------------------------------------------
+# dtype helpers: bf16/f16 values travel as float32 arrays holding representable values
+# ---------------------------------------------------------------------------------------------
+def bf16_bits_to_f32(bits: np.ndarray) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_bf16_bits(a: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even float32 -> bf16 bit patterns (NaN stays a quiet NaN)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    nan = (u & 0x7F800000) == 0x7F800000
+    nan &= (u & 0x007FFFFF) != 0
+    r = (u + np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1))) >> 16
+    r = np.where(nan, (u >> 16) | np.uint32(0x40), r)
+    return r.astype(np.uint16)
+
+
+def round_to(a: np.ndarray, dtype: str) -> np.ndarray:
+    a = np.asarray(a, dtype=np.float32)
+    if dtype == BF16:
+        return bf16_bits_to_f32(f32_to_bf16_bits(a))
+    if dtype == F16:
+        with np.errstate(over="ignore"):
+            return a.astype(np.float16).astype(np.float32)
+    if dtype == F32:
+        return a
+    raise ValueError(dtype)
+
+
+def to_f32(a: np.ndarray, dtype: str) -> np.ndarray:
+    """Storage array (uint16 bits for bf16/f16, or float) -> float32 values."""
+    a = np.asarray(a)
+    if a.dtype == np.uint16:
+        if dtype == BF16:
+            return bf16_bits_to_f32(a)
+        if dtype == F16:
+            return a.view(np.float16).astype(np.float32)
+        raise ValueError("uint16 storage needs dtype bf16 or f16")
+    return a.astype(np.float32, copy=False)
+
+
+# ---------------------------------------------------------------------------------------------
+# routing
+# ---------------------------------------------------------------------------------------------
+_LOG2E = _c(0x3FB8AA3B)
+_C1 = _c(0x3F318000)  # 0.693359375, 9 significant bits
+_C2 = _c(0xB95E8083)  # ln2 - C1
+_P = [_c(0x39500D01), _c(0x3AB60B61), _c(0x3C088889), _c(0x3D2AAAAB), _c(0x3E2AAAAB),
+      _f32(0.5), _f32(1.0), _f32(1.0)]  # 1/7! ... 1/2!, 1/1!, 1/0!
+
+
+def exp_nonpos(d: np.ndarray) -> np.ndarray:
+    """exp(d) for d <= 0 in float32: Cody-Waite reduction n = rint(d log2 e),
+    r = (d - n C1) - n C2, degree-7 Taylor polynomial in Horner form, exact scale by 2^n;
+    d < -80 gives 0, NaN gives NaN. Each operation is one IEEE fp32 multiply or add."""
+    d = np.asarray(d, dtype=np.float32)
+    out = np.zeros(d.shape, dtype=np.float32)
+    ok = d >= _f32(-80.0)
+    x = d[ok]
+    n = np.rint(x * _LOG2E).astype(np.float32)
+    r = (x - n * _C1) - n * _C2
+    p = np.full_like(r, _P[0])
+    for c in _P[1:]:
+        p = p * r + c
+    scale = ((n.astype(np.int32) + 127) << 23).astype(np.uint32).view(np.float32)
+    out[ok] = p * scale
+    nan = np.isnan(d)
+    out[nan] = d[nan]
+    return out
+
+
+_LANES = 64
+_PER_LANE = 4  # experts per lane (E <= 256)
+
+
+def softmax_probs(logits: np.ndarray) -> np.ndarray:
+    """fp32 softmax over the last axis with the kernel's summation order: expert e sits on
+    lane e % 64 as its (e // 64)-th value; each lane sums its values in order, then lanes
+    are combined by halving (lane l + lane l+32, then +16, ...). p = ex * (1 / sum)."""
+    x = np.asarray(logits, dtype=np.float32)
+    T, E = x.shape
+    if E > _LANES * _PER_LANE:
+        raise ValueError("E > 256")
+    m = x.max(axis=1, keepdims=True)
+    ex = exp_nonpos(x - m)
+    pad = np.zeros((T, _LANES * _PER_LANE), dtype=np.float32)
+    pad[:, :E] = ex
+    lanes = pad.reshape(T, _PER_LANE, _LANES)
+    s = lanes[:, 0, :].copy()
+    for i in range(1, _PER_LANE):
+        s = s + lanes[:, i, :]
+    half = _LANES // 2
+    while half >= 1:
+        s = s[:, :half] + s[:, half:2 * half]
+        half //= 2
+    inv = _f32(1.0) / s[:, 0]
+    return ex * inv[:, None]
+
+
+def topk_softmax(logits: np.ndarray, top_k: int, renormalize: bool):
+    """-> (topk_weights float32 [T,k], topk_ids int32 [T,k]); ids in descending weight,
+    ties to the lower expert index; renormalised by division by the in-order sum."""
+    p = softmax_probs(logits)
+    T, E = p.shape
+    if not 1 <= top_k <= E:
+        raise ValueError("top_k out of range")
+    work = p.copy()
+    rows = np.arange(T)
+    w = np.empty((T, top_k), dtype=np.float32)
+    ids = np.empty((T, top_k), dtype=np.int32)
+    for j in range(top_k):
+        idx = np.argmax(work, axis=1)  # first occurrence of the max = lowest index
+        w[:, j] = work[rows, idx]
+        ids[:, j] = idx
+        work[rows, idx] = _f32(-1.0)
+    if renormalize:
+        s = w[:, 0].copy()
+        for j in range(1, top_k):
+            s = s + w[:, j]
+        w = w / s[:, None]
+    return w.astype(np.float32), ids
+
+
+select_experts = topk_softmax
+
+
+# ---------------------------------------------------------------------------------------------
+# alignment
+# ---------------------------------------------------------------------------------------------
+def expert_order(ids: np.ndarray, num_experts: int):
+    """Stable expert sort of flat assignments: -> (counts [E], order [N']) where order lists
+    the flat indices f of expert 0 (ascending), then expert 1, ...; ids outside [0,E) dropped."""
+    flat = np.asarray(ids).reshape(-1).astype(np.int64)
+    valid = (flat >= 0) & (flat < num_experts)
+    counts = np.bincount(flat[valid], minlength=num_experts)
+    keys = np.where(valid, flat, num_experts)
+    order = np.argsort(keys, kind="stable")[: int(valid.sum())]
+    return counts, order.astype(np.int32)
+
+
+def moe_align_block_size(topk_ids: np.ndarray, block_size: int, num_experts: int):
+    """Reference format: (sorted_ids [N + E*(BM-1)], expert_ids [cdiv(len, BM)], ntp [1]).
+    Padding slots hold N; blocks past ntp/BM hold -1."""
+    flat = np.asarray(topk_ids).reshape(-1)
+    N = flat.size
+    counts, order = expert_order(flat, num_experts)
+    padded = (counts + block_size - 1) // block_size * block_size
+    seg = np.concatenate([[0], np.cumsum(padded)]).astype(np.int64)
+    length = N + num_experts * (block_size - 1)
+    sorted_ids = np.full(length, N, dtype=np.int32)
+    expert_ids = np.full((length + block_size - 1) // block_size, -1, dtype=np.int32)
+    start = 0
+    for e in range(num_experts):
+        c = int(counts[e])
+        sorted_ids[seg[e]:seg[e] + c] = order[start:start + c]
+        expert_ids[seg[e] // block_size:seg[e + 1] // block_size] = e
+        start += c
+    return sorted_ids, expert_ids, np.array([seg[-1]], dtype=np.int32)
+
+
+# ---------------------------------------------------------------------------------------------
+# experts
+# ---------------------------------------------------------------------------------------------
+def pack_page(w1: np.ndarray, w3: np.ndarray, w2: np.ndarray) -> np.ndarray:
+    """Page of one expert from HF-layout matrices: gate w1 [I,H], up w3 [I,H], down w2 [H,I]."""
+    return np.concatenate([np.asarray(w1).reshape(-1), np.asarray(w3).reshape(-1),
+                           np.asarray(w2).reshape(-1)])
+
+
+def unpack_page(page: np.ndarray, H: int, dtype: str):
+    """-> (W1 [I,H], W3 [I,H], W2 [H,I]) as float32."""
+    page = np.asarray(page).reshape(-1)
+    I = page.size // (3 * H)
+    f = to_f32(page, dtype)
+    return (f[: I * H].reshape(I, H), f[I * H: 2 * I * H].reshape(I, H),
+            f[2 * I * H:].reshape(H, I))
+
+
+def silu(g: np.ndarray) -> np.ndarray:
+    g = np.asarray(g, dtype=np.float32)
+    return g / (_f32(1.0) + np.exp(-g))
+
+
+def stack_fused_moe(x: np.ndarray, pool: np.ndarray, slots: np.ndarray, topk_weights: np.ndarray,
+                    topk_ids: np.ndarray, dtype: str, num_experts: int | None = None) -> np.ndarray:
+    """y [T,H] float32 (values representable in dtype). x and pool may be float arrays or
+    uint16 bit arrays (bf16/f16). Assignments with an id outside [0,E) or a slot outside the
+    pool contribute nothing."""
+    xf = to_f32(x, dtype)
+    T, H = xf.shape
+    ids = np.asarray(topk_ids).reshape(T, -1)
+    k = ids.shape[1]
+    w = np.asarray(topk_weights, dtype=np.float32).reshape(T, k)
+    slots = np.asarray(slots).reshape(-1)
+    E = num_experts if num_experts is not None else slots.size
+    P = pool.shape[0]
+    c3 = np.zeros((T, k, H), dtype=np.float32)
+    counts, order = expert_order(ids, E)
+    start = 0
+    for e in range(E):
+        c = int(counts[e])
+        f = order[start:start + c]
+        start += c
+        if c == 0:
+            continue
+        slot = int(slots[e])
+        if not 0 <= slot < P:
+            continue
+        W1, W3, W2 = unpack_page(pool[slot], H, dtype)
+        t, j = f // k, f % k
+        xe = xf[t]
+        g = round_to(xe @ W1.T, dtype)
+        u = round_to(xe @ W3.T, dtype)
+        a = round_to(silu(g) * u, dtype)
+        d = (a @ W2.T) * w[t, j][:, None]
+        c3[t, j] = round_to(d, dtype)
+    y = c3[:, 0, :].copy()
+    for j in range(1, k):
+        y = y + c3[:, j, :]
+    return round_to(y, dtype)
+
+
+def fused_moe_forward(x, router_logits, pool, slots, top_k: int, renormalize: bool, dtype: str):
+    """FusedMoE.forward: routing then stack_fused_moe -> (y, topk_weights, topk_ids)."""
+    logits = np.asarray(router_logits, dtype=np.float32)
+    w, ids = topk_softmax(logits, top_k, renormalize)
+    y = stack_fused_moe(x, pool, slots, w, ids, dtype, num_experts=logits.shape[1])
+    return y, w, ids

@@ -1,0 +1,53 @@
+"""Shared helpers for the GPU parity tests: torch <-> oracle conversions and input builders."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import moe_ref as ref
+
+TORCH_TO_ORACLE = {torch.bfloat16: ref.BF16, torch.float16: ref.F16, torch.float32: ref.F32}
+
+
+def to_oracle(t: torch.Tensor) -> np.ndarray:
+    """GPU/CPU tensor -> numpy array the oracle reads (uint16 bits for 16-bit types)."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def f32_of(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def max_rel_err(y: np.ndarray, want: np.ndarray) -> float:
+    """max |y - ref| / max |ref| (the parity metric of the layer outputs)."""
+    denom = float(np.abs(want).max())
+    return float(np.abs(y.astype(np.float64) - want.astype(np.float64)).max()) / max(denom, 1e-30)
+
+
+# Output tolerance per activation dtype: max |y - ref| / max |ref|. bf16 carries 8 mantissa
+# bits and four rounding points; the north-star bound is 1e-2.
+TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-4}
+
+
+def make_pool(E: int, H: int, I: int, dtype: torch.dtype, num_slots: int | None = None,
+              seed: int = 0, scale: float = 0.02, device: str = "cuda"):
+    """Pool [P, 3*I*H] of N(0, scale) pages and a permuted expert->slot map (int64)."""
+    P = num_slots or E
+    g = torch.Generator(device=device).manual_seed(seed)
+    pool = (torch.randn((P, 3 * I * H), generator=g, device=device, dtype=torch.float32) * scale).to(dtype)
+    gc = torch.Generator().manual_seed(seed + 1)
+    slots = torch.randperm(P, generator=gc)[:E].to(device=device, dtype=torch.int64)
+    return pool, slots
+
+
+def zipf_gate_logits(x: torch.Tensor, E: int, s: float = 1.2, seed: int = 0) -> torch.Tensor:
+    """Router logits x Wg^T + b, Wg ~ N(0, 0.02), b_e = ln p_e with p_e ~ (e+1)^-s (a skewed
+    expert load), computed in x's dtype."""
+    g = torch.Generator(device=x.device).manual_seed(seed + 7)
+    wg = (torch.randn((E, x.shape[1]), generator=g, device=x.device) * 0.02).to(x.dtype)
+    p = torch.arange(1, E + 1, dtype=torch.float64) ** (-s)
+    b = torch.log(p / p.sum()).to(device=x.device, dtype=x.dtype)
+    return torch.nn.functional.linear(x, wg) + b

@@ -1,0 +1,108 @@
+"""CPU checks of the C ABI: the library loads, exports exactly what include/specmoe_mi355x.h
+declares, and rejects bad arguments before touching the device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from ae_amd import _lib
+from ae_amd.build import LIB_PATH
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "specmoe_mi355x.h")
+L = _lib.lib()
+VP = ctypes.c_void_p
+A = VP(0x10000)  # an aligned fake address: the calls below return before dereferencing it
+
+
+def _declared():
+    with open(HEADER) as f:
+        text = f.read()
+    return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(smx_\w+)\s*\(", text, re.M)
+
+
+def test_library_built_in_tree():
+    assert os.path.exists(LIB_PATH)
+    assert os.path.dirname(LIB_PATH).endswith("ae_amd")
+
+
+def test_exports_every_declared_symbol():
+    names = _declared()
+    assert len(names) == 8, names
+    assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_version_and_error_strings():
+    assert L.smx_version() == 10000
+    for code, word in [(0, b"success"), (1000, b"invalid"), (1001, b"supported"),
+                       (1002, b"workspace"), (1003, b"aligned")]:
+        assert word in L.smx_error_string(code)
+
+
+def test_workspace_size():
+    ws = L.smx_moe_workspace_size
+    assert ws(32, 4096, 14336, 8, 2, 2) > 0
+    assert ws(64, 4096, 14336, 8, 2, 2) > ws(32, 4096, 14336, 8, 2, 2)
+    assert ws(32, 4096, 14336, 8, 2, 0) > ws(32, 4096, 14336, 8, 2, 2)  # fp32 intermediates
+    assert ws(0, 4096, 14336, 8, 2, 2) > 0
+    # rejected shapes report 0
+    assert ws(32, 4000, 14336, 8, 2, 2) == 0   # H not a multiple of 128 (16-bit)
+    assert ws(32, 4096, 14336, 300, 2, 2) == 0  # E > 256
+    assert ws(32, 4096, 14336, 8, 9, 2) == 0    # top_k > E
+    assert ws(9000, 4096, 14336, 8, 2, 2) == 0  # T*k > 16384
+    assert ws(32, 4096, 14336, 8, 2, 7) == 0    # bad dtype
+
+
+def _stack(**kw):
+    a = dict(hidden=A, out=A, dtype=2, T=4, H=256, pool=A, slots=4, page=3 * 256 * 256, e2s=A,
+             E=4, w=A, ids=A, k=2, ws=A, wsb=1 << 30, stream=VP(0))
+    a.update(kw)
+    return L.smx_stack_fused_moe(a["hidden"], a["out"], a["dtype"], a["T"], a["H"], a["pool"],
+                                 a["slots"], a["page"], a["e2s"], a["E"], a["w"], a["ids"],
+                                 a["k"], a["ws"], a["wsb"], a["stream"])
+
+
+def test_stack_rejects_before_launch():
+    assert _stack(hidden=VP(0)) == _lib.SMX_ERR_INVALID_ARG
+    assert _stack(page=1000) == _lib.SMX_ERR_INVALID_ARG           # not 3*I*H
+    assert _stack(hidden=VP(0x10008)) == _lib.SMX_ERR_MISALIGNED
+    assert _stack(k=5) == _lib.SMX_ERR_INVALID_ARG                 # top_k > E
+    assert _stack(wsb=16) == _lib.SMX_ERR_WORKSPACE
+    assert _stack(ws=VP(0x10004)) == _lib.SMX_ERR_MISALIGNED
+    assert _stack(H=100, page=3 * 100 * 256) == _lib.SMX_ERR_UNSUPPORTED
+    assert _stack(T=0) == _lib.SMX_OK                              # empty: nothing launched
+    assert _stack(T=-1) == _lib.SMX_ERR_INVALID_ARG
+
+
+def test_forward_and_routing_reject_before_launch():
+    f = L.smx_fused_moe_forward
+    args = [A, A, 2, 4, 256, A, 2, 4, 2, 1, A, 4, 3 * 256 * 256, A, VP(0), VP(0), A, 1 << 30, VP(0)]
+    bad_logits = list(args)
+    bad_logits[6] = 5
+    assert f(*bad_logits) == _lib.SMX_ERR_INVALID_ARG
+    zero = list(args)
+    zero[3] = 0
+    assert f(*zero) == _lib.SMX_OK
+    assert L.smx_topk_softmax(A, 2, 0, 8, 2, 1, A, A, VP(0)) == _lib.SMX_OK
+    assert L.smx_topk_softmax(A, 2, 4, 8, 9, 1, A, A, VP(0)) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_topk_softmax(A, 2, 4, 300, 2, 1, A, A, VP(0)) == _lib.SMX_ERR_UNSUPPORTED
+    assert L.smx_moe_align_block_size(A, 10, 0, 16, A, A, A, VP(0)) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_moe_align_block_size(A, 20000, 8, 16, A, A, A, VP(0)) == _lib.SMX_ERR_UNSUPPORTED
+
+
+def test_profile_events_argument_checks():
+    assert L.smx_set_profile_events(None, 0) == _lib.SMX_OK
+    three = (VP * 3)(A, A, A)
+    assert L.smx_set_profile_events(three, 3) == _lib.SMX_ERR_INVALID_ARG
+    holes = (VP * 5)(A, A, VP(0), A, A)
+    assert L.smx_set_profile_events(holes, 5) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_set_profile_events(None, 0) == _lib.SMX_OK
+
+
+def test_python_error_mapping():
+    with pytest.raises(_lib.SmxError) as ei:
+        _lib.check("smx_stack_fused_moe", _lib.SMX_ERR_WORKSPACE)
+    assert ei.value.code == _lib.SMX_ERR_WORKSPACE
+    assert "workspace" in str(ei.value)

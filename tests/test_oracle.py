@@ -1,0 +1,280 @@
+"""Pins the CPU oracle (oracle/moe_ref.py) with checks independent of its own formulas:
+the reference's align docstring example, brute force, library selection routines, float64
+exp/softmax, and a float64 textbook SwiGLU MoE built from separate gate/up/down matrices."""
+import itertools
+import json
+import os
+
+import numpy as np
+import pytest
+
+from oracle import moe_ref as ref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# --------------------------------------------------------------------------------- dtype helpers
+def test_bf16_rounding_known_values():
+    vals = np.array([1.0, 1.0 + 2**-8, 1.0 + 2**-7, 1.0 + 3 * 2**-8, -2.5, 65504.0, 1e-40],
+                    dtype=np.float32)
+    # 1 + 2^-8 is a tie -> even (1.0); 1 + 3*2^-8 is a tie -> even (1 + 2^-6)
+    want = np.array([1.0, 1.0, 1.0 + 2**-7, 1.0 + 2**-6, -2.5, 65536.0, 0.0], dtype=np.float32)
+    got = ref.round_to(vals, ref.BF16)
+    np.testing.assert_array_equal(got[:6], want[:6])
+    assert abs(got[6]) < 1e-39  # subnormal input rounds within the bf16 subnormal range
+
+
+def test_bf16_round_matches_float64_nearest():
+    rng = np.random.default_rng(1)
+    a = (rng.standard_normal(100000) * 10).astype(np.float32)
+    got = ref.round_to(a, ref.BF16).astype(np.float64)
+    # brute force: nearest of the two bf16 neighbours (truncate, truncate + 1 ulp)
+    u = a.view(np.uint32)
+    lo = (u & 0xFFFF0000).view(np.float32).astype(np.float64)
+    hi = ((u & 0xFFFF0000) + 0x10000).view(np.float32).astype(np.float64)
+    x = a.astype(np.float64)
+    dlo, dhi = np.abs(x - lo), np.abs(hi - x)
+    assert np.all(np.minimum(dlo, dhi) == np.abs(got - x))
+
+
+def test_f16_round():
+    a = np.array([1.0 + 2**-11, 1.0 + 3 * 2**-11, 70000.0], dtype=np.float32)
+    np.testing.assert_array_equal(ref.round_to(a, ref.F16), [1.0, 1.0 + 2**-9, np.inf])
+
+
+# ---------------------------------------------------------------------------------------- exp
+def test_exp_nonpos_ulp_error():
+    rng = np.random.default_rng(0)
+    d = np.concatenate([
+        -rng.random(2_000_000, dtype=np.float32) * np.float32(80.0),
+        -rng.random(200_000, dtype=np.float32) * np.float32(1e-3),
+        np.array([0.0, -0.0, -1e-30, -1e-7, -0.34657359, -0.34657360, -1.0, -79.999], np.float32),
+    ]).astype(np.float32)
+    got = ref.exp_nonpos(d)
+    exact = np.exp(d.astype(np.float64))
+    want = exact.astype(np.float32)
+    ulp = np.spacing(want).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - exact) / ulp
+    assert err.max() <= 2.0, err.max()
+    assert ref.exp_nonpos(np.array([0.0], np.float32))[0] == 1.0
+
+
+def test_exp_nonpos_edges():
+    d = np.array([-80.0, -80.0001, -1000.0, -np.inf, np.nan], dtype=np.float32)
+    out = ref.exp_nonpos(d)
+    assert out[0] > 0 and np.isfinite(out[0])
+    assert out[1] == 0 and out[2] == 0 and out[3] == 0
+    assert np.isnan(out[4])
+    # every nonzero result is a normal float
+    assert out[0] >= np.finfo(np.float32).tiny
+
+
+# ------------------------------------------------------------------------------------- softmax
+def test_softmax_against_float64():
+    rng = np.random.default_rng(2)
+    for E in (1, 7, 8, 60, 64, 65, 128, 200, 256):
+        x = (rng.standard_normal((33, E)) * 3).astype(np.float32)
+        p = ref.softmax_probs(x)
+        # the fp32 algorithm subtracts the row max in fp32; start float64 from those differences
+        d32 = (x - x.max(1, keepdims=True)).astype(np.float32)
+        e64 = np.exp(d32.astype(np.float64))
+        p64 = e64 / e64.sum(1, keepdims=True)
+        # exp (<= 2 ulp) + reciprocal + product + summation rounding: a few ulp
+        np.testing.assert_allclose(p, p64, rtol=1e-6, atol=1e-30)
+        np.testing.assert_allclose(p.sum(1), 1.0, rtol=2e-6)
+
+
+def test_softmax_sum_order_is_the_lane_tree():
+    # 70 experts: lanes 0..5 hold two values each. A sequential sum and the lane tree differ
+    # for these magnitudes; the oracle must follow the tree (lane sums, then halving).
+    x = np.full((1, 70), -15.0, dtype=np.float32)
+    x[0, 0] = 0.0
+    x[0, 64] = -0.5
+    ex = ref.exp_nonpos(x - x.max())
+    pad = np.zeros(256, np.float32)
+    pad[:70] = ex[0]
+    lane = pad[:64].copy()
+    for i in range(1, 4):
+        lane = lane + pad[64 * i:64 * i + 64]
+    h = 32
+    while h:
+        lane = lane[:h] + lane[h:2 * h]
+        h //= 2
+    want = ex[0] * (np.float32(1.0) / lane[0])
+    np.testing.assert_array_equal(ref.softmax_probs(x)[0], want)
+
+
+# --------------------------------------------------------------------------------------- top-k
+def _select_by_lexsort(p, k):
+    T, E = p.shape
+    ids = np.empty((T, k), np.int32)
+    for t in range(T):
+        order = np.lexsort((np.arange(E), -p[t].astype(np.float64)))
+        ids[t] = order[:k]
+    return ids
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (60, 4), (64, 6), (2, 2), (256, 8), (5, 1)])
+def test_topk_matches_lexsort_selection(E, k):
+    rng = np.random.default_rng(E * 10 + k)
+    x = (rng.standard_normal((50, E)) * 2).astype(np.float32)
+    p = ref.softmax_probs(x)
+    w, ids = ref.topk_softmax(x, k, renormalize=False)
+    np.testing.assert_array_equal(ids, _select_by_lexsort(p, k))
+    np.testing.assert_array_equal(w, np.take_along_axis(p, ids.astype(np.int64), 1))
+    assert np.all(np.diff(w, axis=1) <= 0)
+
+
+def test_topk_ties_go_to_lower_index():
+    x = np.zeros((3, 8), np.float32)
+    x[1, [2, 5, 6]] = 1.0          # three-way tie at the top
+    x[2] = [0, 3, 3, 1, 3, 0, 0, 1]
+    w, ids = ref.topk_softmax(x, 3, renormalize=False)
+    np.testing.assert_array_equal(ids[0], [0, 1, 2])
+    np.testing.assert_array_equal(ids[1], [2, 5, 6])
+    np.testing.assert_array_equal(ids[2], [1, 2, 4])
+    assert w[0, 0] == w[0, 1] == w[0, 2] == np.float32(1.0) / np.float32(8.0)
+
+
+def test_topk_renormalize_brute_force():
+    # E=8, k=2: all 56 ordered pairs of distinct experts as the top two
+    for a, b in itertools.permutations(range(8), 2):
+        x = np.full((1, 8), -1.0, np.float32)
+        x[0, a], x[0, b] = 2.0, 1.5
+        w, ids = ref.topk_softmax(x, 2, renormalize=True)
+        assert tuple(ids[0]) == (a, b)
+        r = np.exp(0.5)
+        np.testing.assert_allclose(w[0], [r / (1 + r), 1 / (1 + r)], rtol=2e-7)
+        assert abs(float(w[0].sum(dtype=np.float64)) - 1.0) <= 2 * np.finfo(np.float32).eps
+
+
+def test_topk_bf16_logits_select_like_logits():
+    # bf16-representable logits that differ are never merged by the softmax: selecting on the
+    # probabilities equals selecting on the logits (lexsort on logits, ties to lower index).
+    rng = np.random.default_rng(7)
+    x = ref.round_to((rng.standard_normal((400, 8)) * 1.3).astype(np.float32), ref.BF16)
+    _, ids = ref.topk_softmax(x, 2, renormalize=True)
+    np.testing.assert_array_equal(ids, _select_by_lexsort(x, 2))
+
+
+# --------------------------------------------------------------------------------------- align
+def test_align_docstring_example():
+    """specmoe/layers/fused_moe_kernel.py:41-54 (read with expert 0 empty, E=5)."""
+    with open(os.path.join(GOLDEN, "align_docstring_kat.json")) as f:
+        kat = json.load(f)
+    sorted_ids, expert_ids, ntp = ref.moe_align_block_size(
+        np.array(kat["topk_ids"], np.int32), kat["block_size"], kat["num_experts"])
+    np.testing.assert_array_equal(sorted_ids[:kat["num_tokens_post_pad"]], kat["sorted_token_ids"])
+    assert int(ntp[0]) == kat["num_tokens_post_pad"]
+    nb = kat["num_tokens_post_pad"] // kat["block_size"]
+    np.testing.assert_array_equal(expert_ids[:nb], kat["expert_ids"])
+    assert np.all(sorted_ids[kat["num_tokens_post_pad"]:] == len(sum(kat["topk_ids"], [])))
+
+
+def _align_brute(flat, bm, E):
+    out, eids = [], []
+    for e in range(E):
+        run = [f for f in range(len(flat)) if flat[f] == e]
+        while len(run) % bm:
+            run.append(len(flat))
+        out += run
+        eids += [e] * (len(run) // bm)
+    return out, eids
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_align_brute_force(seed):
+    rng = np.random.default_rng(seed)
+    E = int(rng.integers(1, 20))
+    k = int(rng.integers(1, min(E, 6) + 1))
+    T = int(rng.integers(0, 40))
+    bm = int(rng.choice([1, 2, 4, 16, 64]))
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]) if T else np.zeros((0, k), np.int32)
+    flat = ids.reshape(-1).tolist()
+    sorted_ids, expert_ids, ntp = ref.moe_align_block_size(ids, bm, E)
+    want, weids = _align_brute(flat, bm, E)
+    assert int(ntp[0]) == len(want)
+    np.testing.assert_array_equal(sorted_ids[:len(want)], want)
+    assert np.all(sorted_ids[len(want):] == len(flat))
+    np.testing.assert_array_equal(expert_ids[:len(weids)], weids)
+    assert np.all(expert_ids[len(weids):] == -1)
+    # invariants: bijection onto [0, N) among non-sentinel entries
+    real = sorted_ids[sorted_ids < len(flat)]
+    np.testing.assert_array_equal(np.sort(real), np.arange(len(flat)))
+
+
+# ---------------------------------------------------------------------------------- expert math
+def _textbook(x, w1s, w3s, w2s, w, ids):
+    """float64 Mixtral sparse MoE block: y = sum_j w_j * W2 (silu(W1 x) * (W3 x))."""
+    x = x.astype(np.float64)
+    y = np.zeros_like(x)
+    for t in range(x.shape[0]):
+        for j in range(ids.shape[1]):
+            e = ids[t, j]
+            g = w1s[e].astype(np.float64) @ x[t]
+            u = w3s[e].astype(np.float64) @ x[t]
+            a = g / (1 + np.exp(-g)) * u
+            y[t] += w[t, j] * (w2s[e].astype(np.float64) @ a)
+    return y
+
+
+def _make_layer(rng, T, H, I, E, k, P, dtype):
+    x = ref.round_to(rng.standard_normal((T, H)).astype(np.float32), dtype)
+    w1s = [ref.round_to((rng.standard_normal((I, H)) * 0.05).astype(np.float32), dtype) for _ in range(E)]
+    w3s = [ref.round_to((rng.standard_normal((I, H)) * 0.05).astype(np.float32), dtype) for _ in range(E)]
+    w2s = [ref.round_to((rng.standard_normal((H, I)) * 0.05).astype(np.float32), dtype) for _ in range(E)]
+    slots = rng.permutation(P)[:E]
+    pool = np.zeros((P, 3 * I * H), np.float32)
+    for e in range(E):
+        pool[slots[e]] = ref.pack_page(w1s[e], w3s[e], w2s[e])
+    logits = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    return x, w1s, w3s, w2s, slots, pool, logits
+
+
+@pytest.mark.parametrize("dtype,rtol", [(ref.F32, 2e-5), (ref.BF16, 3e-2), (ref.F16, 4e-3)])
+def test_expert_math_against_textbook(dtype, rtol):
+    rng = np.random.default_rng(11)
+    T, H, I, E, k = 9, 64, 96, 5, 2
+    x, w1s, w3s, w2s, slots, pool, logits = _make_layer(rng, T, H, I, E, k, 8, dtype)
+    y, w, ids = ref.fused_moe_forward(x, logits, pool, slots, k, True, dtype)
+    want = _textbook(x, w1s, w3s, w2s, w, ids)
+    err = np.abs(y - want).max() / np.abs(want).max()
+    assert err < rtol, err
+
+
+def test_expert_math_detects_swapped_gate_up():
+    rng = np.random.default_rng(12)
+    T, H, I, E, k = 6, 32, 64, 3, 2
+    x, w1s, w3s, w2s, slots, pool, logits = _make_layer(rng, T, H, I, E, k, 3, ref.F32)
+    y, w, ids = ref.fused_moe_forward(x, logits, pool, slots, k, True, ref.F32)
+    swapped = _textbook(x, w3s, w1s, w2s, w, ids)
+    assert np.abs(y - swapped).max() / np.abs(swapped).max() > 0.05
+
+
+def test_single_expert_is_dense_swiglu():
+    rng = np.random.default_rng(13)
+    T, H, I = 4, 32, 64
+    x, w1s, w3s, w2s, slots, pool, _ = _make_layer(rng, T, H, I, 1, 1, 1, ref.F32)
+    y = ref.stack_fused_moe(x, pool, slots, np.ones((T, 1), np.float32),
+                            np.zeros((T, 1), np.int32), ref.F32)
+    g, u = x @ w1s[0].T, x @ w3s[0].T
+    np.testing.assert_allclose(y, (g / (1 + np.exp(-g)) * u) @ w2s[0].T, rtol=1e-5, atol=1e-6)
+
+
+def test_invalid_ids_and_slots_contribute_nothing():
+    rng = np.random.default_rng(14)
+    T, H, I, E, k = 4, 32, 64, 3, 2
+    x, w1s, w3s, w2s, slots, pool, logits = _make_layer(rng, T, H, I, E, k, 4, ref.F32)
+    w, ids = ref.topk_softmax(logits, k, True)
+    base = ref.stack_fused_moe(x, pool, slots, w, ids, ref.F32)
+    ids2 = ids.copy()
+    ids2[:, 1] = 99
+    y2 = ref.stack_fused_moe(x, pool, slots, w, ids2, ref.F32)
+    w0 = w.copy()
+    w0[:, 1] = 0
+    y0 = ref.stack_fused_moe(x, pool, slots, w0, ids, ref.F32)
+    assert np.abs(y2 - y0).max() <= 1e-5 * np.abs(y0).max()  # BLAS order differs with batch
+    bad = slots.copy()
+    bad[ids[0, 0]] = 1000
+    y3 = ref.stack_fused_moe(x, pool, bad, w, ids, ref.F32)
+    assert not np.allclose(y3, base)
