@@ -60,6 +60,12 @@ def lib() -> ctypes.CDLL:
                 raise ImportError(
                     f"{LIB_PATH} is missing: build it with `python -m ae_amd.build` "
                     "(the MoE path has no fallback implementation)")
+            # PyTorch-ROCm wheels ship their own HIP runtime (libamdhip64.so, SONAME
+            # libamdhip64.so.7). Importing torch first maps it, so this library's
+            # DT_NEEDED libamdhip64.so.7 binds to that same runtime. Loaded the other way
+            # round, torch would map a second runtime and kernels launched here could not
+            # see torch's device context.
+            import torch  # noqa: F401
             handle = ctypes.CDLL(LIB_PATH)
             for name, restype, argtypes in SIGNATURES:
                 fn = getattr(handle, name)

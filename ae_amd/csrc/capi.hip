@@ -36,7 +36,7 @@ struct Plan {
   int tok_tiles = 1;
   int splits = 1;
   int split_steps = 0;
-  size_t hdr = 0, act_expert = 0, act_off = 0, act_cnt = 0, sorted_f = 0, w = 0, ids = 0;
+  size_t hdr = 0, act_expert = 0, act_off = 0, act_cnt = 0, act_slot = 0, sorted_f = 0, w = 0, ids = 0;
   size_t act = 0, part = 0, total = 0;
 };
 
@@ -75,6 +75,7 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype)
   p.act_expert = o; o = align_up(o + sizeof(int32_t) * E);
   p.act_off = o;    o = align_up(o + sizeof(int32_t) * E);
   p.act_cnt = o;    o = align_up(o + sizeof(int32_t) * E);
+  p.act_slot = o;   o = align_up(o + sizeof(int64_t) * E);
   p.sorted_f = o;   o = align_up(o + sizeof(int32_t) * p.N);
   p.w = o;          o = align_up(o + sizeof(float) * p.N);
   p.ids = o;        o = align_up(o + sizeof(int32_t) * p.N);
@@ -92,6 +93,7 @@ RouteBuffers carve(const Plan& p, void* ws) {
   rb.act_off = reinterpret_cast<int32_t*>(b + p.act_off);
   rb.act_cnt = reinterpret_cast<int32_t*>(b + p.act_cnt);
   rb.sorted_f = reinterpret_cast<int32_t*>(b + p.sorted_f);
+  rb.act_slot = reinterpret_cast<int64_t*>(b + p.act_slot);
   return rb;
 }
 
@@ -197,13 +199,13 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
                         const int64_t* expert_to_slot, int64_t E,
                         const float* topk_weights, const int32_t* topk_ids, int64_t top_k,
                         void* workspace, size_t workspace_bytes, void* stream) {
-  if (H <= 0) return SMX_ERR_INVALID_ARG;
+  if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype)) return SMX_ERR_INVALID_ARG;
+  if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
   int64_t I = 0;
   int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, &I);
   if (rc != SMX_OK) return rc;
   rc = check_shape(T, H, I, E, top_k, dtype);
   if (rc != SMX_OK) return rc;
-  if (T == 0) return SMX_OK;
   if (!topk_weights || !topk_ids || !workspace) return SMX_ERR_INVALID_ARG;
   const Plan p = make_plan(T, H, I, E, top_k, dtype);
   if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
@@ -224,13 +226,15 @@ int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, i
                           const int64_t* expert_to_slot, float* topk_weights_out,
                           int32_t* topk_ids_out, void* workspace, size_t workspace_bytes,
                           void* stream) {
-  if (H <= 0 || !valid_dtype(logits_dtype)) return SMX_ERR_INVALID_ARG;
+  if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype) ||
+      !valid_dtype(logits_dtype))
+    return SMX_ERR_INVALID_ARG;
+  if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
   int64_t I = 0;
   int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, &I);
   if (rc != SMX_OK) return rc;
   rc = check_shape(T, H, I, E, top_k, dtype);
   if (rc != SMX_OK) return rc;
-  if (T == 0) return SMX_OK;
   if (!router_logits || !workspace) return SMX_ERR_INVALID_ARG;
   const Plan p = make_plan(T, H, I, E, top_k, dtype);
   if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;

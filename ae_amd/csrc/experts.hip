@@ -24,69 +24,90 @@ namespace smx {
 // MFMA output layout (16x16 f32 accumulator): lane l, register i holds row 4*(l/16)+i of the
 // A operand's 16 rows and column l%16 of the B operand's 16 columns. Operand fragments:
 // lane l holds 16 contiguous bytes of A row l%16 (resp. B column l%16) at K group l/16.
+//
+// Weight loads do not use the fragment layout directly (16 rows x 64 bytes per instruction
+// streams from HBM ~15% slower than wider row segments). Each 16-row tile is loaded in
+// chunks of 256 bytes per row by four instructions of 4 rows x 256 bytes (lane l: row
+// 4i + l/16, bytes 16*(l%16)), written to a wave-private LDS tile, and read back as
+// fragments. The LDS tile is 16 rows x 16 slots of 16 bytes with slot = chunk16 ^ row, so both
+// the row-wise writes and the column-wise fragment reads touch 16 distinct slots per 16
+// lanes (no bank conflicts). One wave's LDS operations execute in order, so a wave reads
+// back its own writes and overwrites a tile only after reading it: no barriers.
 
-template <int DT, int R, int MT>
-struct Chunk {
-  u32x4 a[kUnroll][R];
+constexpr int kTileSlots = kRowTile * 16;  // 16-byte slots per LDS tile (4 KB)
+
+template <int R>
+struct Raw {
+  u32x4 v[4][R];  // [instruction][tile]
 };
 
-template <int DT, int R, int MT>
-__device__ __forceinline__ void load_a(Chunk<DT, R, MT>& c, const char* const (&a)[R], int step0) {
+// Issue the four 4-row x 256-byte loads of one chunk for every tile. base[r] already holds
+// this lane's row (l/16) and byte column (16*(l%16)); instruction i adds 4*i rows.
+template <int R>
+__device__ __forceinline__ void load_raw(Raw<R>& c, const char* const (&base)[R],
+                                         int64_t row4_bytes, int chunk) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u)
+  for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      c.a[u][r] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(a[r] + static_cast<int64_t>(step0 + u) * kStepBytes));
+      c.v[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          base[r] + i * row4_bytes + static_cast<int64_t>(chunk) * (kStepBytes * kUnroll)));
 }
 
-// One chunk: load this chunk's token fragments, optionally issue the next chunk's weight
-// loads, then the MFMAs. Nothing here is conditional on the token count, so the compiler's
-// wait-count pass sees one straight-line path: the MFMAs wait for this chunk's operands only,
-// never for the prefetch (loads retire in issue order, and the prefetch is issued last).
-// Token tiles past the expert's count load a clamped valid row; their columns are dropped
-// by the epilogue.
+__device__ __forceinline__ int swz(int row, int c16) { return row * 16 + ((c16 ^ row) & 15); }
+
 template <int DT, int R, int MT, bool kPrefetch>
-__device__ __forceinline__ void mma_chunk(const Chunk<DT, R, MT>& c, Chunk<DT, R, MT>& next,
-                                          const char* const (&a)[R], const char* const (&b)[MT],
-                                          int step0, f32x4 (&acc)[R][MT]) {
+__device__ __forceinline__ void mma_chunk(const Raw<R>& c, Raw<R>& next, u32x4* lds,
+                                          const char* const (&a)[R], int64_t row4_bytes,
+                                          const char* const (&b)[MT], int chunk,
+                                          f32x4 (&acc)[R][MT]) {
+  const int lane = lane_id();
   u32x4 bf[kUnroll][MT];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      bf[u][mt] = *reinterpret_cast<const u32x4*>(b[mt] + static_cast<int64_t>(step0 + u) * kStepBytes);
-  if constexpr (kPrefetch) load_a(next, a, step0 + kUnroll);
+      bf[u][mt] = *reinterpret_cast<const u32x4*>(
+          b[mt] + static_cast<int64_t>(chunk * kUnroll + u) * kStepBytes);
+  if constexpr (kPrefetch) load_raw(next, a, row4_bytes, chunk + 1);
   // Keep the scheduler from sinking loads into the MFMA sequence (which would shrink the
-  // prefetch distance to a few loads).
+  // prefetch distance) or from waiting on the prefetch early.
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u)
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < R; ++r) lds[r * kTileSlots + swz(4 * i + (lane >> 4), lane & 15)] = c.v[i][r];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    u32x4 af[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) af[r] = lds[r * kTileSlots + swz(lane & 15, 4 * u + (lane >> 4))];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r][mt] = Elem<DT>::mfma(c.a[u][r], bf[u][mt], acc[r][mt]);
+      for (int r = 0; r < R; ++r) acc[r][mt] = Elem<DT>::mfma(af[r], bf[u][mt], acc[r][mt]);
+  }
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// acc[r][mt] += A_r (16 rows x nsteps*64 bytes) . B_mt (16 columns), double-buffered over
-// chunks of kUnroll load steps. nsteps must be a positive multiple of kUnroll.
+// acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt (16 columns), with the next chunk's
+// weight loads in flight while the current chunk is transposed and multiplied.
 template <int DT, int R, int MT>
-__device__ __forceinline__ void stream_mfma(const char* const (&a)[R], const char* const (&b)[MT],
-                                            int nsteps, f32x4 (&acc)[R][MT]) {
-  const int nchunks = nsteps / kUnroll;
-  Chunk<DT, R, MT> c0, c1;
-  load_a(c0, a, 0);
+__device__ __forceinline__ void stream_mfma(const char* const (&a)[R], int64_t row4_bytes,
+                                            const char* const (&b)[MT], int nchunks,
+                                            u32x4* lds, f32x4 (&acc)[R][MT]) {
+  Raw<R> c0, c1;
+  load_raw(c0, a, row4_bytes, 0);
   int c = 0;
   for (; c + 2 < nchunks; c += 2) {
-    mma_chunk<DT, R, MT, true>(c0, c1, a, b, c * kUnroll, acc);
-    mma_chunk<DT, R, MT, true>(c1, c0, a, b, (c + 1) * kUnroll, acc);
+    mma_chunk<DT, R, MT, true>(c0, c1, lds, a, row4_bytes, b, c, acc);
+    mma_chunk<DT, R, MT, true>(c1, c0, lds, a, row4_bytes, b, c + 1, acc);
   }
   if (c + 1 < nchunks) {
-    mma_chunk<DT, R, MT, true>(c0, c1, a, b, c * kUnroll, acc);
-    mma_chunk<DT, R, MT, false>(c1, c0, a, b, (c + 1) * kUnroll, acc);
+    mma_chunk<DT, R, MT, true>(c0, c1, lds, a, row4_bytes, b, c, acc);
+    mma_chunk<DT, R, MT, false>(c1, c0, lds, a, row4_bytes, b, c + 1, acc);
   } else {
-    mma_chunk<DT, R, MT, false>(c0, c1, a, b, c * kUnroll, acc);
+    mma_chunk<DT, R, MT, false>(c0, c1, lds, a, row4_bytes, b, c, acc);
   }
 }
 
@@ -120,17 +141,24 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   const int gw = uniform(blockIdx.x * kExpertWaves + threadIdx.x / kWave);
   const int ai = gw / tiles;
   const int p = gw - ai * tiles;
-  if (ai >= uniform(a.rb.hdr[0])) return;
-  const int e = uniform(a.rb.act_expert[ai]);
+  // ai < max_active <= E, so the per-expert arrays may be read before the active count is
+  // known (the four loads then share one latency); values past the active count are unused.
+  const int active = uniform(a.rb.hdr[0]);
   const int off = uniform(a.rb.act_off[ai]);
   const int m = uniform(a.rb.act_cnt[ai]);
-  const int64_t slot = a.e2s[e];
+  const int64_t slot = a.rb.act_slot[ai];
+  if (ai >= active) return;
   const int H = a.H, I = a.I;
   const S* page = static_cast<const S*>(a.pool) + slot * a.page_elems;
+  const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
+  // coalesced-load lane origin: row lane/16 of the tile, byte column 16*(lane%16)
+  const int64_t lane_origin = (lane >> 4) * row_bytes + (lane & 15) * 16;
   const char* arow[2] = {
-      reinterpret_cast<const char*>(page + static_cast<int64_t>(kRowTile * p + r) * H) + g * 16,
-      reinterpret_cast<const char*>(page + static_cast<int64_t>(I + kRowTile * p + r) * H) + g * 16};
-  const int nsteps = H * static_cast<int>(sizeof(S)) / kStepBytes;
+      reinterpret_cast<const char*>(page + static_cast<int64_t>(kRowTile * p) * H) + lane_origin,
+      reinterpret_cast<const char*>(page + static_cast<int64_t>(I + kRowTile * p) * H) + lane_origin};
+  const int nchunks = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
+  __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
+  u32x4* lds = lds_all[threadIdx.x / kWave];
   const S* x = static_cast<const S*>(a.x);
   S* act = static_cast<S*>(a.act);
 
@@ -147,7 +175,7 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_mfma<DT, 2, MT>(arow, brow, nsteps, acc);
+    stream_mfma<DT, 2, MT>(arow, 4 * row_bytes, brow, nchunks, lds, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -178,19 +206,23 @@ __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
   const int rem = gw - ai * per_expert;
   const int sp = rem / rtiles;
   const int rt = rem - sp * rtiles;
-  if (ai >= uniform(a.rb.hdr[0])) return;
-  const int e = uniform(a.rb.act_expert[ai]);
+  const int active = uniform(a.rb.hdr[0]);
   const int off = uniform(a.rb.act_off[ai]);
   const int m = uniform(a.rb.act_cnt[ai]);
-  const int64_t slot = a.e2s[e];
+  const int64_t slot = a.rb.act_slot[ai];
+  if (ai >= active) return;
   const int H = a.H, I = a.I;
   const int N = a.T * a.k;
   const S* w2 = static_cast<const S*>(a.pool) + slot * a.page_elems + static_cast<int64_t>(2) * I * H;
   const int k0 = sp * a.split_steps * kStepBytes / static_cast<int>(sizeof(S));  // element offset
+  const int64_t row_bytes = static_cast<int64_t>(I) * sizeof(S);
+  const int64_t lane_origin = (lane >> 4) * row_bytes + (lane & 15) * 16;
   const char* arow[R];
 #pragma unroll
   for (int i = 0; i < R; ++i)
-    arow[i] = reinterpret_cast<const char*>(w2 + static_cast<int64_t>((rt * R + i) * kRowTile + r) * I + k0) + g * 16;
+    arow[i] = reinterpret_cast<const char*>(w2 + static_cast<int64_t>((rt * R + i) * kRowTile) * I + k0) + lane_origin;
+  __shared__ u32x4 lds_all[kExpertWaves][R * kTileSlots];
+  u32x4* lds = lds_all[threadIdx.x / kWave];
   const S* act = static_cast<const S*>(a.act);
 
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
@@ -205,7 +237,7 @@ __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_mfma<DT, R, MT>(arow, brow, a.split_steps, acc);
+    stream_mfma<DT, R, MT>(arow, 4 * row_bytes, brow, a.split_steps / kUnroll, lds, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;

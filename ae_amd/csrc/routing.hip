@@ -19,18 +19,23 @@ namespace smx {
 // Semantics follow select_experts as called at specmoe/layers/FusedMoE.py:174-185.
 // ---------------------------------------------------------------------------------------
 template <int LDT>
-__device__ __forceinline__ void wave_topk_softmax(const void* logits, int64_t row, int E, int k,
-                                                  bool renorm, float& w_out, int& id_out) {
-#pragma clang fp contract(off)
+__device__ __forceinline__ void load_logits(const void* logits, int64_t row, int E,
+                                            float (&v)[kMaxExpertsPerLane]) {
   const int lane = lane_id();
-  float p[kMaxExpertsPerLane];
-  float m = -__builtin_inff();
 #pragma unroll
   for (int i = 0; i < kMaxExpertsPerLane; ++i) {
     const int e = lane + kWave * i;
-    p[i] = (e < E) ? load_as_f32<LDT>(logits, row * E + e) : -__builtin_inff();
-    m = fmaxf(m, p[i]);
+    v[i] = (e < E) ? load_as_f32<LDT>(logits, row * E + e) : -__builtin_inff();
   }
+}
+
+__device__ __forceinline__ void wave_topk_softmax(float (&p)[kMaxExpertsPerLane], int E, int k,
+                                                  bool renorm, float& w_out, int& id_out) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < kMaxExpertsPerLane; ++i) m = fmaxf(m, p[i]);
   m = wave_max(m);
   float s = 0.0f;
 #pragma unroll
@@ -78,21 +83,45 @@ __device__ __forceinline__ void wave_topk_softmax(const void* logits, int64_t ro
   }
 }
 
+// Tokens t = first, first + stride, ... (up to kTokBatch of them) handled by one wave: all
+// logit loads are issued before any token is processed, so a wave pays one load latency per
+// batch rather than one per token. fn(t, w, id) receives each token's result on every lane.
+template <int LDT, typename Fn>
+__device__ __forceinline__ void wave_topk_batch(const void* logits, int T, int E, int k,
+                                                bool renorm, int first, int stride, Fn&& fn) {
+  float v[kTokBatch][kMaxExpertsPerLane];
+#pragma unroll
+  for (int b = 0; b < kTokBatch; ++b) {
+    const int t = first + b * stride;
+    if (t < T) load_logits<LDT>(logits, t, E, v[b]);
+  }
+#pragma unroll
+  for (int b = 0; b < kTokBatch; ++b) {
+    const int t = first + b * stride;
+    if (t < T) {
+      float w;
+      int id;
+      wave_topk_softmax(v[b], E, k, renorm, w, id);
+      fn(t, w, id);
+    }
+  }
+}
+
 template <int LDT>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restrict__ logits,
                                                            int T, int E, int k, int renorm,
                                                            float* __restrict__ w,
                                                            int32_t* __restrict__ ids) {
   const int waves = blockDim.x / kWave;
-  for (int t = blockIdx.x * waves + threadIdx.x / kWave; t < T; t += gridDim.x * waves) {
-    float wv;
-    int id;
-    wave_topk_softmax<LDT>(logits, t, E, k, renorm != 0, wv, id);
-    const int lane = lane_id();
-    if (lane < k) {
-      w[(int64_t)t * k + lane] = wv;
-      ids[(int64_t)t * k + lane] = id;
-    }
+  const int stride = gridDim.x * waves;
+  const int lane = lane_id();
+  for (int t0 = blockIdx.x * waves + threadIdx.x / kWave; t0 < T; t0 += stride * kTokBatch) {
+    wave_topk_batch<LDT>(logits, T, E, k, renorm != 0, t0, stride, [&](int t, float wv, int id) {
+      if (lane < k) {
+        w[(int64_t)t * k + lane] = wv;
+        ids[(int64_t)t * k + lane] = id;
+      }
+    });
   }
 }
 
@@ -270,45 +299,46 @@ template <int LDT>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(
     const void* __restrict__ logits, int T, int E, int k, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ ids_out, const int32_t* __restrict__ ids_in,
-    const int64_t* __restrict__ e2s, int64_t num_slots, AlignOutputs out) {
+    const int64_t* __restrict__ e2s, int64_t num_slots, AlignOutputs out, int64_t* act_slot) {
   __shared__ AlignShared sh;
+  __shared__ int64_t slot_of[kMaxExperts];
+  __shared__ int bad;
   const int N = T * k;
   const int wave = threadIdx.x / kWave;
   const int lane = lane_id();
-  __shared__ int bad;
   if (threadIdx.x == 0) bad = 0;
-  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    const int64_t slot = e2s[e];
+    slot_of[e] = (slot >= 0 && slot < num_slots) ? slot : -1;
+  }
   if (logits != nullptr) {
-    for (int t = wave; t < T; t += kRouteWaves) {
-      float wv;
-      int id;
-      wave_topk_softmax<LDT>(logits, t, E, k, renorm != 0, wv, id);
-      if (lane < k) {
-        const int f = t * k + lane;
-        if (w_out) w_out[f] = wv;
-        if (ids_out) ids_out[f] = id;
-        sh.ids[f] = static_cast<int16_t>(id);
-      }
+    for (int t0 = wave; t0 < T; t0 += kRouteWaves * kTokBatch) {
+      wave_topk_batch<LDT>(logits, T, E, k, renorm != 0, t0, kRouteWaves, [&](int t, float wv, int id) {
+        if (lane < k) {
+          const int f = t * k + lane;
+          if (w_out) w_out[f] = wv;
+          if (ids_out) ids_out[f] = id;
+          sh.ids[f] = static_cast<int16_t>(id);
+        }
+      });
     }
   } else {
     for (int f = threadIdx.x; f < N; f += blockDim.x) {
       const int e = ids_in[f];
-      const bool ok = e >= 0 && e < E;
-      if (!ok) bad = 1;
-      sh.ids[f] = static_cast<int16_t>(ok ? e : -1);
+      sh.ids[f] = static_cast<int16_t>((e >= 0 && e < E) ? e : -2);  // -2: out of range
     }
   }
-  __syncthreads();
+  __syncthreads();  // also orders thread 0's `bad = 0` before any `bad = 1`
   for (int f = threadIdx.x; f < N; f += blockDim.x) {
     const int e = sh.ids[f];
-    if (e >= 0) {
-      const int64_t slot = e2s[e];
-      if (slot < 0 || slot >= num_slots) { sh.ids[f] = -1; bad = 1; }
-    }
+    if (e == -2 || (e >= 0 && slot_of[e] < 0)) { sh.ids[f] = -1; bad = 1; }
   }
   __syncthreads();
   if (threadIdx.x == 0) out.hdr[1] = bad;
   align_block(sh, N, E, out);
+  // pool slot of each active expert, so the expert kernels need one dependent load, not two
+  for (int e = threadIdx.x; e < E; e += blockDim.x)
+    if (sh.cnt[e] > 0) act_slot[sh.act[e]] = slot_of[e];
 }
 
 // ---------------------------------------------------------------------------------------
@@ -350,9 +380,9 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
   out.sorted_f = rb.sorted_f;
   out.bm = 1;
   switch (ldt) {
-    case kF32: route_kernel<kF32><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
-    case kF16: route_kernel<kF16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
-    default: route_kernel<kBF16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    case kF32: route_kernel<kF32><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, rb.act_slot); break;
+    case kF16: route_kernel<kF16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, rb.act_slot); break;
+    default: route_kernel<kBF16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, rb.act_slot); break;
   }
   return hipGetLastError();
 }

@@ -12,6 +12,7 @@ constexpr int kMaxExperts = 256;
 constexpr int kMaxExpertsPerLane = kMaxExperts / kWave;
 constexpr int kMaxAssignments = 16384;  // T * top_k
 constexpr int kMaxTopK = 16;
+constexpr int kTokBatch = 4;            // tokens whose logits a wave loads before computing
 
 // Expert-kernel geometry.
 constexpr int kExpertThreads = 256;                 // 4 independent waves per workgroup
@@ -19,9 +20,12 @@ constexpr int kExpertWaves = kExpertThreads / kWave;
 constexpr int kRowTile = 16;                        // weight rows per MFMA tile
 constexpr int kTokTile = 16;                        // token columns per MFMA tile
 constexpr int kStepBytes = 64;                      // row bytes one 16-byte/lane load step covers
-constexpr int kUnroll = 4;                          // load steps per pipelined chunk
+constexpr int kUnroll = 4;                          // load steps per chunk (256 bytes per row)
 constexpr int kDownRows = 2;                        // row tiles per wave in the down projection
 constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 tokens)
+
+static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
+              "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");
 
 struct RouteBuffers {
   int32_t* hdr;         // [0] active experts, [1] dropped-assignment flag
@@ -29,6 +33,7 @@ struct RouteBuffers {
   int32_t* act_off;     // [E] first sorted position of each active expert
   int32_t* act_cnt;     // [E] assignments routed to each active expert
   int32_t* sorted_f;    // [T*k] flat assignment index f = t*k + j at each sorted position
+  int64_t* act_slot;    // [E] pool slot of each active expert
 };
 
 struct ExpertArgs {

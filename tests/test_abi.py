@@ -34,6 +34,19 @@ def test_exports_every_declared_symbol():
         assert hasattr(L, n), n
 
 
+def test_one_hip_runtime_when_loaded_before_torch():
+    """Loading the library first must not leave two HIP runtimes mapped in the process."""
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("import sys; sys.path.insert(0, %r); from ae_amd import _lib; _lib.lib(); import torch; "
+            "maps = open('/proc/self/maps').read().splitlines(); "
+            "print(len({l.split()[-1] for l in maps if 'libamdhip64' in l}))" % root)
+    out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.strip() == "1", out.stdout
+
+
 def test_version_and_error_strings():
     assert L.smx_version() == 10000
     for code, word in [(0, b"success"), (1000, b"invalid"), (1001, b"supported"),
@@ -73,6 +86,7 @@ def test_stack_rejects_before_launch():
     assert _stack(ws=VP(0x10004)) == _lib.SMX_ERR_MISALIGNED
     assert _stack(H=100, page=3 * 100 * 256) == _lib.SMX_ERR_UNSUPPORTED
     assert _stack(T=0) == _lib.SMX_OK                              # empty: nothing launched
+    assert _stack(T=0, hidden=VP(0), out=VP(0), ws=VP(0)) == _lib.SMX_OK  # null data is fine
     assert _stack(T=-1) == _lib.SMX_ERR_INVALID_ARG
 
 
