@@ -12,7 +12,7 @@ using namespace smx;
 
 constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
 constexpr size_t kAlign = 256;
-constexpr int64_t kTargetDownWaves = 8192;  // enough waves to cover 256 CUs several times
+constexpr int64_t kTargetDownWaves = 4096;  // down-projection waves to aim for (splits = this / units)
 
 // Optional measurement events (smx_set_profile_events): recorded on the launch stream
 // before routing and after each of the four kernels.
@@ -51,6 +51,8 @@ int check_shape(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype
   if ((H * eb) % chunk != 0 || (I * eb) % chunk != 0) return SMX_ERR_UNSUPPORTED;
   if (H % (kRowTile * kDownRows) != 0 || I % kRowTile != 0) return SMX_ERR_UNSUPPORTED;
   if (H > (1 << 20) || I > (1 << 20)) return SMX_ERR_UNSUPPORTED;
+  // per-lane token/activation offsets are 32-bit
+  if (T * H * eb >= (int64_t{1} << 31) || T * k * I * eb >= (int64_t{1} << 31)) return SMX_ERR_UNSUPPORTED;
   return SMX_OK;
 }
 
@@ -146,6 +148,7 @@ int check_pool(const void* hidden, const void* out, const void* pool, int64_t nu
   if (!hidden || !out || !pool || !e2s || num_slots <= 0 || page_elems <= 0) return SMX_ERR_INVALID_ARG;
   if (page_elems % (3 * H) != 0) return SMX_ERR_INVALID_ARG;
   *I = page_elems / (3 * H);
+  if (page_elems > (int64_t{1} << 30)) return SMX_ERR_UNSUPPORTED;  // page bytes < 2^32 (32-bit offsets)
   if (!aligned16(hidden) || !aligned16(out) || !aligned16(pool)) return SMX_ERR_MISALIGNED;
   return SMX_OK;
 }

@@ -29,59 +29,85 @@ namespace smx {
 // streams from HBM ~15% slower than wider row segments). Each 16-row tile is loaded in
 // chunks of 256 bytes per row by four instructions of 4 rows x 256 bytes (lane l: row
 // 4i + l/16, bytes 16*(l%16)), written to a wave-private LDS tile, and read back as
-// fragments. The LDS tile is 16 rows x 16 slots of 16 bytes with slot = chunk16 ^ row, so both
-// the row-wise writes and the column-wise fragment reads touch 16 distinct slots per 16
-// lanes (no bank conflicts). One wave's LDS operations execute in order, so a wave reads
+// fragments. The LDS tile stores row r's 16-byte slot c at slot 17*r + c: the row pitch of
+// 17 slots puts the 16 slots a 16-lane group touches, row-wise on write and column-wise on
+// read, in 16 distinct bank groups (no conflicts), and keeps every address a per-lane base
+// plus a compile-time offset. One wave's LDS operations execute in order, so a wave reads
 // back its own writes and overwrites a tile only after reading it: no barriers.
+//
+// Loads are buffer loads: a scalar resource (base, size) plus a 32-bit per-lane offset and a
+// wave-uniform scalar offset (tile, instruction and chunk), which keeps the per-lane address
+// state to one VGPR per stream.
 
-constexpr int kTileSlots = kRowTile * 16;  // 16-byte slots per LDS tile (4 KB)
+constexpr int kPitch = 17;                        // LDS row pitch in 16-byte slots
+constexpr int kTileSlots = kRowTile * kPitch;     // slots per LDS tile (4352 bytes)
+constexpr int kBufDword3 = 0x00020000;            // gfx9 raw-buffer resource word 3
+constexpr int kNonTemporal = 2;                   // cache-policy bit: streaming (read once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufDword3);
+}
 
 template <int R>
 struct Raw {
   u32x4 v[4][R];  // [instruction][tile]
 };
 
-// Issue the four 4-row x 256-byte loads of one chunk for every tile. base[r] already holds
-// this lane's row (l/16) and byte column (16*(l%16)); instruction i adds 4*i rows.
+struct WeightStream {
+  __amdgpu_buffer_rsrc_t rsrc;  // the expert's page
+  uint32_t base;                // byte offset of tile 0's first row at chunk 0
+  uint32_t tile_stride;         // bytes between consecutive tiles
+  uint32_t row4;                // bytes of 4 rows
+  uint32_t lane_off;            // per lane: row l/16, byte column 16*(l%16)
+};
+
 template <int R>
-__device__ __forceinline__ void load_raw(Raw<R>& c, const char* const (&base)[R],
-                                         int64_t row4_bytes, int chunk) {
+__device__ __forceinline__ void load_raw(Raw<R>& c, const WeightStream& w, int chunk) {
+  const uint32_t cbase = w.base + static_cast<uint32_t>(chunk) * (kStepBytes * kUnroll);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int r = 0; r < R; ++r)
-      c.v[i][r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-          base[r] + i * row4_bytes + static_cast<int64_t>(chunk) * (kStepBytes * kUnroll)));
+      c.v[i][r] = __builtin_amdgcn_raw_buffer_load_b128(
+          w.rsrc, w.lane_off, cbase + r * w.tile_stride + i * w.row4, kNonTemporal);
 }
 
-__device__ __forceinline__ int swz(int row, int c16) { return row * 16 + ((c16 ^ row) & 15); }
+// Token operand: column c of token tile mt is a row of a row-major matrix; lane l reads its
+// 16 bytes at K group l/16.
+template <int MT>
+struct TokenStream {
+  __amdgpu_buffer_rsrc_t rsrc;
+  uint32_t base;     // byte offset of the K range (wave-uniform)
+  uint32_t off[MT];  // per lane: row offset + 16*(l/16)
+};
 
 template <int DT, int R, int MT, bool kPrefetch>
 __device__ __forceinline__ void mma_chunk(const Raw<R>& c, Raw<R>& next, u32x4* lds,
-                                          const char* const (&a)[R], int64_t row4_bytes,
-                                          const char* const (&b)[MT], int chunk,
-                                          f32x4 (&acc)[R][MT]) {
+                                          const WeightStream& w, const TokenStream<MT>& b,
+                                          int chunk, int next_chunk, f32x4 (&acc)[R][MT]) {
   const int lane = lane_id();
+  const uint32_t bbase = b.base + static_cast<uint32_t>(chunk) * (kStepBytes * kUnroll);
   u32x4 bf[kUnroll][MT];
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      bf[u][mt] = *reinterpret_cast<const u32x4*>(
-          b[mt] + static_cast<int64_t>(chunk * kUnroll + u) * kStepBytes);
-  if constexpr (kPrefetch) load_raw(next, a, row4_bytes, chunk + 1);
+      bf[u][mt] = __builtin_amdgcn_raw_buffer_load_b128(b.rsrc, b.off[mt], bbase + u * kStepBytes, 0);
+  if constexpr (kPrefetch) load_raw(next, w, next_chunk);
   // Keep the scheduler from sinking loads into the MFMA sequence (which would shrink the
   // prefetch distance) or from waiting on the prefetch early.
   __builtin_amdgcn_sched_barrier(0);
+  u32x4* wr = lds + kPitch * (lane >> 4) + (lane & 15);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int r = 0; r < R; ++r) lds[r * kTileSlots + swz(4 * i + (lane >> 4), lane & 15)] = c.v[i][r];
+    for (int r = 0; r < R; ++r) wr[r * kTileSlots + 4 * kPitch * i] = c.v[i][r];
+  const u32x4* rd = lds + kPitch * (lane & 15) + (lane >> 4);
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     u32x4 af[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) af[r] = lds[r * kTileSlots + swz(lane & 15, 4 * u + (lane >> 4))];
+    for (int r = 0; r < R; ++r) af[r] = rd[r * kTileSlots + 4 * u];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -90,24 +116,61 @@ __device__ __forceinline__ void mma_chunk(const Raw<R>& c, Raw<R>& next, u32x4* 
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt (16 columns), with the next chunk's
-// weight loads in flight while the current chunk is transposed and multiplied.
-template <int DT, int R, int MT>
-__device__ __forceinline__ void stream_mfma(const char* const (&a)[R], int64_t row4_bytes,
-                                            const char* const (&b)[MT], int nchunks,
-                                            u32x4* lds, f32x4 (&acc)[R][MT]) {
-  Raw<R> c0, c1;
-  load_raw(c0, a, row4_bytes, 0);
-  int c = 0;
-  for (; c + 2 < nchunks; c += 2) {
-    mma_chunk<DT, R, MT, true>(c0, c1, lds, a, row4_bytes, b, c, acc);
-    mma_chunk<DT, R, MT, true>(c1, c0, lds, a, row4_bytes, b, c + 1, acc);
-  }
-  if (c + 1 < nchunks) {
-    mma_chunk<DT, R, MT, true>(c0, c1, lds, a, row4_bytes, b, c, acc);
-    mma_chunk<DT, R, MT, false>(c1, c0, lds, a, row4_bytes, b, c + 1, acc);
+// acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt (16 columns). Weight chunks are
+// loaded kDepth chunks ahead of the one being transposed and multiplied (a ring of kDepth+1
+// register buffers), so each wave keeps kDepth chunks of weights in flight.
+template <int DT, int R, int MT, int kDepth>
+__device__ __forceinline__ void stream_mfma(const WeightStream& w, const TokenStream<MT>& b,
+                                            int nchunks, u32x4* lds, f32x4 (&acc)[R][MT]) {
+  static_assert(kDepth == 1 || kDepth == 2, "prefetch depth 1 or 2");
+  if constexpr (kDepth == 1) {
+    Raw<R> c0, c1;
+    load_raw(c0, w, 0);
+    int c = 0;
+    for (; c + 2 < nchunks; c += 2) {
+      mma_chunk<DT, R, MT, true>(c0, c1, lds, w, b, c, c + 1, acc);
+      mma_chunk<DT, R, MT, true>(c1, c0, lds, w, b, c + 1, c + 2, acc);
+    }
+    if (c + 1 < nchunks) {
+      mma_chunk<DT, R, MT, true>(c0, c1, lds, w, b, c, c + 1, acc);
+      mma_chunk<DT, R, MT, false>(c1, c0, lds, w, b, c + 1, 0, acc);
+    } else {
+      mma_chunk<DT, R, MT, false>(c0, c1, lds, w, b, c, 0, acc);
+    }
   } else {
-    mma_chunk<DT, R, MT, false>(c0, c1, lds, a, row4_bytes, b, c, acc);
+    Raw<R> c0, c1, c2;
+    load_raw(c0, w, 0);
+    if (nchunks > 1) load_raw(c1, w, 1);
+    int c = 0;
+    for (; c + 5 < nchunks; c += 3) {  // chunks c..c+2 consumed, c+2..c+4 issued
+      mma_chunk<DT, R, MT, true>(c0, c2, lds, w, b, c, c + 2, acc);
+      mma_chunk<DT, R, MT, true>(c1, c0, lds, w, b, c + 1, c + 3, acc);
+      mma_chunk<DT, R, MT, true>(c2, c1, lds, w, b, c + 2, c + 4, acc);
+    }
+    // 1..5 chunks remain (c..nchunks-1); chunks c and c+1 (if it exists) are in c0, c1
+    const int rem = nchunks - c;
+    if (rem >= 3) {
+      mma_chunk<DT, R, MT, true>(c0, c2, lds, w, b, c, c + 2, acc);
+      if (rem >= 4) {
+        mma_chunk<DT, R, MT, true>(c1, c0, lds, w, b, c + 1, c + 3, acc);
+        if (rem == 5) {
+          mma_chunk<DT, R, MT, true>(c2, c1, lds, w, b, c + 2, c + 4, acc);
+          mma_chunk<DT, R, MT, false>(c0, c2, lds, w, b, c + 3, 0, acc);
+          mma_chunk<DT, R, MT, false>(c1, c2, lds, w, b, c + 4, 0, acc);
+        } else {
+          mma_chunk<DT, R, MT, false>(c2, c1, lds, w, b, c + 2, 0, acc);
+          mma_chunk<DT, R, MT, false>(c0, c1, lds, w, b, c + 3, 0, acc);
+        }
+      } else {
+        mma_chunk<DT, R, MT, false>(c1, c0, lds, w, b, c + 1, 0, acc);
+        mma_chunk<DT, R, MT, false>(c2, c0, lds, w, b, c + 2, 0, acc);
+      }
+    } else if (rem == 2) {
+      mma_chunk<DT, R, MT, false>(c0, c2, lds, w, b, c, 0, acc);
+      mma_chunk<DT, R, MT, false>(c1, c2, lds, w, b, c + 1, 0, acc);
+    } else {
+      mma_chunk<DT, R, MT, false>(c0, c2, lds, w, b, c, 0, acc);
+    }
   }
 }
 
@@ -131,6 +194,11 @@ __device__ __forceinline__ void store4(void* base, int64_t idx, float v0, float 
 }
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
 
 template <int DT, int MT>
 __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
@@ -146,36 +214,38 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   const int active = uniform(a.rb.hdr[0]);
   const int off = uniform(a.rb.act_off[ai]);
   const int m = uniform(a.rb.act_cnt[ai]);
-  const int64_t slot = a.rb.act_slot[ai];
+  const int64_t slot = uniform64(a.rb.act_slot[ai]);
   if (ai >= active) return;
   const int H = a.H, I = a.I;
-  const S* page = static_cast<const S*>(a.pool) + slot * a.page_elems;
   const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
-  // coalesced-load lane origin: row lane/16 of the tile, byte column 16*(lane%16)
-  const int64_t lane_origin = (lane >> 4) * row_bytes + (lane & 15) * 16;
-  const char* arow[2] = {
-      reinterpret_cast<const char*>(page + static_cast<int64_t>(kRowTile * p) * H) + lane_origin,
-      reinterpret_cast<const char*>(page + static_cast<int64_t>(I + kRowTile * p) * H) + lane_origin};
+  const int64_t page_bytes = a.page_elems * static_cast<int64_t>(sizeof(S));
+  WeightStream ws;  // tile 0: gate rows [16p, 16p+16); tile 1: the matching up rows
+  ws.rsrc = make_rsrc(static_cast<const char*>(a.pool) + slot * page_bytes, static_cast<uint32_t>(page_bytes));
+  ws.base = static_cast<uint32_t>(kRowTile * p * row_bytes);
+  ws.tile_stride = static_cast<uint32_t>(I * row_bytes);
+  ws.row4 = static_cast<uint32_t>(4 * row_bytes);
+  ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
   const int nchunks = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
   __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
   u32x4* lds = lds_all[threadIdx.x / kWave];
-  const S* x = static_cast<const S*>(a.x);
   S* act = static_cast<S*>(a.act);
 
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
-    const char* brow[MT];
+    TokenStream<MT> tb;
+    tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
+    tb.base = 0;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = min(q0 + mt * kTokTile + r, m - 1);
       const int tok = a.rb.sorted_f[off + q] / a.k;
-      brow[mt] = reinterpret_cast<const char*>(x + static_cast<int64_t>(tok) * H) + g * 16;
+      tb.off[mt] = static_cast<uint32_t>(tok * row_bytes + g * 16);
     }
     f32x4 acc[2][MT];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_mfma<DT, 2, MT>(arow, 4 * row_bytes, brow, nchunks, lds, acc);
+    stream_mfma<DT, 2, MT, kGateUpDepth>(ws, tb, nchunks, lds, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -209,35 +279,37 @@ __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
   const int active = uniform(a.rb.hdr[0]);
   const int off = uniform(a.rb.act_off[ai]);
   const int m = uniform(a.rb.act_cnt[ai]);
-  const int64_t slot = a.rb.act_slot[ai];
+  const int64_t slot = uniform64(a.rb.act_slot[ai]);
   if (ai >= active) return;
   const int H = a.H, I = a.I;
   const int N = a.T * a.k;
-  const S* w2 = static_cast<const S*>(a.pool) + slot * a.page_elems + static_cast<int64_t>(2) * I * H;
-  const int k0 = sp * a.split_steps * kStepBytes / static_cast<int>(sizeof(S));  // element offset
   const int64_t row_bytes = static_cast<int64_t>(I) * sizeof(S);
-  const int64_t lane_origin = (lane >> 4) * row_bytes + (lane & 15) * 16;
-  const char* arow[R];
-#pragma unroll
-  for (int i = 0; i < R; ++i)
-    arow[i] = reinterpret_cast<const char*>(w2 + static_cast<int64_t>((rt * R + i) * kRowTile) * I + k0) + lane_origin;
+  const int64_t k0_bytes = static_cast<int64_t>(sp) * a.split_steps * kStepBytes;
+  const int64_t page_bytes = a.page_elems * static_cast<int64_t>(sizeof(S));
+  WeightStream ws;  // tiles: rows [(rt*R + i)*16, +16) of W2 (after W1, W3), this split's K slice
+  ws.rsrc = make_rsrc(static_cast<const char*>(a.pool) + slot * page_bytes, static_cast<uint32_t>(page_bytes));
+  ws.base = static_cast<uint32_t>(2 * H * row_bytes + rt * R * kRowTile * row_bytes + k0_bytes);
+  ws.tile_stride = static_cast<uint32_t>(kRowTile * row_bytes);
+  ws.row4 = static_cast<uint32_t>(4 * row_bytes);
+  ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
   __shared__ u32x4 lds_all[kExpertWaves][R * kTileSlots];
   u32x4* lds = lds_all[threadIdx.x / kWave];
-  const S* act = static_cast<const S*>(a.act);
 
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
-    const char* brow[MT];
+    TokenStream<MT> tb;
+    tb.rsrc = make_rsrc(a.act, static_cast<uint32_t>(static_cast<int64_t>(N) * row_bytes));
+    tb.base = static_cast<uint32_t>(k0_bytes);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = min(q0 + mt * kTokTile + r, m - 1);
-      brow[mt] = reinterpret_cast<const char*>(act + static_cast<int64_t>(off + q) * I + k0) + g * 16;
+      tb.off[mt] = static_cast<uint32_t>((off + q) * row_bytes + g * 16);
     }
     f32x4 acc[R][MT];
 #pragma unroll
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_mfma<DT, R, MT>(arow, 4 * row_bytes, brow, a.split_steps / kUnroll, lds, acc);
+    stream_mfma<DT, R, MT, kDownDepth>(ws, tb, a.split_steps / kUnroll, lds, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;

@@ -23,6 +23,8 @@ constexpr int kStepBytes = 64;                      // row bytes one 16-byte/lan
 constexpr int kUnroll = 4;                          // load steps per chunk (256 bytes per row)
 constexpr int kDownRows = 2;                        // row tiles per wave in the down projection
 constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 tokens)
+constexpr int kGateUpDepth = 1;                     // weight chunks in flight per wave (gate/up)
+constexpr int kDownDepth = 1;                       // weight chunks in flight per wave (down)
 
 static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
               "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");

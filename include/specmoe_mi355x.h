@@ -39,8 +39,9 @@ enum smx_status {
 
 /* Limits: 1 <= E <= 256; 1 <= top_k <= min(E, 16); T*top_k <= 16384;
  * H and I multiples of 128 for 16-bit types and of 64 for fp32 (a weight row is a whole
- * number of 256-byte chunks); H, I <= 2^20. T == 0 is a no-op. Larger T*top_k or E
- * return SMX_ERR_UNSUPPORTED. */
+ * number of 256-byte chunks); H, I <= 2^20; T*H and T*top_k*I activation bytes < 2^31;
+ * page_elems <= 2^30.
+ * T == 0 is a no-op. Shapes outside these limits return SMX_ERR_UNSUPPORTED. */
 
 /* Library version (major*10000 + minor*100 + patch). */
 int smx_version(void);
