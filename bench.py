@@ -42,7 +42,39 @@ def parse():
     ap.add_argument("--rotate", type=int, default=2, help="expert pool copies rotated per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-calls", type=int, default=2, help="CPU baseline sample: layer calls")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 1 GiB device copy 10 times (HBM counter calibration)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "traffic_gateup_kernel_mixtral_t32.json")
+
+
+def copy_calibration():
+    """A plain copy of known size, profiled beside the MoE kernels to scale the HBM byte
+    counters (FETCH_SIZE / WRITE_SIZE) to bytes."""
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n,
+                      "launches": 10}), flush=True)
+
+
+def measured_traffic(T, H, I, E, k):
+    """HBM bytes per gateup_kernel launch measured with rocprofv3 counters for this workload
+    (committed under profiles/), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("workload") != {"tokens": T, "hidden": H, "ffn": I, "experts": E, "top_k": k}:
+        return None
+    return t.get("bytes_per_launch")
 
 
 def main():
@@ -52,6 +84,9 @@ def main():
               "(the multi-GPU sharding of this path is a design, not a measured run)",
               file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     from ae_amd import _lib
     from ae_amd.layers._torch import ptr
@@ -172,7 +207,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gateup_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(T, H, I, E, k),
             "algorithmic_bytes": gateup_bytes,
             "us_per_launch": round(stage_us[1], 2),
         },
