@@ -1,6 +1,7 @@
 // Routing kernels: top-k softmax gating and the token -> expert sort.
 //
-// topk_softmax_kernel     one wave per token (lane = expert, up to 4 experts per lane).
+// topk_softmax_kernel     G lanes per token (G = next power of two >= E, at least 8; a wave
+//                         holds 64/G tokens; for E > 64 a lane holds up to 4 experts).
 // align_kernel            one workgroup: per-wave histograms built from ballot/popcount,
 //                         a wave-level scan in LDS, then a stable scatter; emits either the
 //                         compact per-expert lists the expert kernels consume or the
@@ -11,115 +12,129 @@
 namespace smx {
 
 // ---------------------------------------------------------------------------------------
-// Top-k softmax of one row, computed by one wave. On return lane j < k holds the j-th pick
-// (descending probability, ties to the lower expert index) in (w, id); other lanes hold
-// w = 0, id = -1. The arithmetic (max, exp_nonpos, per-lane sequential sum over the lane's
-// experts e = lane + 64*i, xor-butterfly across lanes, p = ex * (1/sum), renormalisation by
-// division with the sum taken in j order) is restated exactly by the oracle.
-// Semantics follow select_experts as called at specmoe/layers/FusedMoE.py:174-185.
+// Top-k softmax, G lanes per token (G = 8, 16, 32 or 64; a wave holds 64/G tokens). Lane j of
+// a group holds expert j (and j + 64*i for G = 64, up to 256 experts). On return lane j < k of
+// each group holds the j-th pick (descending probability, ties to the lower expert index).
+// The arithmetic (max, exp_nonpos, per-lane sequential sum, xor butterfly over the group,
+// p = ex * (1/sum), renormalisation by division with the sum taken in j order) equals the
+// oracle's 64-lane tree bit for bit: with E <= G every lane at or past G holds an exact zero,
+// so the butterfly steps at offsets >= G only add zeros. Semantics follow select_experts as
+// called at specmoe/layers/FusedMoE.py:174-185.
 // ---------------------------------------------------------------------------------------
-template <int LDT>
-__device__ __forceinline__ void load_logits(const void* logits, int64_t row, int E,
-                                            float (&v)[kMaxExpertsPerLane]) {
-  const int lane = lane_id();
+template <int G>
+struct TopkGroup {
+  static constexpr int kPerLane = (G == kWave) ? kMaxExpertsPerLane : 1;  // experts per lane
+  static constexpr int kTokens = kWave / G;                               // tokens per wave
+};
+
+template <int LDT, int G>
+__device__ __forceinline__ void load_logits(const void* logits, int t, int T, int E,
+                                            float (&v)[TopkGroup<G>::kPerLane]) {
+  const int j = lane_id() % G;
 #pragma unroll
-  for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-    const int e = lane + kWave * i;
-    v[i] = (e < E) ? load_as_f32<LDT>(logits, row * E + e) : -__builtin_inff();
+  for (int i = 0; i < TopkGroup<G>::kPerLane; ++i) {
+    const int e = j + G * i;
+    v[i] = (t < T && e < E) ? load_as_f32<LDT>(logits, static_cast<int64_t>(t) * E + e) : -__builtin_inff();
   }
 }
 
-__device__ __forceinline__ void wave_topk_softmax(float (&p)[kMaxExpertsPerLane], int E, int k,
-                                                  bool renorm, float& w_out, int& id_out) {
+template <int G>
+__device__ __forceinline__ void group_topk_softmax(float (&p)[TopkGroup<G>::kPerLane], int E, int k,
+                                                   bool renorm, float& w_out, int& id_out) {
 #pragma clang fp contract(off)
+  constexpr int PL = TopkGroup<G>::kPerLane;
   const int lane = lane_id();
+  const int j = lane % G;
+  const int base = lane - j;
   float m = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < kMaxExpertsPerLane; ++i) m = fmaxf(m, p[i]);
-  m = wave_max(m);
+  for (int i = 0; i < PL; ++i) m = fmaxf(m, p[i]);
+#pragma unroll
+  for (int off = G / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
   float s = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-    const int e = lane + kWave * i;
+  for (int i = 0; i < PL; ++i) {
+    const int e = j + G * i;
     p[i] = (e < E) ? exp_nonpos(p[i] - m) : 0.0f;
     s = (i == 0) ? p[i] : s + p[i];
   }
-  s = wave_sum_butterfly(s);
+#pragma unroll
+  for (int off = G / 2; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, kWave);
   const float inv = 1.0f / s;
 #pragma unroll
-  for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-    const int e = lane + kWave * i;
+  for (int i = 0; i < PL; ++i) {
+    const int e = j + G * i;
     p[i] = (e < E) ? p[i] * inv : -1.0f;  // -1 marks "not selectable"
   }
   w_out = 0.0f;
   id_out = -1;
-  for (int j = 0; j < k; ++j) {
+  for (int jj = 0; jj < k; ++jj) {
     float bp = -2.0f;
     int be = 0x7fffffff;
 #pragma unroll
-    for (int i = 0; i < kMaxExpertsPerLane; ++i) {
-      if (p[i] > bp) { bp = p[i]; be = lane + kWave * i; }  // ascending e: strict > keeps lowest
+    for (int i = 0; i < PL; ++i) {
+      if (p[i] > bp) { bp = p[i]; be = j + G * i; }  // ascending e: strict > keeps lowest
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
+    for (int off = G / 2; off >= 1; off >>= 1) {
       const float op = __shfl_xor(bp, off, kWave);
       const int oe = __shfl_xor(be, off, kWave);
       if (op > bp || (op == bp && oe < be)) { bp = op; be = oe; }
     }
-    if (lane == (be & (kWave - 1))) {
+    if (j == be % G) {
 #pragma unroll
-      for (int i = 0; i < kMaxExpertsPerLane; ++i)
-        if (i == (be >> 6)) p[i] = -1.0f;
+      for (int i = 0; i < PL; ++i)
+        if (i == be / G) p[i] = -1.0f;
     }
-    if (lane == j) { w_out = bp; id_out = be; }
+    if (j == jj) { w_out = bp; id_out = be; }
   }
   if (renorm) {
     float sum = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      const float v = __shfl(w_out, j, kWave);
-      sum = (j == 0) ? v : sum + v;
+    for (int jj = 0; jj < k; ++jj) {
+      const float v = __shfl(w_out, base + jj, kWave);
+      sum = (jj == 0) ? v : sum + v;
     }
-    if (lane < k) w_out = w_out / sum;
+    if (j < k) w_out = w_out / sum;
   }
 }
 
-// Tokens t = first, first + stride, ... (up to kTokBatch of them) handled by one wave: all
-// logit loads are issued before any token is processed, so a wave pays one load latency per
-// batch rather than one per token. fn(t, w, id) receives each token's result on every lane.
-template <int LDT, typename Fn>
-__device__ __forceinline__ void wave_topk_batch(const void* logits, int T, int E, int k,
-                                                bool renorm, int first, int stride, Fn&& fn) {
-  float v[kTokBatch][kMaxExpertsPerLane];
+// The tokens of `passes` consecutive wave-passes: token t = (pass0 + b) * stride + slot, where
+// slot = lane / G. All logit loads are issued before any token is computed, so a wave pays
+// one load latency per batch. fn(t, w, id) is called on every lane (t may be >= T).
+template <int LDT, int G, typename Fn>
+__device__ __forceinline__ void topk_batch(const void* logits, int T, int E, int k, bool renorm,
+                                           int first, int stride, Fn&& fn) {
+  constexpr int PL = TopkGroup<G>::kPerLane;
+  float v[kTokBatch][PL];
+#pragma unroll
+  for (int b = 0; b < kTokBatch; ++b) load_logits<LDT, G>(logits, first + b * stride, T, E, v[b]);
 #pragma unroll
   for (int b = 0; b < kTokBatch; ++b) {
-    const int t = first + b * stride;
-    if (t < T) load_logits<LDT>(logits, t, E, v[b]);
-  }
-#pragma unroll
-  for (int b = 0; b < kTokBatch; ++b) {
-    const int t = first + b * stride;
-    if (t < T) {
+    if (first + b * stride - lane_id() / G < T) {  // some token of this wave-pass exists
       float w;
       int id;
-      wave_topk_softmax(v[b], E, k, renorm, w, id);
-      fn(t, w, id);
+      group_topk_softmax<G>(v[b], E, k, renorm, w, id);
+      fn(first + b * stride, w, id);
     }
   }
 }
 
-template <int LDT>
+template <int LDT, int G>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restrict__ logits,
                                                            int T, int E, int k, int renorm,
                                                            float* __restrict__ w,
                                                            int32_t* __restrict__ ids) {
+  constexpr int TPW = TopkGroup<G>::kTokens;
   const int waves = blockDim.x / kWave;
-  const int stride = gridDim.x * waves;
   const int lane = lane_id();
-  for (int t0 = blockIdx.x * waves + threadIdx.x / kWave; t0 < T; t0 += stride * kTokBatch) {
-    wave_topk_batch<LDT>(logits, T, E, k, renorm != 0, t0, stride, [&](int t, float wv, int id) {
-      if (lane < k) {
-        w[(int64_t)t * k + lane] = wv;
-        ids[(int64_t)t * k + lane] = id;
+  const int j = lane % G;
+  const int stride = gridDim.x * waves * TPW;  // tokens per pass of the whole grid
+  for (int t0 = (blockIdx.x * waves + threadIdx.x / kWave) * TPW + lane / G; t0 - lane / G < T;
+       t0 += stride * kTokBatch) {
+    topk_batch<LDT, G>(logits, T, E, k, renorm != 0, t0, stride, [&](int t, float wv, int id) {
+      if (t < T && j < k) {
+        w[static_cast<int64_t>(t) * k + j] = wv;
+        ids[static_cast<int64_t>(t) * k + j] = id;
       }
     });
   }
@@ -133,20 +148,23 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restric
 // specmoe/layers/fused_moe_kernel.py:16-85 (its docstring example fixes the order).
 // ---------------------------------------------------------------------------------------
 struct AlignShared {
-  int16_t ids[kMaxAssignments];
+  int16_t ids[kMaxAssignments];        // expert per flat assignment; -1 dropped, -2 out of range
   int cntw[kRouteWaves][kMaxExperts];  // per-wave counts, then per-wave start positions
   int cnt[kMaxExperts];
   int off[kMaxExperts + 1];            // compact exclusive prefix
   int seg[kMaxExperts + 1];            // block-padded exclusive prefix
   int act[kMaxExperts + 1];            // active-expert exclusive prefix
+  int64_t slot[kMaxExperts];           // pool slot per expert (-1: unmapped), route only
+  int bad;                             // an assignment was dropped
 };
 
 struct AlignOutputs {
   // compact lists for the expert kernels (may be null)
-  int32_t* hdr;         // [0] = number of active experts
+  int32_t* hdr;         // [0] = number of active experts, [1] = dropped-assignment flag
   int32_t* act_expert;  // [E]
   int32_t* act_off;     // [E]
   int32_t* act_cnt;     // [E]
+  int64_t* act_slot;    // [E]
   int32_t* sorted_f;    // [N]
   // reference-format outputs (may be null)
   int32_t* sorted_ids;  // [N + E*(BM-1)]
@@ -156,17 +174,21 @@ struct AlignOutputs {
 };
 
 // Walks this wave's contiguous range of f in 64-wide chunks; for every group of lanes that
-// share an expert, calls fn(mask, e) on all lanes of the wave (uniform control flow).
-template <typename Fn>
-__device__ __forceinline__ void for_each_expert_group(const AlignShared& sh, int N, int wave,
-                                                      Fn&& fn) {
+// share an expert, calls fn(mask, e, f, mine, leader) on all lanes of the wave (uniform
+// control flow). Assignments whose expert is unroutable count as dropped.
+template <bool kCheckSlots, typename Fn>
+__device__ __forceinline__ void for_each_expert_group(AlignShared& sh, int N, int wave, Fn&& fn) {
   const int lane = lane_id();
   const int per_wave = ((N + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
   const int begin = wave * per_wave;
   const int end = min(N, begin + per_wave);
   for (int base = begin; base < end; base += kWave) {
     const int f = base + lane;
-    const int e = (f < end) ? static_cast<int>(sh.ids[f]) : -1;
+    int e = (f < end) ? static_cast<int>(sh.ids[f]) : -1;
+    if (e == -2 || (kCheckSlots && e >= 0 && sh.slot[e] < 0)) {
+      sh.bad = 1;
+      e = -1;
+    }
     uint64_t pending = ballot(e >= 0);
     while (pending) {
       const int leader = __ffsll(static_cast<long long>(pending)) - 1;
@@ -178,39 +200,38 @@ __device__ __forceinline__ void for_each_expert_group(const AlignShared& sh, int
   }
 }
 
+// Stable expert sort of the assignments in sh.ids. Precondition (caller): sh.cntw zeroed,
+// sh.ids (and sh.slot when kCheckSlots) written, and a barrier since.
+template <bool kCheckSlots>
 __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& out) {
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = lane_id();
-  for (int i = tid; i < kRouteWaves * kMaxExperts; i += blockDim.x) (&sh.cntw[0][0])[i] = 0;
-  __syncthreads();
 
   // pass 1: per-wave histograms
-  for_each_expert_group(sh, N, wave, [&](uint64_t m, int el, int, bool, int leader) {
+  for_each_expert_group<kCheckSlots>(sh, N, wave, [&](uint64_t m, int el, int, bool, int leader) {
     if (lane == leader) sh.cntw[wave][el] += __popcll(m);
   });
   __syncthreads();
 
-  // per expert: total, and per-wave exclusive prefix (over waves, in wave order)
-  for (int e = tid; e < E; e += blockDim.x) {
-    int run = 0;
-    for (int w = 0; w < kRouteWaves; ++w) {
-      const int c = sh.cntw[w][e];
-      sh.cntw[w][e] = run;
-      run += c;
-    }
-    sh.cnt[e] = run;
-  }
-  __syncthreads();
-
-  // prefix over experts (wave 0; each lane owns 4 consecutive experts)
+  // wave 0: per-expert totals and per-wave prefixes, then exclusive scans over experts
+  // (each lane owns 4 consecutive experts), the per-wave start positions and the compact
+  // active-expert table.
   if (wave == 0) {
     const int bm = out.bm > 0 ? out.bm : 1;
     int c[4], sc = 0, sp = 0, sa = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
-      c[i] = (e < E) ? sh.cnt[e] : 0;
+      c[i] = 0;
+      if (e < E) {
+        for (int w = 0; w < kRouteWaves; ++w) {
+          const int v = sh.cntw[w][e];
+          sh.cntw[w][e] = c[i];  // per-wave exclusive prefix, in wave order
+          c[i] += v;
+        }
+        sh.cnt[e] = c[i];
+      }
       sc += c[i];
       sp += (c[i] + bm - 1) / bm * bm;
       sa += c[i] > 0;
@@ -228,6 +249,15 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
       if (e <= E) { sh.off[e] = bc; sh.seg[e] = bp; sh.act[e] = ba; }
+      if (e < E) {
+        for (int w = 0; w < kRouteWaves; ++w) sh.cntw[w][e] += bc;
+        if (out.act_expert && c[i] > 0) {
+          out.act_expert[ba] = e;
+          out.act_off[ba] = bc;
+          out.act_cnt[ba] = c[i];
+          if constexpr (kCheckSlots) out.act_slot[ba] = sh.slot[e];
+        }
+      }
       bc += c[i];
       bp += (c[i] + bm - 1) / bm * bm;
       ba += c[i] > 0;
@@ -235,27 +265,14 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
     if (E == 4 * kWave && lane == kWave - 1) { sh.off[E] = bc; sh.seg[E] = bp; sh.act[E] = ba; }
   }
   __syncthreads();
-
-  // per-wave start positions; compact active-expert table
-  for (int e = tid; e < E; e += blockDim.x) {
-    const int o = sh.off[e];
-    for (int w = 0; w < kRouteWaves; ++w) sh.cntw[w][e] += o;
-    if (out.act_expert && sh.cnt[e] > 0) {
-      const int a = sh.act[e];
-      out.act_expert[a] = e;
-      out.act_off[a] = o;
-      out.act_cnt[a] = sh.cnt[e];
-    }
-  }
   if (tid == 0) {
-    if (out.hdr) out.hdr[0] = sh.act[E];
+    if (out.hdr) { out.hdr[0] = sh.act[E]; out.hdr[1] = sh.bad; }
     if (out.ntp) out.ntp[0] = sh.seg[E];
   }
-  __syncthreads();
 
   // pass 2: stable scatter
   const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-  for_each_expert_group(sh, N, wave, [&](uint64_t m, int el, int f, bool mine, int leader) {
+  for_each_expert_group<kCheckSlots>(sh, N, wave, [&](uint64_t m, int el, int f, bool mine, int leader) {
     const int base = sh.cntw[wave][el];
     if (mine) {
       const int pos = base + __popcll(m & lt_mask);
@@ -279,43 +296,50 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
   }
 }
 
+__device__ __forceinline__ void zero_counts(AlignShared& sh) {
+  for (int i = threadIdx.x; i < kRouteWaves * kMaxExperts; i += blockDim.x) (&sh.cntw[0][0])[i] = 0;
+  if (threadIdx.x == 0) sh.bad = 0;
+}
+
 // Reference-format alignment of caller-provided ids.
 __global__ __launch_bounds__(kRouteThreads) void align_kernel(const int32_t* __restrict__ ids,
                                                               int N, int E, AlignOutputs out) {
   __shared__ AlignShared sh;
+  zero_counts(sh);
   for (int f = threadIdx.x; f < N; f += blockDim.x) {
     const int e = ids[f];
     sh.ids[f] = static_cast<int16_t>((e >= 0 && e < E) ? e : -1);
   }
   __syncthreads();
-  align_block(sh, N, E, out);
+  align_block<false>(sh, N, E, out);
 }
 
-// Routing for the expert kernels. With logits != null the top-k softmax runs first (one wave
-// per token, results to w/ids and LDS); otherwise ids come from the caller. Then the compact
-// expert sort. Ids outside [0,E) and experts whose pool slot is outside [0,num_slots) are
-// dropped here (they contribute nothing) and flagged in hdr[1].
-template <int LDT>
+// Routing for the expert kernels. With logits != null the top-k softmax runs first (results
+// to w/ids and LDS); otherwise ids come from the caller. Then the compact expert sort.
+// Assignments with an id outside [0,E), or whose expert's pool slot is outside
+// [0,num_slots), are dropped (they contribute nothing) and flagged in hdr[1].
+template <int LDT, int G>
 __global__ __launch_bounds__(kRouteThreads) void route_kernel(
     const void* __restrict__ logits, int T, int E, int k, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ ids_out, const int32_t* __restrict__ ids_in,
-    const int64_t* __restrict__ e2s, int64_t num_slots, AlignOutputs out, int64_t* act_slot) {
+    const int64_t* __restrict__ e2s, int64_t num_slots, AlignOutputs out) {
   __shared__ AlignShared sh;
-  __shared__ int64_t slot_of[kMaxExperts];
-  __shared__ int bad;
+  constexpr int TPW = TopkGroup<G>::kTokens;
   const int N = T * k;
   const int wave = threadIdx.x / kWave;
   const int lane = lane_id();
-  if (threadIdx.x == 0) bad = 0;
+  zero_counts(sh);
   for (int e = threadIdx.x; e < E; e += blockDim.x) {
     const int64_t slot = e2s[e];
-    slot_of[e] = (slot >= 0 && slot < num_slots) ? slot : -1;
+    sh.slot[e] = (slot >= 0 && slot < num_slots) ? slot : -1;
   }
   if (logits != nullptr) {
-    for (int t0 = wave; t0 < T; t0 += kRouteWaves * kTokBatch) {
-      wave_topk_batch<LDT>(logits, T, E, k, renorm != 0, t0, kRouteWaves, [&](int t, float wv, int id) {
-        if (lane < k) {
-          const int f = t * k + lane;
+    const int j = lane % G;
+    const int stride = kRouteWaves * TPW;
+    for (int t0 = wave * TPW + lane / G; t0 - lane / G < T; t0 += stride * kTokBatch) {
+      topk_batch<LDT, G>(logits, T, E, k, renorm != 0, t0, stride, [&](int t, float wv, int id) {
+        if (t < T && j < k) {
+          const int f = t * k + j;
           if (w_out) w_out[f] = wv;
           if (ids_out) ids_out[f] = id;
           sh.ids[f] = static_cast<int16_t>(id);
@@ -325,34 +349,45 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
   } else {
     for (int f = threadIdx.x; f < N; f += blockDim.x) {
       const int e = ids_in[f];
-      sh.ids[f] = static_cast<int16_t>((e >= 0 && e < E) ? e : -2);  // -2: out of range
+      sh.ids[f] = static_cast<int16_t>((e >= 0 && e < E) ? e : -2);
     }
   }
-  __syncthreads();  // also orders thread 0's `bad = 0` before any `bad = 1`
-  for (int f = threadIdx.x; f < N; f += blockDim.x) {
-    const int e = sh.ids[f];
-    if (e == -2 || (e >= 0 && slot_of[e] < 0)) { sh.ids[f] = -1; bad = 1; }
-  }
   __syncthreads();
-  if (threadIdx.x == 0) out.hdr[1] = bad;
-  align_block(sh, N, E, out);
-  // pool slot of each active expert, so the expert kernels need one dependent load, not two
-  for (int e = threadIdx.x; e < E; e += blockDim.x)
-    if (sh.cnt[e] > 0) act_slot[sh.act[e]] = slot_of[e];
+  align_block<true>(sh, N, E, out);
 }
 
 // ---------------------------------------------------------------------------------------
 // Host-side launchers
 // ---------------------------------------------------------------------------------------
+static int group_for(int E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64; }
+
+template <int LDT, int G>
+static void topk_launch(const void* logits, int T, int E, int k, int renorm, float* w, int32_t* ids,
+                        hipStream_t s) {
+  const int waves = 4;
+  const int per_block = waves * TopkGroup<G>::kTokens * kTokBatch;
+  int blocks = (T + per_block - 1) / per_block;
+  if (blocks > 65535) blocks = 65535;
+  topk_softmax_kernel<LDT, G><<<blocks, waves * kWave, 0, s>>>(logits, T, E, k, renorm, w, ids);
+}
+
+template <int LDT>
+static void topk_launch_g(const void* logits, int T, int E, int k, int renorm, float* w,
+                          int32_t* ids, hipStream_t s) {
+  switch (group_for(E)) {
+    case 8: topk_launch<LDT, 8>(logits, T, E, k, renorm, w, ids, s); break;
+    case 16: topk_launch<LDT, 16>(logits, T, E, k, renorm, w, ids, s); break;
+    case 32: topk_launch<LDT, 32>(logits, T, E, k, renorm, w, ids, s); break;
+    default: topk_launch<LDT, 64>(logits, T, E, k, renorm, w, ids, s); break;
+  }
+}
+
 hipError_t launch_topk_softmax(const void* logits, int ldt, int T, int E, int k, int renorm,
                                float* w, int32_t* ids, hipStream_t s) {
-  const int waves = 4;
-  int blocks = (T + waves - 1) / waves;
-  if (blocks > 65535) blocks = 65535;
   switch (ldt) {
-    case kF32: topk_softmax_kernel<kF32><<<blocks, waves * kWave, 0, s>>>(logits, T, E, k, renorm, w, ids); break;
-    case kF16: topk_softmax_kernel<kF16><<<blocks, waves * kWave, 0, s>>>(logits, T, E, k, renorm, w, ids); break;
-    default: topk_softmax_kernel<kBF16><<<blocks, waves * kWave, 0, s>>>(logits, T, E, k, renorm, w, ids); break;
+    case kF32: topk_launch_g<kF32>(logits, T, E, k, renorm, w, ids, s); break;
+    case kF16: topk_launch_g<kF16>(logits, T, E, k, renorm, w, ids, s); break;
+    default: topk_launch_g<kBF16>(logits, T, E, k, renorm, w, ids, s); break;
   }
   return hipGetLastError();
 }
@@ -368,6 +403,18 @@ hipError_t launch_align(const int32_t* ids, int N, int E, int bm, int32_t* sorte
   return hipGetLastError();
 }
 
+template <int LDT>
+static void route_launch_g(const void* logits, int T, int E, int k, int renorm, float* w_out,
+                           int32_t* ids_out, const int32_t* ids_in, const int64_t* e2s,
+                           int64_t num_slots, const AlignOutputs& out, hipStream_t s) {
+  switch (group_for(E)) {
+    case 8: route_kernel<LDT, 8><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    case 16: route_kernel<LDT, 16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    case 32: route_kernel<LDT, 32><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    default: route_kernel<LDT, 64><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+  }
+}
+
 hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int renorm,
                         float* w_out, int32_t* ids_out, const int32_t* ids_in,
                         const int64_t* e2s, int64_t num_slots, const RouteBuffers& rb,
@@ -377,12 +424,13 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
   out.act_expert = rb.act_expert;
   out.act_off = rb.act_off;
   out.act_cnt = rb.act_cnt;
+  out.act_slot = rb.act_slot;
   out.sorted_f = rb.sorted_f;
   out.bm = 1;
   switch (ldt) {
-    case kF32: route_kernel<kF32><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, rb.act_slot); break;
-    case kF16: route_kernel<kF16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, rb.act_slot); break;
-    default: route_kernel<kBF16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, rb.act_slot); break;
+    case kF32: route_launch_g<kF32>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+    case kF16: route_launch_g<kF16>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+    default: route_launch_g<kBF16>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
   }
   return hipGetLastError();
 }

@@ -6,7 +6,7 @@
 namespace smx {
 
 // Routing limits (one workgroup sorts all assignments in LDS).
-constexpr int kRouteThreads = 1024;
+constexpr int kRouteThreads = 256;
 constexpr int kRouteWaves = kRouteThreads / kWave;
 constexpr int kMaxExperts = 256;
 constexpr int kMaxExpertsPerLane = kMaxExperts / kWave;
