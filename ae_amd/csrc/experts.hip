@@ -72,28 +72,61 @@ __device__ __forceinline__ void load_raw(Raw<R>& c, const WeightStream& w, int c
           w.rsrc, w.lane_off, cbase + r * w.tile_stride + i * w.row4, kNonTemporal);
 }
 
-// Token operand: column c of token tile mt is a row of a row-major matrix; lane l reads its
-// 16 bytes at K group l/16.
+// Token operand, shared by the workgroup. The 4 waves of a workgroup work on the same expert
+// and step through K together. Each chunk of the MT token tiles (16 token rows x 256 bytes
+// each) is loaded once per workgroup -- wave w loads rows 4w..4w+3 of every tile, one
+// 4-row x 256-byte instruction per tile -- into a double-buffered LDS tile with the same
+// padded layout as the weight tiles, and every wave reads its MFMA B fragments from there.
+// One barrier per chunk; every wave of a workgroup runs the same number of chunks.
 template <int MT>
-struct TokenStream {
+struct SharedTokens {
   __amdgpu_buffer_rsrc_t rsrc;
   uint32_t base;     // byte offset of the K range (wave-uniform)
-  uint32_t off[MT];  // per lane: row offset + 16*(l/16)
+  uint32_t off[MT];  // per lane: offset of row 4*wave + l/16 of tile j, + 16*(l%16)
 };
 
-template <int DT, int R, int MT, bool kPrefetch>
-__device__ __forceinline__ void mma_chunk(const Raw<R>& c, Raw<R>& next, u32x4* lds,
-                                          const WeightStream& w, const TokenStream<MT>& b,
-                                          int chunk, int next_chunk, f32x4 (&acc)[R][MT]) {
+template <int MT>
+struct RawTokens {
+  u32x4 v[MT];
+};
+
+template <int MT>
+__device__ __forceinline__ void load_tokens(RawTokens<MT>& rb, const SharedTokens<MT>& t, int chunk) {
+  const uint32_t cbase = t.base + static_cast<uint32_t>(chunk) * (kStepBytes * kUnroll);
+#pragma unroll
+  for (int j = 0; j < MT; ++j) rb.v[j] = __builtin_amdgcn_raw_buffer_load_b128(t.rsrc, t.off[j], cbase, 0);
+}
+
+template <int MT>
+__device__ __forceinline__ void store_tokens(const RawTokens<MT>& rb, u32x4* bt) {
   const int lane = lane_id();
-  const uint32_t bbase = b.base + static_cast<uint32_t>(chunk) * (kStepBytes * kUnroll);
-  u32x4 bf[kUnroll][MT];
+  const int wave = threadIdx.x / kWave;
+  u32x4* wr = bt + kPitch * (4 * wave + (lane >> 4)) + (lane & 15);
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      bf[u][mt] = __builtin_amdgcn_raw_buffer_load_b128(b.rsrc, b.off[mt], bbase + u * kStepBytes, 0);
-  if constexpr (kPrefetch) load_raw(next, w, next_chunk);
+  for (int j = 0; j < MT; ++j) wr[j * kTileSlots] = rb.v[j];
+}
+
+// Workgroup barrier ordering LDS only: in-flight global loads stay in flight.
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// One chunk: issue the next chunk's token loads, then its weight loads (so waiting for the
+// tokens never waits for the weights); transpose this chunk's weights through the
+// wave-private LDS tile; MFMAs against the shared token tile `bt`; publish the next chunk's
+// token tile into `bt_next`; barrier.
+template <int DT, int R, int MT, bool kPrefetch>
+__device__ __forceinline__ void wg_chunk(const Raw<R>& c, Raw<R>& next, RawTokens<MT>& rb,
+                                         u32x4* lds, const u32x4* bt, u32x4* bt_next,
+                                         const WeightStream& w, const SharedTokens<MT>& t,
+                                         int chunk, f32x4 (&acc)[R][MT]) {
+  const int lane = lane_id();
+  if constexpr (kPrefetch) {
+    load_tokens(rb, t, chunk + 1);
+    load_raw(next, w, chunk + 1);
+  }
   // Keep the scheduler from sinking loads into the MFMA sequence (which would shrink the
   // prefetch distance) or from waiting on the prefetch early.
   __builtin_amdgcn_sched_barrier(0);
@@ -103,74 +136,48 @@ __device__ __forceinline__ void mma_chunk(const Raw<R>& c, Raw<R>& next, u32x4* 
 #pragma unroll
     for (int r = 0; r < R; ++r) wr[r * kTileSlots + 4 * kPitch * i] = c.v[i][r];
   const u32x4* rd = lds + kPitch * (lane & 15) + (lane >> 4);
+  const u32x4* brd = bt + kPitch * (lane & 15) + (lane >> 4);
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     u32x4 af[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) af[r] = rd[r * kTileSlots + 4 * u];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt) {
+      const u32x4 bf = brd[mt * kTileSlots + 4 * u];
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r][mt] = Elem<DT>::mfma(af[r], bf[u][mt], acc[r][mt]);
+      for (int r = 0; r < R; ++r) acc[r][mt] = Elem<DT>::mfma(af[r], bf, acc[r][mt]);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kPrefetch) store_tokens(rb, bt_next);
+  wg_barrier();
 }
 
-// acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt (16 columns). Weight chunks are
-// loaded kDepth chunks ahead of the one being transposed and multiplied (a ring of kDepth+1
-// register buffers), so each wave keeps kDepth chunks of weights in flight.
-template <int DT, int R, int MT, int kDepth>
-__device__ __forceinline__ void stream_mfma(const WeightStream& w, const TokenStream<MT>& b,
-                                            int nchunks, u32x4* lds, f32x4 (&acc)[R][MT]) {
-  static_assert(kDepth == 1 || kDepth == 2, "prefetch depth 1 or 2");
-  if constexpr (kDepth == 1) {
-    Raw<R> c0, c1;
-    load_raw(c0, w, 0);
-    int c = 0;
-    for (; c + 2 < nchunks; c += 2) {
-      mma_chunk<DT, R, MT, true>(c0, c1, lds, w, b, c, c + 1, acc);
-      mma_chunk<DT, R, MT, true>(c1, c0, lds, w, b, c + 1, c + 2, acc);
-    }
-    if (c + 1 < nchunks) {
-      mma_chunk<DT, R, MT, true>(c0, c1, lds, w, b, c, c + 1, acc);
-      mma_chunk<DT, R, MT, false>(c1, c0, lds, w, b, c + 1, 0, acc);
-    } else {
-      mma_chunk<DT, R, MT, false>(c0, c1, lds, w, b, c, 0, acc);
-    }
+// acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt, the workgroup streaming the token
+// chunks through `bsh` (two buffers of MT tiles) while each wave streams its own weights.
+template <int DT, int R, int MT>
+__device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTokens<MT>& t,
+                                          int nchunks, u32x4* lds, u32x4* bsh,
+                                          f32x4 (&acc)[R][MT]) {
+  Raw<R> c0, c1;
+  RawTokens<MT> rb;
+  u32x4* b0 = bsh;
+  u32x4* b1 = bsh + MT * kTileSlots;
+  load_tokens(rb, t, 0);
+  load_raw(c0, w, 0);
+  store_tokens(rb, b0);
+  wg_barrier();
+  int c = 0;
+  for (; c + 2 < nchunks; c += 2) {
+    wg_chunk<DT, R, MT, true>(c0, c1, rb, lds, b0, b1, w, t, c, acc);
+    wg_chunk<DT, R, MT, true>(c1, c0, rb, lds, b1, b0, w, t, c + 1, acc);
+  }
+  if (c + 1 < nchunks) {
+    wg_chunk<DT, R, MT, true>(c0, c1, rb, lds, b0, b1, w, t, c, acc);
+    wg_chunk<DT, R, MT, false>(c1, c0, rb, lds, b1, b0, w, t, c + 1, acc);
   } else {
-    Raw<R> c0, c1, c2;
-    load_raw(c0, w, 0);
-    if (nchunks > 1) load_raw(c1, w, 1);
-    int c = 0;
-    for (; c + 5 < nchunks; c += 3) {  // chunks c..c+2 consumed, c+2..c+4 issued
-      mma_chunk<DT, R, MT, true>(c0, c2, lds, w, b, c, c + 2, acc);
-      mma_chunk<DT, R, MT, true>(c1, c0, lds, w, b, c + 1, c + 3, acc);
-      mma_chunk<DT, R, MT, true>(c2, c1, lds, w, b, c + 2, c + 4, acc);
-    }
-    // 1..5 chunks remain (c..nchunks-1); chunks c and c+1 (if it exists) are in c0, c1
-    const int rem = nchunks - c;
-    if (rem >= 3) {
-      mma_chunk<DT, R, MT, true>(c0, c2, lds, w, b, c, c + 2, acc);
-      if (rem >= 4) {
-        mma_chunk<DT, R, MT, true>(c1, c0, lds, w, b, c + 1, c + 3, acc);
-        if (rem == 5) {
-          mma_chunk<DT, R, MT, true>(c2, c1, lds, w, b, c + 2, c + 4, acc);
-          mma_chunk<DT, R, MT, false>(c0, c2, lds, w, b, c + 3, 0, acc);
-          mma_chunk<DT, R, MT, false>(c1, c2, lds, w, b, c + 4, 0, acc);
-        } else {
-          mma_chunk<DT, R, MT, false>(c2, c1, lds, w, b, c + 2, 0, acc);
-          mma_chunk<DT, R, MT, false>(c0, c1, lds, w, b, c + 3, 0, acc);
-        }
-      } else {
-        mma_chunk<DT, R, MT, false>(c1, c0, lds, w, b, c + 1, 0, acc);
-        mma_chunk<DT, R, MT, false>(c2, c0, lds, w, b, c + 2, 0, acc);
-      }
-    } else if (rem == 2) {
-      mma_chunk<DT, R, MT, false>(c0, c2, lds, w, b, c, 0, acc);
-      mma_chunk<DT, R, MT, false>(c1, c2, lds, w, b, c + 1, 0, acc);
-    } else {
-      mma_chunk<DT, R, MT, false>(c0, c2, lds, w, b, c, 0, acc);
-    }
+    wg_chunk<DT, R, MT, false>(c0, c1, rb, lds, b0, b1, w, t, c, acc);
   }
 }
 
@@ -200,22 +207,29 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Workgroup = (active expert, 4 consecutive weight tiles): wave w owns tile 4*group + w. A
+// wave past the expert's last tile streams the last tile again and stores nothing, so every
+// wave of a workgroup runs the same chunks and barriers.
 template <int DT, int MT>
 __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   using S = typename Elem<DT>::S;
   const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int tiles = a.I / kRowTile;
-  const int gw = uniform(blockIdx.x * kExpertWaves + threadIdx.x / kWave);
-  const int ai = gw / tiles;
-  const int p = gw - ai * tiles;
+  const int groups = (tiles + kExpertWaves - 1) / kExpertWaves;
+  const int ai = blockIdx.x / groups;  // uniform across the workgroup
+  const int tg = blockIdx.x - ai * groups;
   // ai < max_active <= E, so the per-expert arrays may be read before the active count is
-  // known (the four loads then share one latency); values past the active count are unused.
+  // known (the loads then share one latency); values past the active count are unused.
   const int active = uniform(a.rb.hdr[0]);
   const int off = uniform(a.rb.act_off[ai]);
   const int m = uniform(a.rb.act_cnt[ai]);
   const int64_t slot = uniform64(a.rb.act_slot[ai]);
   if (ai >= active) return;
+  const int praw = tg * kExpertWaves + wave;
+  const bool owner = praw < tiles;
+  const int p = owner ? praw : tiles - 1;
   const int H = a.H, I = a.I;
   const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
   const int64_t page_bytes = a.page_elems * static_cast<int64_t>(sizeof(S));
@@ -227,29 +241,30 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
   const int nchunks = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
   __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
-  u32x4* lds = lds_all[threadIdx.x / kWave];
+  __shared__ u32x4 bsh[2 * MT * kTileSlots];
+  u32x4* lds = lds_all[wave];
   S* act = static_cast<S*>(a.act);
 
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
-    TokenStream<MT> tb;
+    SharedTokens<MT> tb;
     tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
     tb.base = 0;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int q = min(q0 + mt * kTokTile + r, m - 1);
+    for (int j = 0; j < MT; ++j) {
+      const int q = min(q0 + j * kTokTile + 4 * wave + (lane >> 4), m - 1);
       const int tok = a.rb.sorted_f[off + q] / a.k;
-      tb.off[mt] = static_cast<uint32_t>(tok * row_bytes + g * 16);
+      tb.off[j] = static_cast<uint32_t>(tok * row_bytes + (lane & 15) * 16);
     }
     f32x4 acc[2][MT];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_mfma<DT, 2, MT, kGateUpDepth>(ws, tb, nchunks, lds, acc);
+    stream_wg<DT, 2, MT>(ws, tb, nchunks, lds, bsh, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
-      if (q < m) {
+      if (owner && q < m) {
         float o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -263,24 +278,30 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   }
 }
 
+// Workgroup = (active expert, K split, 4 consecutive pairs of W2 row tiles): wave w owns
+// rows [32*(4*group + w), +32). Waves past the last pair repeat it and store nothing.
 template <int DT, int MT>
 __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
   using S = typename Elem<DT>::S;
   constexpr int R = kDownRows;
   const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
   const int r = lane & 15, g = lane >> 4;
   const int rtiles = a.H / (kRowTile * R);
-  const int per_expert = rtiles * a.splits;
-  const int gw = uniform(blockIdx.x * kExpertWaves + threadIdx.x / kWave);
-  const int ai = gw / per_expert;
-  const int rem = gw - ai * per_expert;
-  const int sp = rem / rtiles;
-  const int rt = rem - sp * rtiles;
+  const int groups = (rtiles + kExpertWaves - 1) / kExpertWaves;
+  const int per_expert = groups * a.splits;
+  const int ai = blockIdx.x / per_expert;  // uniform across the workgroup
+  const int rem = blockIdx.x - ai * per_expert;
+  const int sp = rem / groups;
+  const int tg = rem - sp * groups;
   const int active = uniform(a.rb.hdr[0]);
   const int off = uniform(a.rb.act_off[ai]);
   const int m = uniform(a.rb.act_cnt[ai]);
   const int64_t slot = uniform64(a.rb.act_slot[ai]);
   if (ai >= active) return;
+  const int rtraw = tg * kExpertWaves + wave;
+  const bool owner = rtraw < rtiles;
+  const int rt = owner ? rtraw : rtiles - 1;
   const int H = a.H, I = a.I;
   const int N = a.T * a.k;
   const int64_t row_bytes = static_cast<int64_t>(I) * sizeof(S);
@@ -293,27 +314,28 @@ __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
   ws.row4 = static_cast<uint32_t>(4 * row_bytes);
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
   __shared__ u32x4 lds_all[kExpertWaves][R * kTileSlots];
-  u32x4* lds = lds_all[threadIdx.x / kWave];
+  __shared__ u32x4 bsh[2 * MT * kTileSlots];
+  u32x4* lds = lds_all[wave];
 
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
-    TokenStream<MT> tb;
+    SharedTokens<MT> tb;
     tb.rsrc = make_rsrc(a.act, static_cast<uint32_t>(static_cast<int64_t>(N) * row_bytes));
     tb.base = static_cast<uint32_t>(k0_bytes);
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int q = min(q0 + mt * kTokTile + r, m - 1);
-      tb.off[mt] = static_cast<uint32_t>((off + q) * row_bytes + g * 16);
+    for (int j = 0; j < MT; ++j) {
+      const int q = min(q0 + j * kTokTile + 4 * wave + (lane >> 4), m - 1);
+      tb.off[j] = static_cast<uint32_t>((off + q) * row_bytes + (lane & 15) * 16);
     }
     f32x4 acc[R][MT];
 #pragma unroll
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_mfma<DT, R, MT, kDownDepth>(ws, tb, a.split_steps / kUnroll, lds, acc);
+    stream_wg<DT, R, MT>(ws, tb, a.split_steps / kUnroll, lds, bsh, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
-      if (q < m) {
+      if (owner && q < m) {
         const int f = a.rb.sorted_f[off + q];
         float* dst = a.part + (static_cast<int64_t>(sp) * N + f) * H;
 #pragma unroll
@@ -353,13 +375,11 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineArgs c) {
 template <int DT, int MT>
 static hipError_t launch_stage_t(int stage, const ExpertArgs& a, int max_active, hipStream_t s) {
   if (stage == 0) {
-    const int64_t waves = static_cast<int64_t>(max_active) * (a.I / kRowTile);
-    const unsigned blocks = static_cast<unsigned>((waves + kExpertWaves - 1) / kExpertWaves);
-    gateup_kernel<DT, MT><<<blocks, kExpertThreads, 0, s>>>(a);
+    const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
+    gateup_kernel<DT, MT><<<static_cast<unsigned>(max_active * groups), kExpertThreads, 0, s>>>(a);
   } else {
-    const int64_t waves = static_cast<int64_t>(max_active) * (a.H / (kRowTile * kDownRows)) * a.splits;
-    const unsigned blocks = static_cast<unsigned>((waves + kExpertWaves - 1) / kExpertWaves);
-    down_kernel<DT, MT><<<blocks, kExpertThreads, 0, s>>>(a);
+    const int64_t groups = (a.H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves;
+    down_kernel<DT, MT><<<static_cast<unsigned>(max_active * groups * a.splits), kExpertThreads, 0, s>>>(a);
   }
   return hipGetLastError();
 }
