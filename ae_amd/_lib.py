@@ -34,6 +34,11 @@ SIGNATURES = [
     ("smx_fused_moe_forward", ctypes.c_int,
      [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,
       _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
+    ("smx_moe_shared_workspace_size", _sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
+    ("smx_fused_moe_shared_forward", ctypes.c_int,
+     [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,
+      _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, ctypes.c_float,
+      _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

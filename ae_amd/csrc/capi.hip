@@ -6,6 +6,8 @@
 #include "../../include/specmoe_mi355x.h"
 #include "smx_kernels.h"
 
+#include <cmath>
+
 namespace {
 
 using namespace smx;
@@ -37,7 +39,11 @@ struct Plan {
   int splits = 1;
   int split_steps = 0;
   size_t hdr = 0, act_expert = 0, act_off = 0, act_cnt = 0, act_slot = 0, sorted_f = 0, w = 0, ids = 0;
+  size_t tmask = 0;
   size_t act = 0, part = 0, total = 0;
+  // shared expert (Is > 0)
+  int Is = 0, s_splits = 1, s_split_steps = 0, s_tok_groups = 0, s_gateup_blocks = 0, s_down_blocks = 0;
+  size_t act_s = 0, part_s = 0;
 };
 
 // Shape limits shared by the workspace query and the entry points.
@@ -56,7 +62,28 @@ int check_shape(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype
   return SMX_OK;
 }
 
-Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype) {
+// Largest divisor of n that is <= want (at least 1).
+int64_t divisor_at_most(int64_t n, int64_t want) {
+  int64_t s = 1;
+  for (int64_t d = 1; d <= n && d <= want; ++d)
+    if (n % d == 0) s = d;
+  return s;
+}
+
+// Is = intermediate size of the always-active shared expert, 0 when there is none.
+// Limits of the shared expert's intermediate size (the routed limits on I, plus 32-bit
+// offsets into its page and activations).
+int check_shared(int64_t T, int64_t H, int64_t Is, int dtype) {
+  if (Is < 0) return SMX_ERR_INVALID_ARG;
+  if (Is == 0) return SMX_OK;
+  const int64_t eb = dtype_bytes(dtype);
+  const int64_t chunk = static_cast<int64_t>(kStepBytes) * kUnroll;
+  if ((Is * eb) % chunk != 0 || Is % kRowTile != 0 || Is > (1 << 20)) return SMX_ERR_UNSUPPORTED;
+  if (3 * H * Is * eb >= (int64_t{1} << 32) || T * Is * eb >= (int64_t{1} << 31)) return SMX_ERR_UNSUPPORTED;
+  return SMX_OK;
+}
+
+Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype, int64_t Is = 0) {
   Plan p;
   p.N = static_cast<int>(T * k);
   p.max_active = static_cast<int>(E < p.N ? E : p.N);
@@ -67,11 +94,23 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype)
   const int64_t units = static_cast<int64_t>(p.max_active > 0 ? p.max_active : 1) * (H / (kRowTile * kDownRows));
   int64_t want = (kTargetDownWaves + units - 1) / units;
   if (want < 1) want = 1;
-  int64_t s = 1;
-  for (int64_t d = 1; d <= nchunks && d <= want; ++d)
-    if (nchunks % d == 0) s = d;
+  const int64_t s = divisor_at_most(nchunks, want);
   p.splits = static_cast<int>(s);
   p.split_steps = static_cast<int>(nchunks / s * kUnroll);
+  if (Is > 0) {
+    // The shared expert's down projection is split so that its waves stream about as many
+    // chunks as a routed wave; its token ranges match the kernel's token-tile span.
+    const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+    const int64_t per = nchunks / s;
+    const int64_t ss = divisor_at_most(schunks, (schunks + per - 1) / per);
+    const int64_t span = T < kTokTile * kMaxTokTiles ? T : kTokTile * kMaxTokTiles;
+    p.Is = static_cast<int>(Is);
+    p.s_splits = static_cast<int>(ss);
+    p.s_split_steps = static_cast<int>(schunks / ss * kUnroll);
+    p.s_tok_groups = static_cast<int>((T + span - 1) / span);
+    p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + kExpertWaves - 1) / kExpertWaves));
+    p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves) * ss);
+  }
   size_t o = 0;
   p.hdr = o;        o = align_up(o + 64);
   p.act_expert = o; o = align_up(o + sizeof(int32_t) * E);
@@ -79,10 +118,15 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype)
   p.act_cnt = o;    o = align_up(o + sizeof(int32_t) * E);
   p.act_slot = o;   o = align_up(o + sizeof(int64_t) * E);
   p.sorted_f = o;   o = align_up(o + sizeof(int32_t) * p.N);
+  p.tmask = o;      o = align_up(o + sizeof(int32_t) * T);
   p.w = o;          o = align_up(o + sizeof(float) * p.N);
   p.ids = o;        o = align_up(o + sizeof(int32_t) * p.N);
   p.act = o;        o = align_up(o + static_cast<size_t>(eb) * p.N * I);
   p.part = o;       o = align_up(o + sizeof(float) * static_cast<size_t>(s) * p.N * H);
+  if (Is > 0) {
+    p.act_s = o;    o = align_up(o + static_cast<size_t>(eb) * T * Is);
+    p.part_s = o;   o = align_up(o + sizeof(float) * static_cast<size_t>(p.s_splits) * T * H);
+  }
   p.total = o;
   return p;
 }
@@ -96,14 +140,24 @@ RouteBuffers carve(const Plan& p, void* ws) {
   rb.act_cnt = reinterpret_cast<int32_t*>(b + p.act_cnt);
   rb.sorted_f = reinterpret_cast<int32_t*>(b + p.sorted_f);
   rb.act_slot = reinterpret_cast<int64_t*>(b + p.act_slot);
+  rb.tmask = reinterpret_cast<int32_t*>(b + p.tmask);
   return rb;
 }
 
-// Shared tail of both MoE entry points: expert kernels then combine.
+// The optional block-level terms of smx_fused_moe_shared_forward.
+struct BlockTerms {
+  bool block = false;         // combine in the block form
+  float scale = 1.0f;         // routed scaling factor
+  const void* shared_page = nullptr;
+  const void* sgate = nullptr;
+  int sgate_dtype = kF32;
+};
+
+// Shared tail of the MoE entry points: expert kernels then combine.
 int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t T, int64_t H,
                 int64_t I, int64_t E, int64_t k, const void* pool, int64_t num_slots,
                 int64_t page_elems, const int64_t* e2s, const float* w, const int32_t* ids,
-                void* ws, hipStream_t s) {
+                void* ws, hipStream_t s, const BlockTerms& bt = BlockTerms{}) {
   char* b = static_cast<char*>(ws);
   ExpertArgs a{};
   a.x = hidden;
@@ -119,6 +173,17 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   a.part = reinterpret_cast<float*>(b + p.part);
   a.splits = p.splits;
   a.split_steps = p.split_steps;
+  if (p.Is > 0) {
+    a.sh.page = bt.shared_page;
+    a.sh.I = p.Is;
+    a.sh.act = b + p.act_s;
+    a.sh.part = reinterpret_cast<float*>(b + p.part_s);
+    a.sh.splits = p.s_splits;
+    a.sh.split_steps = p.s_split_steps;
+    a.sh.tok_groups = p.s_tok_groups;
+    a.sh.gateup_blocks = p.s_gateup_blocks;
+    a.sh.down_blocks = p.s_down_blocks;
+  }
   hipError_t err = launch_gateup(dtype, a, p.max_active, p.tok_tiles, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(2, s);
@@ -128,15 +193,18 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   CombineArgs c{};
   c.part = a.part;
   c.w = w;
-  c.ids = ids;
-  c.e2s = e2s;
-  c.num_slots = num_slots;
+  c.tmask = a.rb.tmask;
   c.y = out;
   c.T = static_cast<int>(T);
   c.H = static_cast<int>(H);
   c.k = static_cast<int>(k);
-  c.E = static_cast<int>(E);
   c.splits = p.splits;
+  c.block = bt.block ? 1 : 0;
+  c.scale = bt.scale;
+  c.part_s = p.Is > 0 ? a.sh.part : nullptr;
+  c.splits_s = p.s_splits;
+  c.sgate = bt.sgate;
+  c.sgate_dtype = bt.sgate_dtype;
   err = launch_combine(dtype, c, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(4, s);
@@ -144,11 +212,13 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
 }
 
 int check_pool(const void* hidden, const void* out, const void* pool, int64_t num_slots,
-               int64_t page_elems, const int64_t* e2s, int64_t H, int64_t* I) {
+               int64_t page_elems, const int64_t* e2s, int64_t H, int dtype, int64_t* I) {
   if (!hidden || !out || !pool || !e2s || num_slots <= 0 || page_elems <= 0) return SMX_ERR_INVALID_ARG;
   if (page_elems % (3 * H) != 0) return SMX_ERR_INVALID_ARG;
   *I = page_elems / (3 * H);
-  if (page_elems > (int64_t{1} << 30)) return SMX_ERR_UNSUPPORTED;  // page bytes < 2^32 (32-bit offsets)
+  // 32-bit offsets and sizes within a page
+  if (page_elems > (int64_t{1} << 30) || page_elems * dtype_bytes(dtype) >= (int64_t{1} << 32))
+    return SMX_ERR_UNSUPPORTED;
   if (!aligned16(hidden) || !aligned16(out) || !aligned16(pool)) return SMX_ERR_MISALIGNED;
   return SMX_OK;
 }
@@ -205,7 +275,7 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
   if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype)) return SMX_ERR_INVALID_ARG;
   if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
   int64_t I = 0;
-  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, &I);
+  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, dtype, &I);
   if (rc != SMX_OK) return rc;
   rc = check_shape(T, H, I, E, top_k, dtype);
   if (rc != SMX_OK) return rc;
@@ -223,23 +293,30 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
                      expert_to_slot, topk_weights, topk_ids, workspace, s);
 }
 
-int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
-                          const void* router_logits, int logits_dtype, int64_t E, int64_t top_k,
-                          int renormalize, const void* pool, int64_t num_slots, int64_t page_elems,
-                          const int64_t* expert_to_slot, float* topk_weights_out,
-                          int32_t* topk_ids_out, void* workspace, size_t workspace_bytes,
-                          void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Routing plus expert computation (smx_fused_moe_forward and its block form).
+int fused_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                  const void* router_logits, int logits_dtype, int64_t E, int64_t top_k,
+                  int renormalize, const void* pool, int64_t num_slots, int64_t page_elems,
+                  const int64_t* expert_to_slot, int64_t Is, const BlockTerms& bt,
+                  float* topk_weights_out, int32_t* topk_ids_out, void* workspace,
+                  size_t workspace_bytes, void* stream) {
   if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype) ||
       !valid_dtype(logits_dtype))
     return SMX_ERR_INVALID_ARG;
   if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
   int64_t I = 0;
-  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, &I);
+  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, dtype, &I);
   if (rc != SMX_OK) return rc;
   rc = check_shape(T, H, I, E, top_k, dtype);
   if (rc != SMX_OK) return rc;
+  rc = check_shared(T, H, Is, dtype);
+  if (rc != SMX_OK) return rc;
   if (!router_logits || !workspace) return SMX_ERR_INVALID_ARG;
-  const Plan p = make_plan(T, H, I, E, top_k, dtype);
+  const Plan p = make_plan(T, H, I, E, top_k, dtype, Is);
   if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
   if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
   char* b = static_cast<char*>(workspace);
@@ -253,7 +330,53 @@ int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, i
   if (err != hipSuccess) return static_cast<int>(err);
   mark(1, s);
   return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, w, ids, workspace, s);
+                     expert_to_slot, w, ids, workspace, s, bt);
+}
+
+}  // namespace
+
+extern "C" {
+
+int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                          const void* router_logits, int logits_dtype, int64_t E, int64_t top_k,
+                          int renormalize, const void* pool, int64_t num_slots, int64_t page_elems,
+                          const int64_t* expert_to_slot, float* topk_weights_out,
+                          int32_t* topk_ids_out, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  return fused_forward(hidden, out, dtype, T, H, router_logits, logits_dtype, E, top_k, renormalize,
+                       pool, num_slots, page_elems, expert_to_slot, 0, BlockTerms{}, topk_weights_out,
+                       topk_ids_out, workspace, workspace_bytes, stream);
+}
+
+size_t smx_moe_shared_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
+                                     int64_t shared_I, int dtype) {
+  if (check_shape(T, H, I, E, top_k, dtype) != SMX_OK || check_shared(T, H, shared_I, dtype) != SMX_OK)
+    return 0;
+  return make_plan(T, H, I, E, top_k, dtype, shared_I).total;
+}
+
+int smx_fused_moe_shared_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                                 const void* router_logits, int logits_dtype, int64_t E,
+                                 int64_t top_k, int renormalize, const void* pool,
+                                 int64_t num_slots, int64_t page_elems,
+                                 const int64_t* expert_to_slot, const void* shared_page,
+                                 int64_t shared_I, const void* shared_gate_logits,
+                                 float routed_scaling_factor, float* topk_weights_out,
+                                 int32_t* topk_ids_out, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  if (shared_I < 0 || (shared_I == 0) != (shared_page == nullptr) ||
+      (shared_I == 0 && shared_gate_logits != nullptr) || !std::isfinite(routed_scaling_factor))
+    return SMX_ERR_INVALID_ARG;
+  if (T > 0 && shared_page && !aligned16(shared_page)) return SMX_ERR_MISALIGNED;
+  BlockTerms bt;
+  bt.block = true;
+  bt.scale = routed_scaling_factor;
+  bt.shared_page = shared_page;
+  bt.sgate = shared_gate_logits;
+  bt.sgate_dtype = logits_dtype;
+  return fused_forward(hidden, out, dtype, T, H, router_logits, logits_dtype, E, top_k, renormalize,
+                       pool, num_slots, page_elems, expert_to_slot, shared_I, bt, topk_weights_out,
+                       topk_ids_out, workspace, workspace_bytes, stream);
 }
 
 int smx_set_profile_events(void* const* events, int count) {

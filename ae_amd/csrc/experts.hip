@@ -11,7 +11,8 @@
 //                   act = round(silu(round(gate)) * round(up)) into `act` (row = sorted pos).
 //   down_kernel     wave = (active expert, 32 rows of W2, K split): streams W2 over its K
 //                   slice of I and writes fp32 partials part[split][f][h].
-//   combine_kernel  y[t] = round(sum_j round(w[t,j] * sum_split part[split][t*k+j])).
+//   combine_kernel  y[t] = round(sum_j round(w[t,j] * sum_split part[split][t*k+j])), one wave
+//                   per assignment of a token (and one for the shared expert's partials).
 //
 // Arithmetic and rounding points follow stack_fused_moe
 // (specmoe/layers/fused_moe_kernel.py:319-349): C1 rounded to the activation dtype (:203),
@@ -207,44 +208,73 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
   return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-// Workgroup = (active expert, 4 consecutive weight tiles): wave w owns tile 4*group + w. A
-// wave past the expert's last tile streams the last tile again and stores nothing, so every
-// wave of a workgroup runs the same chunks and barriers.
+// The work item of one workgroup: an expert page and a list of m token rows starting at
+// position `off` (routed: sorted positions, token = sorted_f / k; shared expert: token rows
+// off.. directly). `tg` is the workgroup's index among the item's workgroups.
+struct WorkItem {
+  const char* page;
+  int64_t page_bytes;
+  int I;
+  int off, m, tg;
+  bool shared;
+};
+
+// Leading `sh.*_blocks` workgroups run the shared expert (v = token range, then tg);
+// the rest run routed experts (ai = active-expert index, then tg). Returns false for a
+// workgroup whose routed expert is not active in this batch.
+template <typename S>
+__device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
+                                          WorkItem& w) {
+  const int64_t elem = static_cast<int64_t>(sizeof(S));
+  const int b = blockIdx.x;
+  if (b < shared_blocks) {
+    const int v = b / per_item;
+    const int span = a.T < kTokTile * kMaxTokTiles ? a.T : kTokTile * kMaxTokTiles;
+    w.page = static_cast<const char*>(a.sh.page);
+    w.page_bytes = 3 * static_cast<int64_t>(a.H) * a.sh.I * elem;
+    w.I = a.sh.I;
+    w.off = v * span;
+    w.m = min(span, a.T - w.off);
+    w.tg = b - v * per_item;
+    w.shared = true;
+    return true;
+  }
+  const int rb = b - shared_blocks;
+  const int ai = rb / per_item;  // uniform across the workgroup
+  // ai < max_active <= E, so the per-expert arrays may be read before the active count is
+  // known (the loads then share one latency); values past the active count are unused.
+  const int active = uniform(a.rb.hdr[0]);
+  w.off = uniform(a.rb.act_off[ai]);
+  w.m = uniform(a.rb.act_cnt[ai]);
+  const int64_t slot = uniform64(a.rb.act_slot[ai]);
+  w.page_bytes = a.page_elems * elem;
+  w.page = static_cast<const char*>(a.pool) + slot * w.page_bytes;
+  w.I = a.I;
+  w.tg = rb - ai * per_item;
+  w.shared = false;
+  return ai < active;
+}
+
+// The token passes of one gate/up workgroup with MT token tiles per pass: wave `wave` owns
+// weight-row tile p (gate rows [16p, 16p+16) and the matching up rows); `owner` is false for
+// a wave past the expert's last tile (it streams tile p again and stores nothing).
 template <int DT, int MT>
-__global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
+__device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkItem& it, int p,
+                                              bool owner, u32x4* lds, u32x4* bsh) {
   using S = typename Elem<DT>::S;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int tiles = a.I / kRowTile;
-  const int groups = (tiles + kExpertWaves - 1) / kExpertWaves;
-  const int ai = blockIdx.x / groups;  // uniform across the workgroup
-  const int tg = blockIdx.x - ai * groups;
-  // ai < max_active <= E, so the per-expert arrays may be read before the active count is
-  // known (the loads then share one latency); values past the active count are unused.
-  const int active = uniform(a.rb.hdr[0]);
-  const int off = uniform(a.rb.act_off[ai]);
-  const int m = uniform(a.rb.act_cnt[ai]);
-  const int64_t slot = uniform64(a.rb.act_slot[ai]);
-  if (ai >= active) return;
-  const int praw = tg * kExpertWaves + wave;
-  const bool owner = praw < tiles;
-  const int p = owner ? praw : tiles - 1;
-  const int H = a.H, I = a.I;
+  const int H = a.H, I = it.I, off = it.off, m = it.m;
   const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
-  const int64_t page_bytes = a.page_elems * static_cast<int64_t>(sizeof(S));
   WeightStream ws;  // tile 0: gate rows [16p, 16p+16); tile 1: the matching up rows
-  ws.rsrc = make_rsrc(static_cast<const char*>(a.pool) + slot * page_bytes, static_cast<uint32_t>(page_bytes));
+  ws.rsrc = make_rsrc(it.page, static_cast<uint32_t>(it.page_bytes));
   ws.base = static_cast<uint32_t>(kRowTile * p * row_bytes);
   ws.tile_stride = static_cast<uint32_t>(I * row_bytes);
   ws.row4 = static_cast<uint32_t>(4 * row_bytes);
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
   const int nchunks = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
-  __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
-  __shared__ u32x4 bsh[2 * MT * kTileSlots];
-  u32x4* lds = lds_all[wave];
-  S* act = static_cast<S*>(a.act);
-
+  S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     SharedTokens<MT> tb;
     tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
@@ -252,7 +282,7 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       const int q = min(q0 + j * kTokTile + 4 * wave + (lane >> 4), m - 1);
-      const int tok = a.rb.sorted_f[off + q] / a.k;
+      const int tok = it.shared ? off + q : a.rb.sorted_f[off + q] / a.k;
       tb.off[j] = static_cast<uint32_t>(tok * row_bytes + (lane & 15) * 16);
     }
     f32x4 acc[2][MT];
@@ -278,48 +308,58 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   }
 }
 
-// Workgroup = (active expert, K split, 4 consecutive pairs of W2 row tiles): wave w owns
-// rows [32*(4*group + w), +32). Waves past the last pair repeat it and store nothing.
+// Workgroup = (work item, 4 consecutive weight tiles): wave w owns tile 4*tg + w. A wave
+// past the expert's last tile streams the last tile again and stores nothing, so every
+// wave of a workgroup runs the same chunks and barriers. The token tiles per pass follow
+// the item's token count (up to MT): an expert with few tokens streams its weights with
+// one tile of 16 tokens.
 template <int DT, int MT>
-__global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
+__global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
+  const int wave = threadIdx.x / kWave;
+  const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
+  const int Iw = in_shared ? a.sh.I : a.I;
+  const int tiles = Iw / kRowTile;
+  const int groups = (tiles + kExpertWaves - 1) / kExpertWaves;
+  WorkItem it;
+  if (!work_item<typename Elem<DT>::S>(a, a.sh.gateup_blocks, groups, it)) return;
+  const int praw = it.tg * kExpertWaves + wave;
+  const bool owner = praw < tiles;
+  const int p = owner ? praw : tiles - 1;
+  __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
+  __shared__ u32x4 bsh[2 * MT * kTileSlots];
+  u32x4* lds = lds_all[wave];
+  if (MT == 1 || it.m <= kTokTile) gateup_passes<DT, 1>(a, it, p, owner, lds, bsh);
+  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<DT, (MT >= 2 ? 2 : 1)>(a, it, p, owner, lds, bsh);
+  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<DT, (MT >= 3 ? 3 : 1)>(a, it, p, owner, lds, bsh);
+  else gateup_passes<DT, MT>(a, it, p, owner, lds, bsh);
+}
+
+// The token passes of one down workgroup with MT token tiles per pass: wave `wave` owns W2
+// rows [32*rt, 32*rt + 32) over the K slice of split sp.
+template <int DT, int MT>
+__device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem& it, int rt,
+                                            bool owner, int sp, int split_steps, u32x4* lds,
+                                            u32x4* bsh) {
   using S = typename Elem<DT>::S;
   constexpr int R = kDownRows;
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
   const int r = lane & 15, g = lane >> 4;
-  const int rtiles = a.H / (kRowTile * R);
-  const int groups = (rtiles + kExpertWaves - 1) / kExpertWaves;
-  const int per_expert = groups * a.splits;
-  const int ai = blockIdx.x / per_expert;  // uniform across the workgroup
-  const int rem = blockIdx.x - ai * per_expert;
-  const int sp = rem / groups;
-  const int tg = rem - sp * groups;
-  const int active = uniform(a.rb.hdr[0]);
-  const int off = uniform(a.rb.act_off[ai]);
-  const int m = uniform(a.rb.act_cnt[ai]);
-  const int64_t slot = uniform64(a.rb.act_slot[ai]);
-  if (ai >= active) return;
-  const int rtraw = tg * kExpertWaves + wave;
-  const bool owner = rtraw < rtiles;
-  const int rt = owner ? rtraw : rtiles - 1;
-  const int H = a.H, I = a.I;
-  const int N = a.T * a.k;
+  const int H = a.H, I = it.I, off = it.off, m = it.m;
+  const int rows = it.shared ? a.T : a.T * a.k;  // rows of act and of one split of part
   const int64_t row_bytes = static_cast<int64_t>(I) * sizeof(S);
-  const int64_t k0_bytes = static_cast<int64_t>(sp) * a.split_steps * kStepBytes;
-  const int64_t page_bytes = a.page_elems * static_cast<int64_t>(sizeof(S));
+  const int64_t k0_bytes = static_cast<int64_t>(sp) * split_steps * kStepBytes;
   WeightStream ws;  // tiles: rows [(rt*R + i)*16, +16) of W2 (after W1, W3), this split's K slice
-  ws.rsrc = make_rsrc(static_cast<const char*>(a.pool) + slot * page_bytes, static_cast<uint32_t>(page_bytes));
+  ws.rsrc = make_rsrc(it.page, static_cast<uint32_t>(it.page_bytes));
   ws.base = static_cast<uint32_t>(2 * H * row_bytes + rt * R * kRowTile * row_bytes + k0_bytes);
   ws.tile_stride = static_cast<uint32_t>(kRowTile * row_bytes);
   ws.row4 = static_cast<uint32_t>(4 * row_bytes);
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
-  __shared__ u32x4 lds_all[kExpertWaves][R * kTileSlots];
-  __shared__ u32x4 bsh[2 * MT * kTileSlots];
-  u32x4* lds = lds_all[wave];
-
+  const void* act = it.shared ? a.sh.act : a.act;
+  float* part = it.shared ? a.sh.part : a.part;
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     SharedTokens<MT> tb;
-    tb.rsrc = make_rsrc(a.act, static_cast<uint32_t>(static_cast<int64_t>(N) * row_bytes));
+    tb.rsrc = make_rsrc(act, static_cast<uint32_t>(static_cast<int64_t>(rows) * row_bytes));
     tb.base = static_cast<uint32_t>(k0_bytes);
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
@@ -331,13 +371,13 @@ __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<DT, R, MT>(ws, tb, a.split_steps / kUnroll, lds, bsh, acc);
+    stream_wg<DT, R, MT>(ws, tb, split_steps / kUnroll, lds, bsh, acc);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
       if (owner && q < m) {
-        const int f = a.rb.sorted_f[off + q];
-        float* dst = a.part + (static_cast<int64_t>(sp) * N + f) * H;
+        const int f = it.shared ? off + q : a.rb.sorted_f[off + q];
+        float* dst = part + (static_cast<int64_t>(sp) * rows + f) * H;
 #pragma unroll
         for (int i = 0; i < R; ++i)
           *reinterpret_cast<f32x4*>(dst + (rt * R + i) * kRowTile + 4 * g) = acc[i][mt];
@@ -346,28 +386,120 @@ __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
   }
 }
 
-// One thread per 4 output elements.
-template <int DT>
-__global__ __launch_bounds__(256) void combine_kernel(CombineArgs c) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int hq = c.H / 4;
-  if (idx >= static_cast<int64_t>(c.T) * hq) return;
-  const int t = static_cast<int>(idx / hq);
-  const int h = static_cast<int>(idx - static_cast<int64_t>(t) * hq) * 4;
-  const int N = c.T * c.k;
-  f32x4 y = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < c.k; ++j) {
-    const int f = t * c.k + j;
-    const int e = c.ids[f];
-    if (e < 0 || e >= c.E) continue;
-    const int64_t slot = c.e2s[e];
-    if (slot < 0 || slot >= c.num_slots) continue;
-    f32x4 v = *reinterpret_cast<const f32x4*>(c.part + static_cast<int64_t>(f) * c.H + h);
-    for (int s = 1; s < c.splits; ++s)
-      v += *reinterpret_cast<const f32x4*>(c.part + (static_cast<int64_t>(s) * N + f) * c.H + h);
-    const float wf = c.w[f];
+// Workgroup = (work item, K split, 4 consecutive pairs of W2 row tiles): wave w owns rows
+// [32*(4*group + w), +32). Waves past the last pair repeat it and store nothing. Token tiles
+// per pass as in gateup_kernel.
+template <int DT, int MT>
+__global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
+  const int wave = threadIdx.x / kWave;
+  const int rtiles = a.H / (kRowTile * kDownRows);
+  const int groups = (rtiles + kExpertWaves - 1) / kExpertWaves;
+  const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.down_blocks;
+  const int splits = in_shared ? a.sh.splits : a.splits;
+  const int split_steps = in_shared ? a.sh.split_steps : a.split_steps;
+  WorkItem it;
+  if (!work_item<typename Elem<DT>::S>(a, a.sh.down_blocks, groups * splits, it)) return;
+  const int sp = it.tg / groups;
+  const int tg = it.tg - sp * groups;
+  const int rtraw = tg * kExpertWaves + wave;
+  const bool owner = rtraw < rtiles;
+  const int rt = owner ? rtraw : rtiles - 1;
+  __shared__ u32x4 lds_all[kExpertWaves][kDownRows * kTileSlots];
+  __shared__ u32x4 bsh[2 * MT * kTileSlots];
+  u32x4* lds = lds_all[wave];
+  if (MT == 1 || it.m <= kTokTile) down_passes<DT, 1>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else if (MT == 2 || it.m <= 2 * kTokTile) down_passes<DT, (MT >= 2 ? 2 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else if (MT == 3 || it.m <= 3 * kTokTile) down_passes<DT, (MT >= 3 ? 3 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else down_passes<DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
+}
+
+__device__ __forceinline__ float load_scalar(const void* base, int dtype, int64_t i) {
+  switch (dtype) {
+    case kF32: return load_as_f32<kF32>(base, i);
+    case kF16: return load_as_f32<kF16>(base, i);
+    default: return load_as_f32<kBF16>(base, i);
+  }
+}
+
+constexpr int kCombineBatch = 8;        // split loads in flight per lane
+constexpr int kCombineMaxWaves = 16;
+
+// Sum over the splits of one partial row segment (4 outputs per lane), in split order.
+__device__ __forceinline__ f32x4 split_sum(const float* src, int64_t split_stride, int splits) {
+  f32x4 v = {0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < splits; s0 += kCombineBatch) {
+    f32x4 a[kCombineBatch];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) y[i] += Elem<DT>::round(v[i] * wf);
+    for (int u = 0; u < kCombineBatch; ++u)
+      a[u] = s0 + u < splits ? *reinterpret_cast<const f32x4*>(src + (s0 + u) * split_stride)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u)
+      if (s0 + u < splits) v += a[u];
+  }
+  return v;
+}
+
+// Workgroup = (token t, 256 consecutive outputs: lane l owns outputs 4l..4l+3 of the chunk).
+// Work item i < k is assignment t*k + i: its splits are summed in split order and the term
+// round(w * sum) goes to LDS; item k (block form with a shared expert) is the shared
+// expert's split sum. Wave w takes items w, w + waves, ... Wave 0 then adds the k terms in
+// j order (y = round(sum_j term_j), deterministic) and applies the block form
+// y = round(round(round(y) * scale) + s * round(shared)) with s = 1 or
+// round(sigmoid(gate logit)) and the product rounded, as the unfused block computes it.
+template <int DT>
+__global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(CombineArgs c) {
+  __shared__ f32x4 terms[kMaxTopK + 1][kWave];
+  const int lane = lane_id();
+  const int wave = threadIdx.x / kWave;
+  const int waves = blockDim.x / kWave;
+  const int chunks = (c.H + 4 * kWave - 1) / (4 * kWave);
+  const int t = blockIdx.x / chunks;
+  const int h = ((blockIdx.x - t * chunks) * kWave + lane) * 4;
+  const bool live = h < c.H;
+  const uint32_t vm = static_cast<uint32_t>(c.tmask[t]);
+  const int items = c.k + (c.part_s != nullptr ? 1 : 0);
+  for (int i = wave; i < items; i += waves) {
+    f32x4 term = {0.f, 0.f, 0.f, 0.f};
+    if (i < c.k) {
+      if (live && ((vm >> i) & 1u)) {
+        const int64_t f = static_cast<int64_t>(t) * c.k + i;
+        const f32x4 v = split_sum(c.part + f * c.H + h, static_cast<int64_t>(c.T) * c.k * c.H, c.splits);
+        const float wf = c.w[f];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) term[e] = Elem<DT>::round(v[e] * wf);
+      }
+    } else if (live) {
+      term = split_sum(c.part_s + static_cast<int64_t>(t) * c.H + h, static_cast<int64_t>(c.T) * c.H, c.splits_s);
+    }
+    terms[i][lane] = term;
+  }
+  __syncthreads();
+  if (wave != 0 || !live) return;
+  f32x4 y = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < c.k; ++j)
+    if ((vm >> j) & 1u) y += terms[j][lane];
+  if (c.block) {
+    const bool scaled = c.scale != 1.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y[e] = Elem<DT>::round(y[e]);
+      if (scaled) y[e] = Elem<DT>::round(y[e] * c.scale);
+    }
+    if (c.part_s) {
+      const f32x4 d = terms[c.k][lane];
+      float gs = 1.0f;
+      if (c.sgate) {
+        const float z = load_scalar(c.sgate, c.sgate_dtype, t);
+        gs = Elem<DT>::round(1.0f / (1.0f + __expf(-z)));
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float sh = Elem<DT>::round(d[e]);
+        if (c.sgate) sh = Elem<DT>::round(gs * sh);
+        y[e] += sh;
+      }
+    }
   }
   store4<DT>(c.y, static_cast<int64_t>(t) * c.H + h, y[0], y[1], y[2], y[3]);
 }
@@ -376,10 +508,12 @@ template <int DT, int MT>
 static hipError_t launch_stage_t(int stage, const ExpertArgs& a, int max_active, hipStream_t s) {
   if (stage == 0) {
     const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
-    gateup_kernel<DT, MT><<<static_cast<unsigned>(max_active * groups), kExpertThreads, 0, s>>>(a);
+    const int64_t blocks = a.sh.gateup_blocks + max_active * groups;
+    gateup_kernel<DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   } else {
     const int64_t groups = (a.H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves;
-    down_kernel<DT, MT><<<static_cast<unsigned>(max_active * groups * a.splits), kExpertThreads, 0, s>>>(a);
+    const int64_t blocks = a.sh.down_blocks + max_active * groups * a.splits;
+    down_kernel<DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   }
   return hipGetLastError();
 }
@@ -413,12 +547,14 @@ hipError_t launch_down(int dtype, const ExpertArgs& a, int max_active, int tok_t
 }
 
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s) {
-  const int64_t threads = static_cast<int64_t>(c.T) * (c.H / 4);
-  const unsigned blocks = static_cast<unsigned>((threads + 255) / 256);
+  const int chunks = (c.H + 4 * kWave - 1) / (4 * kWave);
+  const unsigned blocks = static_cast<unsigned>(static_cast<int64_t>(c.T) * chunks);
+  const int items = c.k + (c.part_s != nullptr ? 1 : 0);
+  const int threads = (items < kCombineMaxWaves ? items : kCombineMaxWaves) * kWave;
   switch (dtype) {
-    case kF32: combine_kernel<kF32><<<blocks, 256, 0, s>>>(c); break;
-    case kF16: combine_kernel<kF16><<<blocks, 256, 0, s>>>(c); break;
-    default: combine_kernel<kBF16><<<blocks, 256, 0, s>>>(c); break;
+    case kF32: combine_kernel<kF32><<<blocks, threads, 0, s>>>(c); break;
+    case kF16: combine_kernel<kF16><<<blocks, threads, 0, s>>>(c); break;
+    default: combine_kernel<kBF16><<<blocks, threads, 0, s>>>(c); break;
   }
   return hipGetLastError();
 }

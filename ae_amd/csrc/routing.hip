@@ -2,160 +2,320 @@
 //
 // topk_softmax_kernel     G lanes per token (G = next power of two >= E, at least 8; a wave
 //                         holds 64/G tokens; for E > 64 a lane holds up to 4 experts).
-// align_kernel            one workgroup: per-wave histograms built from ballot/popcount,
-//                         a wave-level scan in LDS, then a stable scatter; emits either the
-//                         compact per-expert lists the expert kernels consume or the
-//                         reference's block-padded (sorted_ids, expert_ids, ntp) format.
-// route_kernel            both of the above fused in one launch (one workgroup).
+// align_kernel            one workgroup: per-wave histograms (lanes sharing an expert found
+//                         by ballots over the id bits), a wave-level scan in LDS, then a
+//                         stable scatter; emits either the compact per-expert lists the
+//                         expert kernels consume or the reference's block-padded
+//                         (sorted_ids, expert_ids, ntp) format.
+// route_kernel            both of the above fused in one launch (one workgroup of 4-16
+//                         waves, sized to the batch).
 #include "smx_kernels.h"
 
 namespace smx {
 
 // ---------------------------------------------------------------------------------------
 // Top-k softmax, G lanes per token (G = 8, 16, 32 or 64; a wave holds 64/G tokens). Lane j of
-// a group holds expert j (and j + 64*i for G = 64, up to 256 experts). On return lane j < k of
-// each group holds the j-th pick (descending probability, ties to the lower expert index).
-// The arithmetic (max, exp_nonpos, per-lane sequential sum, xor butterfly over the group,
-// p = ex * (1/sum), renormalisation by division with the sum taken in j order) equals the
-// oracle's 64-lane tree bit for bit: with E <= G every lane at or past G holds an exact zero,
-// so the butterfly steps at offsets >= G only add zeros. Semantics follow select_experts as
-// called at specmoe/layers/FusedMoE.py:174-185.
+// a group holds experts j + G*i, i < PL (PL = 4 only for G = 64: up to 256 experts). On
+// return lane j < k of each group holds the j-th pick (descending probability, ties to the
+// lower expert index). The arithmetic (max, exp_nonpos, per-lane sequential sum, butterfly
+// over the group with offsets 1, 2, ..., G/2, p = ex * (1/sum), renormalisation by division
+// with the sum taken in j order) equals the oracle's 64-lane butterfly bit for bit: with
+// E <= G every lane at or past G holds an exact zero, so the oracle's steps at offsets >= G
+// only add zeros.
+// Semantics follow select_experts as called at specmoe/layers/FusedMoE.py:174-185.
+//
+// NB wave-passes (NB groups of tokens) are computed in lockstep: every butterfly step is
+// issued for all NB before the next, so the NB independent shuffle chains hide each
+// other's latency.
 // ---------------------------------------------------------------------------------------
-template <int G>
+template <int G, int PL>
 struct TopkGroup {
-  static constexpr int kPerLane = (G == kWave) ? kMaxExpertsPerLane : 1;  // experts per lane
-  static constexpr int kTokens = kWave / G;                               // tokens per wave
+  static_assert(PL == 1 || G == kWave, "several experts per lane only with whole-wave groups");
+  static constexpr int kTokens = kWave / G;  // tokens per wave-pass
 };
 
-template <int LDT, int G>
-__device__ __forceinline__ void load_logits(const void* logits, int t, int T, int E,
-                                            float (&v)[TopkGroup<G>::kPerLane]) {
+// Lane j of a group reads experts j + G*i of token t. Experts past E read -inf (never
+// selected); a token past T reads zeros so that its arithmetic stays finite (its results
+// are discarded).
+template <int LDT, int G, int PL>
+__device__ __forceinline__ void load_logits(const void* logits, int t, int T, int E, float (&v)[PL]) {
   const int j = lane_id() % G;
 #pragma unroll
-  for (int i = 0; i < TopkGroup<G>::kPerLane; ++i) {
+  for (int i = 0; i < PL; ++i) {
     const int e = j + G * i;
-    v[i] = (t < T && e < E) ? load_as_f32<LDT>(logits, static_cast<int64_t>(t) * E + e) : -__builtin_inff();
+    v[i] = e >= E ? -__builtin_inff()
+                  : (t < T ? load_as_f32<LDT>(logits, static_cast<int64_t>(t) * E + e) : 0.0f);
   }
 }
 
+// Cross-lane exchange within rows of 16 lanes by DPP (a VALU operand modifier, no LDS
+// round trip). Controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (lane i <-> 7 - i within 8), row_mirror (lane i <-> 15 - i within 16).
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float readlane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// op-reduction over the G lanes of each group; every lane of the group gets the result.
+// The steps pair lane i with i^1, i^2, then (on values already equal across each quad,
+// resp. half-row) with the mirrored lane, which holds the same value as lane i^4 (resp.
+// i^8); rows are combined as op(op(r0, r1), op(r2, r3)) from lanes 0, 16, 32, 48. For a
+// commutative op every intermediate value equals that of the xor butterfly over offsets
+// 1, 2, 4, ..., G/2 (for fp32 addition bit for bit: a + b == b + a exactly).
+template <int G, typename Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+  v = op(v, dpp<kDppXor1>(v));
+  v = op(v, dpp<kDppXor2>(v));
+  v = op(v, dpp<kDppHalfMirror>(v));
+  if constexpr (G >= 16) v = op(v, dpp<kDppMirror>(v));
+  if constexpr (G >= 32) {
+    const float r0 = readlane(v, 0), r1 = readlane(v, 16), r2 = readlane(v, 32), r3 = readlane(v, 48);
+    if constexpr (G == 32) v = lane_id() < 32 ? op(r0, r1) : op(r2, r3);
+    else v = op(op(r0, r1), op(r2, r3));
+  }
+  return v;
+}
+
+// (p, e) pair order: larger p first, ties to the lower expert index.
+__device__ __forceinline__ bool better(float op, int oe, float bp, int be) {
+  return op > bp || (op == bp && oe < be);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& bp, int& be) {
+  const float op = dpp<CTRL>(bp);
+  const int oe = dpp<CTRL>(be);
+  if (better(op, oe, bp, be)) { bp = op; be = oe; }
+}
+
+// Arg-max over the G lanes of each group, the same reduction shape as group_reduce.
 template <int G>
-__device__ __forceinline__ void group_topk_softmax(float (&p)[TopkGroup<G>::kPerLane], int E, int k,
-                                                   bool renorm, float& w_out, int& id_out) {
+__device__ __forceinline__ void group_argmax(float& bp, int& be) {
+  argmax_step<kDppXor1>(bp, be);
+  argmax_step<kDppXor2>(bp, be);
+  argmax_step<kDppHalfMirror>(bp, be);
+  if constexpr (G >= 16) argmax_step<kDppMirror>(bp, be);
+  if constexpr (G >= 32) {
+    float p[4];
+    int e[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = readlane(bp, 16 * r);
+      e[r] = __builtin_amdgcn_readlane(be, 16 * r);
+    }
+    if (better(p[1], e[1], p[0], e[0])) { p[0] = p[1]; e[0] = e[1]; }
+    if (better(p[3], e[3], p[2], e[2])) { p[2] = p[3]; e[2] = e[3]; }
+    if constexpr (G == 32) {
+      const bool hi = lane_id() >= 32;
+      bp = hi ? p[2] : p[0];
+      be = hi ? e[2] : e[0];
+    } else {
+      if (better(p[2], e[2], p[0], e[0])) { p[0] = p[2]; e[0] = e[2]; }
+      bp = p[0];
+      be = e[0];
+    }
+  }
+}
+
+template <int G, int PL, int NB>
+__device__ __forceinline__ void group_topk_softmax(float (&p)[NB][PL], int E, int k, bool renorm,
+                                                   float (&w_out)[NB], int (&id_out)[NB]) {
 #pragma clang fp contract(off)
-  constexpr int PL = TopkGroup<G>::kPerLane;
   const int lane = lane_id();
   const int j = lane % G;
   const int base = lane - j;
-  float m = -__builtin_inff();
+  float m[NB], s[NB];
 #pragma unroll
-  for (int i = 0; i < PL; ++i) m = fmaxf(m, p[i]);
+  for (int b = 0; b < NB; ++b) {
+    m[b] = -__builtin_inff();
 #pragma unroll
-  for (int off = G / 2; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, kWave));
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int e = j + G * i;
-    p[i] = (e < E) ? exp_nonpos(p[i] - m) : 0.0f;
-    s = (i == 0) ? p[i] : s + p[i];
+    for (int i = 0; i < PL; ++i) m[b] = fmaxf(m[b], p[b][i]);
+    m[b] = group_reduce<G>(m[b], [](float a, float c) { return fmaxf(a, c); });
   }
 #pragma unroll
-  for (int off = G / 2; off >= 1; off >>= 1) s = s + __shfl_xor(s, off, kWave);
-  const float inv = 1.0f / s;
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int e = j + G * i;
-    p[i] = (e < E) ? p[i] * inv : -1.0f;  // -1 marks "not selectable"
-  }
-  w_out = 0.0f;
-  id_out = -1;
-  for (int jj = 0; jj < k; ++jj) {
-    float bp = -2.0f;
-    int be = 0x7fffffff;
+  for (int b = 0; b < NB; ++b) {
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
-      if (p[i] > bp) { bp = p[i]; be = j + G * i; }  // ascending e: strict > keeps lowest
+      const int e = j + G * i;
+      p[b][i] = (e < E) ? exp_nonpos(p[b][i] - m[b]) : 0.0f;
+      s[b] = (i == 0) ? p[b][i] : s[b] + p[b][i];
     }
+    s[b] = group_reduce<G>(s[b], [](float a, float c) { return a + c; });
+  }
 #pragma unroll
-    for (int off = G / 2; off >= 1; off >>= 1) {
-      const float op = __shfl_xor(bp, off, kWave);
-      const int oe = __shfl_xor(be, off, kWave);
-      if (op > bp || (op == bp && oe < be)) { bp = op; be = oe; }
+  for (int b = 0; b < NB; ++b) {
+    const float inv = 1.0f / s[b];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int e = j + G * i;
+      p[b][i] = (e < E) ? p[b][i] * inv : -1.0f;  // -1 marks "not selectable"
     }
-    if (j == be % G) {
+    w_out[b] = 0.0f;
+    id_out[b] = -1;
+  }
+  for (int jj = 0; jj < k; ++jj) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float bp = -2.0f;
+      int be = 0x7fffffff;
 #pragma unroll
       for (int i = 0; i < PL; ++i)
-        if (i == be / G) p[i] = -1.0f;
+        if (p[b][i] > bp) { bp = p[b][i]; be = j + G * i; }  // ascending e: strict > keeps lowest
+      group_argmax<G>(bp, be);
+      if (j == be % G) {
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+          if (i == be / G) p[b][i] = -1.0f;
+      }
+      if (j == jj) { w_out[b] = bp; id_out[b] = be; }
     }
-    if (j == jj) { w_out = bp; id_out = be; }
   }
   if (renorm) {
-    float sum = 0.0f;
-    for (int jj = 0; jj < k; ++jj) {
-      const float v = __shfl(w_out, base + jj, kWave);
-      sum = (jj == 0) ? v : sum + v;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float sum = 0.0f;
+      for (int jj = 0; jj < k; ++jj) {
+        const float v = (G == kWave) ? readlane(w_out[b], jj) : __shfl(w_out[b], base + jj, kWave);
+        sum = (jj == 0) ? v : sum + v;
+      }
+      if (j < k) w_out[b] = w_out[b] / sum;
     }
-    if (j < k) w_out = w_out / sum;
   }
 }
 
-// The tokens of `passes` consecutive wave-passes: token t = (pass0 + b) * stride + slot, where
-// slot = lane / G. All logit loads are issued before any token is computed, so a wave pays
-// one load latency per batch. fn(t, w, id) is called on every lane (t may be >= T).
-template <int LDT, int G, typename Fn>
+// Top-k by ranking, for one expert per lane (E <= 64). The softmax is as above; then lane j
+// of a group forms the exact 64-bit key (bits(p) << 8) | (255 - j) -- p >= 0, so larger keys
+// mean larger p, ties to the lower expert index -- and its rank is the number of larger keys
+// in its group, read back from the wave's LDS slice (independent compares instead of k
+// dependent arg-max rounds). Lane j with rank r < k is the r-th pick: slot_out = r (else -1).
+// Renormalisation divides by the picks' sum taken in rank order.
+struct RankScratch {
+  uint64_t key[kTokBatch][kWave];
+  float pick[kTokBatch][kWave];
+};
+
+template <int G, int NB>
+__device__ __forceinline__ void group_topk_rank(float (&p)[NB][1], int E, int k, bool renorm,
+                                                RankScratch& rs, float (&w_out)[NB],
+                                                int (&id_out)[NB], int (&slot_out)[NB]) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  const int j = lane % G;
+  const int base = lane - j;
+  const bool valid = j < E;
+  uint64_t key[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float m = group_reduce<G>(p[b][0], [](float a, float c) { return fmaxf(a, c); });
+    const float ex = valid ? exp_nonpos(p[b][0] - m) : 0.0f;
+    const float s = group_reduce<G>(ex, [](float a, float c) { return a + c; });
+    p[b][0] = ex * (1.0f / s);
+    key[b] = valid ? ((static_cast<uint64_t>(__float_as_uint(p[b][0])) << 8) | static_cast<uint64_t>(255 - j)) : 0ull;
+    rs.key[b][lane] = key[b];
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    int rank = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) rank += rs.key[b][base + g] > key[b] ? 1 : 0;
+    slot_out[b] = (valid && rank < k) ? rank : -1;
+    w_out[b] = p[b][0];
+    id_out[b] = j;
+  }
+  if (renorm) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      if (slot_out[b] >= 0) rs.pick[b][base + slot_out[b]] = w_out[b];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float sum = rs.pick[b][base];
+      for (int r = 1; r < k; ++r) sum = sum + rs.pick[b][base + r];
+      w_out[b] = w_out[b] / sum;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();  // the slice is reused by the next batch
+}
+
+// The tokens of kTokBatch consecutive wave-passes: token t = first + b * stride for this
+// lane's group. All logit loads are issued before any token is computed, so a wave pays one
+// load latency per batch. fn(t, w, id) is called on every lane (t may be >= T).
+// fn(t, slot, w, id) is called for every pick of token t (t < T): slot in [0, k).
+template <int LDT, int G, int PL, typename Fn>
 __device__ __forceinline__ void topk_batch(const void* logits, int T, int E, int k, bool renorm,
-                                           int first, int stride, Fn&& fn) {
-  constexpr int PL = TopkGroup<G>::kPerLane;
+                                           int first, int stride, RankScratch& rs, Fn&& fn) {
   float v[kTokBatch][PL];
 #pragma unroll
-  for (int b = 0; b < kTokBatch; ++b) load_logits<LDT, G>(logits, first + b * stride, T, E, v[b]);
+  for (int b = 0; b < kTokBatch; ++b) load_logits<LDT, G, PL>(logits, first + b * stride, T, E, v[b]);
+  float w[kTokBatch];
+  int id[kTokBatch];
+  int slot[kTokBatch];
+  if constexpr (PL == 1) {
+    group_topk_rank<G, kTokBatch>(v, E, k, renorm, rs, w, id, slot);
+  } else {
+    group_topk_softmax<G, PL, kTokBatch>(v, E, k, renorm, w, id);
+    const int j = lane_id() % G;
+#pragma unroll
+    for (int b = 0; b < kTokBatch; ++b) slot[b] = j < k ? j : -1;
+  }
 #pragma unroll
   for (int b = 0; b < kTokBatch; ++b) {
-    if (first + b * stride - lane_id() / G < T) {  // some token of this wave-pass exists
-      float w;
-      int id;
-      group_topk_softmax<G>(v[b], E, k, renorm, w, id);
-      fn(first + b * stride, w, id);
-    }
+    const int t = first + b * stride;
+    if (t < T && slot[b] >= 0) fn(t, slot[b], w[b], id[b]);
   }
 }
 
-template <int LDT, int G>
+template <int LDT, int G, int PL>
 __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restrict__ logits,
                                                            int T, int E, int k, int renorm,
                                                            float* __restrict__ w,
                                                            int32_t* __restrict__ ids) {
-  constexpr int TPW = TopkGroup<G>::kTokens;
+  constexpr int TPW = TopkGroup<G, PL>::kTokens;
   const int waves = blockDim.x / kWave;
   const int lane = lane_id();
-  const int j = lane % G;
   const int stride = gridDim.x * waves * TPW;  // tokens per pass of the whole grid
+  __shared__ RankScratch rs_all[4];
+  RankScratch& rs = rs_all[threadIdx.x / kWave];
   for (int t0 = (blockIdx.x * waves + threadIdx.x / kWave) * TPW + lane / G; t0 - lane / G < T;
        t0 += stride * kTokBatch) {
-    topk_batch<LDT, G>(logits, T, E, k, renorm != 0, t0, stride, [&](int t, float wv, int id) {
-      if (t < T && j < k) {
-        w[static_cast<int64_t>(t) * k + j] = wv;
-        ids[static_cast<int64_t>(t) * k + j] = id;
-      }
+    topk_batch<LDT, G, PL>(logits, T, E, k, renorm != 0, t0, stride, rs, [&](int t, int slot, float wv, int id) {
+      w[static_cast<int64_t>(t) * k + slot] = wv;
+      ids[static_cast<int64_t>(t) * k + slot] = id;
     });
   }
 }
 
 // ---------------------------------------------------------------------------------------
 // Expert sort of flat assignments f = t*k + j held in LDS (ids_l[f], -1 = dropped).
-// Stable: within an expert, assignments appear in ascending f. Counts come from per-wave
-// histograms built with ballot/popcount over 64-assignment chunks; ranks are the popcount
-// of the ballot below the lane. Reference: moe_align_block_size,
+// Stable: within an expert, assignments appear in ascending f. Each wave walks a contiguous
+// range of f in 64-wide chunks; the lanes of a chunk that share an expert are found with one
+// ballot per bit of the expert id (no loop over the experts present), a lane's rank among
+// them is the popcount of that mask below the lane, and the lowest such lane (rank 0) owns
+// the group's per-wave count. Reference: moe_align_block_size,
 // specmoe/layers/fused_moe_kernel.py:16-85 (its docstring example fixes the order).
 // ---------------------------------------------------------------------------------------
 struct AlignShared {
-  int16_t ids[kMaxAssignments];        // expert per flat assignment; -1 dropped, -2 out of range
-  int cntw[kRouteWaves][kMaxExperts];  // per-wave counts, then per-wave start positions
+  int16_t ids[kMaxAssignments];           // expert per flat assignment; -1 dropped, -2 out of range
+  int cntw[kRouteMaxWaves][kMaxExperts];  // per-wave counts, then per-wave start positions
   int cnt[kMaxExperts];
-  int off[kMaxExperts + 1];            // compact exclusive prefix
-  int seg[kMaxExperts + 1];            // block-padded exclusive prefix
-  int act[kMaxExperts + 1];            // active-expert exclusive prefix
-  int64_t slot[kMaxExperts];           // pool slot per expert (-1: unmapped), route only
-  int bad;                             // an assignment was dropped
+  int off[kMaxExperts + 1];               // compact exclusive prefix
+  int seg[kMaxExperts + 1];               // block-padded exclusive prefix
+  int act[kMaxExperts + 1];               // active-expert exclusive prefix
+  int64_t slot[kMaxExperts];              // pool slot per expert (-1: unmapped), route only
+  int bad;                                // an assignment was dropped
 };
 
 struct AlignOutputs {
@@ -166,6 +326,7 @@ struct AlignOutputs {
   int32_t* act_cnt;     // [E]
   int64_t* act_slot;    // [E]
   int32_t* sorted_f;    // [N]
+  int32_t* tmask;       // [T] per token: bit j set if assignment t*k+j is routable
   // reference-format outputs (may be null)
   int32_t* sorted_ids;  // [N + E*(BM-1)]
   int32_t* expert_ids;  // [ceil((N + E*(BM-1)) / BM)]
@@ -173,13 +334,29 @@ struct AlignOutputs {
   int bm;
 };
 
-// Walks this wave's contiguous range of f in 64-wide chunks; for every group of lanes that
-// share an expert, calls fn(mask, e, f, mine, leader) on all lanes of the wave (uniform
-// control flow). Assignments whose expert is unroutable count as dropped.
+// Lanes of the wave whose (valid) expert id equals this lane's: one ballot per id bit.
+__device__ __forceinline__ uint64_t same_expert_lanes(int e, bool valid, int nbits) {
+  uint64_t same = ballot(valid);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t m = ballot(bit);
+    same &= bit ? m : ~m;
+  }
+  return same;
+}
+
+// Walks this wave's contiguous range of f in 64-wide chunks and calls fn(e, f, rank, count)
+// on every lane holding a routable assignment (e = its expert, rank = its position among the
+// chunk's assignments to e, count = their number). Assignments whose expert is unroutable
+// count as dropped.
 template <bool kCheckSlots, typename Fn>
-__device__ __forceinline__ void for_each_expert_group(AlignShared& sh, int N, int wave, Fn&& fn) {
+__device__ __forceinline__ void for_each_assignment(AlignShared& sh, int N, int E, Fn&& fn) {
   const int lane = lane_id();
-  const int per_wave = ((N + kRouteWaves - 1) / kRouteWaves + kWave - 1) / kWave * kWave;
+  const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  const int per_wave = ((N + nw - 1) / nw + kWave - 1) / kWave * kWave;
   const int begin = wave * per_wave;
   const int end = min(N, begin + per_wave);
   for (int base = begin; base < end; base += kWave) {
@@ -189,14 +366,8 @@ __device__ __forceinline__ void for_each_expert_group(AlignShared& sh, int N, in
       sh.bad = 1;
       e = -1;
     }
-    uint64_t pending = ballot(e >= 0);
-    while (pending) {
-      const int leader = __ffsll(static_cast<long long>(pending)) - 1;
-      const int el = __shfl(e, leader, kWave);
-      const uint64_t m = ballot(e == el);
-      fn(m, el, f, e == el, leader);
-      pending &= ~m;
-    }
+    const uint64_t same = same_expert_lanes(e, e >= 0, nbits);
+    if (e >= 0) fn(e, f, __popcll(same & lt_mask), __popcll(same));
   }
 }
 
@@ -207,10 +378,11 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = lane_id();
+  const int nw = blockDim.x / kWave;
 
-  // pass 1: per-wave histograms
-  for_each_expert_group<kCheckSlots>(sh, N, wave, [&](uint64_t m, int el, int, bool, int leader) {
-    if (lane == leader) sh.cntw[wave][el] += __popcll(m);
+  // pass 1: per-wave histograms (one writer per expert and chunk: the rank-0 lane)
+  for_each_assignment<kCheckSlots>(sh, N, E, [&](int e, int, int rank, int count) {
+    if (rank == 0) sh.cntw[wave][e] += count;
   });
   __syncthreads();
 
@@ -225,7 +397,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
       const int e = lane * 4 + i;
       c[i] = 0;
       if (e < E) {
-        for (int w = 0; w < kRouteWaves; ++w) {
+        for (int w = 0; w < nw; ++w) {
           const int v = sh.cntw[w][e];
           sh.cntw[w][e] = c[i];  // per-wave exclusive prefix, in wave order
           c[i] += v;
@@ -250,7 +422,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
       const int e = lane * 4 + i;
       if (e <= E) { sh.off[e] = bc; sh.seg[e] = bp; sh.act[e] = ba; }
       if (e < E) {
-        for (int w = 0; w < kRouteWaves; ++w) sh.cntw[w][e] += bc;
+        for (int w = 0; w < nw; ++w) sh.cntw[w][e] += bc;
         if (out.act_expert && c[i] > 0) {
           out.act_expert[ba] = e;
           out.act_off[ba] = bc;
@@ -270,16 +442,14 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
     if (out.ntp) out.ntp[0] = sh.seg[E];
   }
 
-  // pass 2: stable scatter
-  const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
-  for_each_expert_group<kCheckSlots>(sh, N, wave, [&](uint64_t m, int el, int f, bool mine, int leader) {
-    const int base = sh.cntw[wave][el];
-    if (mine) {
-      const int pos = base + __popcll(m & lt_mask);
-      if (out.sorted_f) out.sorted_f[pos] = f;
-      if (out.sorted_ids) out.sorted_ids[sh.seg[el] + (pos - sh.off[el])] = f;
-    }
-    if (lane == leader) sh.cntw[wave][el] = base + __popcll(m);
+  // pass 2: stable scatter. Every lane reads its expert's running position before the
+  // rank-0 lane advances it (one wave's LDS operations execute in program order).
+  for_each_assignment<kCheckSlots>(sh, N, E, [&](int e, int f, int rank, int count) {
+    const int base = sh.cntw[wave][e];
+    const int pos = base + rank;
+    if (out.sorted_f) out.sorted_f[pos] = f;
+    if (out.sorted_ids) out.sorted_ids[sh.seg[e] + (pos - sh.off[e])] = f;
+    if (rank == 0) sh.cntw[wave][e] = base + count;
   });
 
   // reference format: sentinel padding and per-block expert ids
@@ -287,7 +457,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
     const int bm = out.bm;
     const int len = N + E * (bm - 1);
     const int nblocks = (len + bm - 1) / bm;
-    for (int e = wave; e < E; e += kRouteWaves) {
+    for (int e = wave; e < E; e += nw) {
       for (int p = sh.seg[e] + sh.cnt[e] + lane; p < sh.seg[e + 1]; p += kWave) out.sorted_ids[p] = N;
       for (int b = sh.seg[e] / bm + lane; b < sh.seg[e + 1] / bm; b += kWave) out.expert_ids[b] = e;
     }
@@ -296,14 +466,17 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
   }
 }
 
+// Zeroes the per-wave counts of the launched waves (16 bytes per store).
 __device__ __forceinline__ void zero_counts(AlignShared& sh) {
-  for (int i = threadIdx.x; i < kRouteWaves * kMaxExperts; i += blockDim.x) (&sh.cntw[0][0])[i] = 0;
+  const int n4 = static_cast<int>(blockDim.x / kWave) * kMaxExperts / 4;
+  u32x4* c = reinterpret_cast<u32x4*>(&sh.cntw[0][0]);
+  for (int i = threadIdx.x; i < n4; i += blockDim.x) c[i] = u32x4{0u, 0u, 0u, 0u};
   if (threadIdx.x == 0) sh.bad = 0;
 }
 
 // Reference-format alignment of caller-provided ids.
-__global__ __launch_bounds__(kRouteThreads) void align_kernel(const int32_t* __restrict__ ids,
-                                                              int N, int E, AlignOutputs out) {
+__global__ __launch_bounds__(kRouteMaxThreads) void align_kernel(const int32_t* __restrict__ ids,
+                                                                 int N, int E, AlignOutputs out) {
   __shared__ AlignShared sh;
   zero_counts(sh);
   for (int f = threadIdx.x; f < N; f += blockDim.x) {
@@ -318,32 +491,32 @@ __global__ __launch_bounds__(kRouteThreads) void align_kernel(const int32_t* __r
 // to w/ids and LDS); otherwise ids come from the caller. Then the compact expert sort.
 // Assignments with an id outside [0,E), or whose expert's pool slot is outside
 // [0,num_slots), are dropped (they contribute nothing) and flagged in hdr[1].
-template <int LDT, int G>
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(
+// One workgroup of 4-16 waves (the host sizes it to the batch).
+template <int LDT, int G, int PL>
+__global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
     const void* __restrict__ logits, int T, int E, int k, int renorm,
     float* __restrict__ w_out, int32_t* __restrict__ ids_out, const int32_t* __restrict__ ids_in,
     const int64_t* __restrict__ e2s, int64_t num_slots, AlignOutputs out) {
   __shared__ AlignShared sh;
-  constexpr int TPW = TopkGroup<G>::kTokens;
+  constexpr int TPW = TopkGroup<G, PL>::kTokens;
   const int N = T * k;
   const int wave = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
   const int lane = lane_id();
   zero_counts(sh);
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    const int64_t slot = e2s[e];
-    sh.slot[e] = (slot >= 0 && slot < num_slots) ? slot : -1;
-  }
+  // blockDim.x >= 256 >= E: one expert per thread. The slot is stored to LDS after the top-k
+  // so that this load's latency overlaps the logit loads.
+  const int64_t my_slot = threadIdx.x < E ? e2s[threadIdx.x] : -1;
   if (logits != nullptr) {
-    const int j = lane % G;
-    const int stride = kRouteWaves * TPW;
+    __shared__ RankScratch rs_all[kRouteMaxWaves];
+    const int stride = nw * TPW;
     for (int t0 = wave * TPW + lane / G; t0 - lane / G < T; t0 += stride * kTokBatch) {
-      topk_batch<LDT, G>(logits, T, E, k, renorm != 0, t0, stride, [&](int t, float wv, int id) {
-        if (t < T && j < k) {
-          const int f = t * k + j;
-          if (w_out) w_out[f] = wv;
-          if (ids_out) ids_out[f] = id;
-          sh.ids[f] = static_cast<int16_t>(id);
-        }
+      topk_batch<LDT, G, PL>(logits, T, E, k, renorm != 0, t0, stride, rs_all[wave],
+                             [&](int t, int slot, float wv, int id) {
+        const int f = t * k + slot;
+        if (w_out) w_out[f] = wv;
+        if (ids_out) ids_out[f] = id;
+        sh.ids[f] = static_cast<int16_t>(id);
       });
     }
   } else {
@@ -352,33 +525,60 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(
       sh.ids[f] = static_cast<int16_t>((e >= 0 && e < E) ? e : -2);
     }
   }
+  if (threadIdx.x < E) sh.slot[threadIdx.x] = (my_slot >= 0 && my_slot < num_slots) ? my_slot : -1;
   __syncthreads();
+  if (out.tmask) {
+    for (int t = threadIdx.x; t < T; t += blockDim.x) {
+      uint32_t m = 0;
+      for (int j = 0; j < k; ++j) {
+        const int e = sh.ids[t * k + j];
+        if (e >= 0 && sh.slot[e] >= 0) m |= 1u << j;
+      }
+      out.tmask[t] = static_cast<int32_t>(m);
+    }
+  }
   align_block<true>(sh, N, E, out);
 }
 
 // ---------------------------------------------------------------------------------------
 // Host-side launchers
 // ---------------------------------------------------------------------------------------
+// Largest T*E whose top-k runs inside the single routing workgroup.
+constexpr int64_t kFusedTopkMaxElems = 1024;
+
+// Lanes per token: the power of two >= E, at least 8, at most a wave.
 static int group_for(int E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64; }
 
-template <int LDT, int G>
+// Waves of the single routing workgroup: one per kTokBatch wave-passes of top-k or per 256
+// assignments, between 4 and 16.
+static int route_waves(int T, int N, int tokens_per_pass) {
+  const int by_tokens = (T + tokens_per_pass * kTokBatch - 1) / (tokens_per_pass * kTokBatch);
+  const int by_assign = (N + 255) / 256;
+  int w = by_tokens > by_assign ? by_tokens : by_assign;
+  return w < 4 ? 4 : (w > kRouteMaxWaves ? kRouteMaxWaves : w);
+}
+
+template <int LDT, int G, int PL>
 static void topk_launch(const void* logits, int T, int E, int k, int renorm, float* w, int32_t* ids,
                         hipStream_t s) {
   const int waves = 4;
-  const int per_block = waves * TopkGroup<G>::kTokens * kTokBatch;
+  const int per_block = waves * TopkGroup<G, PL>::kTokens * kTokBatch;
   int blocks = (T + per_block - 1) / per_block;
   if (blocks > 65535) blocks = 65535;
-  topk_softmax_kernel<LDT, G><<<blocks, waves * kWave, 0, s>>>(logits, T, E, k, renorm, w, ids);
+  topk_softmax_kernel<LDT, G, PL><<<blocks, waves * kWave, 0, s>>>(logits, T, E, k, renorm, w, ids);
 }
 
 template <int LDT>
 static void topk_launch_g(const void* logits, int T, int E, int k, int renorm, float* w,
                           int32_t* ids, hipStream_t s) {
   switch (group_for(E)) {
-    case 8: topk_launch<LDT, 8>(logits, T, E, k, renorm, w, ids, s); break;
-    case 16: topk_launch<LDT, 16>(logits, T, E, k, renorm, w, ids, s); break;
-    case 32: topk_launch<LDT, 32>(logits, T, E, k, renorm, w, ids, s); break;
-    default: topk_launch<LDT, 64>(logits, T, E, k, renorm, w, ids, s); break;
+    case 8: topk_launch<LDT, 8, 1>(logits, T, E, k, renorm, w, ids, s); break;
+    case 16: topk_launch<LDT, 16, 1>(logits, T, E, k, renorm, w, ids, s); break;
+    case 32: topk_launch<LDT, 32, 1>(logits, T, E, k, renorm, w, ids, s); break;
+    default:
+      if (E <= kWave) topk_launch<LDT, 64, 1>(logits, T, E, k, renorm, w, ids, s);
+      else topk_launch<LDT, 64, kMaxExpertsPerLane>(logits, T, E, k, renorm, w, ids, s);
+      break;
   }
 }
 
@@ -399,8 +599,17 @@ hipError_t launch_align(const int32_t* ids, int N, int E, int bm, int32_t* sorte
   out.expert_ids = expert_ids;
   out.ntp = ntp;
   out.bm = bm;
-  align_kernel<<<1, kRouteThreads, 0, s>>>(ids, N, E, out);
+  align_kernel<<<1, route_waves(0, N, 1) * kWave, 0, s>>>(ids, N, E, out);
   return hipGetLastError();
+}
+
+template <int LDT, int G, int PL>
+static void route_launch(const void* logits, int T, int E, int k, int renorm, float* w_out,
+                         int32_t* ids_out, const int32_t* ids_in, const int64_t* e2s,
+                         int64_t num_slots, const AlignOutputs& out, hipStream_t s) {
+  const int threads = route_waves(logits ? T : 0, T * k, TopkGroup<G, PL>::kTokens) * kWave;
+  route_kernel<LDT, G, PL><<<1, threads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in,
+                                                e2s, num_slots, out);
 }
 
 template <int LDT>
@@ -408,10 +617,13 @@ static void route_launch_g(const void* logits, int T, int E, int k, int renorm, 
                            int32_t* ids_out, const int32_t* ids_in, const int64_t* e2s,
                            int64_t num_slots, const AlignOutputs& out, hipStream_t s) {
   switch (group_for(E)) {
-    case 8: route_kernel<LDT, 8><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
-    case 16: route_kernel<LDT, 16><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
-    case 32: route_kernel<LDT, 32><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
-    default: route_kernel<LDT, 64><<<1, kRouteThreads, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    case 8: route_launch<LDT, 8, 1>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+    case 16: route_launch<LDT, 16, 1>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+    case 32: route_launch<LDT, 32, 1>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+    default:
+      if (E <= kWave) route_launch<LDT, 64, 1>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s);
+      else route_launch<LDT, 64, kMaxExpertsPerLane>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s);
+      break;
   }
 }
 
@@ -426,7 +638,21 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
   out.act_cnt = rb.act_cnt;
   out.act_slot = rb.act_slot;
   out.sorted_f = rb.sorted_f;
+  out.tmask = rb.tmask;
   out.bm = 1;
+  // the ids-given form needs no top-k: one instantiation serves every E
+  if (logits == nullptr) {
+    route_launch<kF32, 8, 1>(nullptr, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s);
+    return hipGetLastError();
+  }
+  // Large batches: the top-k runs over many workgroups first (one workgroup would be bound by
+  // one CU's VALU throughput), then the sort reads the ids it wrote.
+  if (static_cast<int64_t>(T) * E > kFusedTopkMaxElems && w_out != nullptr && ids_out != nullptr) {
+    hipError_t err = launch_topk_softmax(logits, ldt, T, E, k, renorm, w_out, ids_out, s);
+    if (err != hipSuccess) return err;
+    route_launch<kF32, 8, 1>(nullptr, T, E, k, renorm, nullptr, nullptr, ids_out, e2s, num_slots, out, s);
+    return hipGetLastError();
+  }
   switch (ldt) {
     case kF32: route_launch_g<kF32>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
     case kF16: route_launch_g<kF16>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;

@@ -6,13 +6,13 @@
 namespace smx {
 
 // Routing limits (one workgroup sorts all assignments in LDS).
-constexpr int kRouteThreads = 256;
-constexpr int kRouteWaves = kRouteThreads / kWave;
+constexpr int kRouteMaxWaves = 16;                  // waves of the single routing workgroup
+constexpr int kRouteMaxThreads = kRouteMaxWaves * kWave;
 constexpr int kMaxExperts = 256;
 constexpr int kMaxExpertsPerLane = kMaxExperts / kWave;
 constexpr int kMaxAssignments = 16384;  // T * top_k
 constexpr int kMaxTopK = 16;
-constexpr int kTokBatch = 4;            // tokens whose logits a wave loads before computing
+constexpr int kTokBatch = 1;            // wave-passes of tokens a wave computes together
 
 // Expert-kernel geometry.
 constexpr int kExpertThreads = 256;                 // 4 independent waves per workgroup
@@ -23,8 +23,6 @@ constexpr int kStepBytes = 64;                      // row bytes one 16-byte/lan
 constexpr int kUnroll = 4;                          // load steps per chunk (256 bytes per row)
 constexpr int kDownRows = 2;                        // row tiles per wave in the down projection
 constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 tokens)
-constexpr int kGateUpDepth = 1;                     // weight chunks in flight per wave (gate/up)
-constexpr int kDownDepth = 1;                       // weight chunks in flight per wave (down)
 
 static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
               "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");
@@ -36,6 +34,23 @@ struct RouteBuffers {
   int32_t* act_cnt;     // [E] assignments routed to each active expert
   int32_t* sorted_f;    // [T*k] flat assignment index f = t*k + j at each sorted position
   int64_t* act_slot;    // [E] pool slot of each active expert
+  int32_t* tmask;       // [T] bit j set: assignment t*k+j contributes (routable expert and slot)
+};
+
+// An always-active expert that every token passes through (the shared expert of the
+// Qwen-MoE and DeepSeek-V2 MoE blocks). It runs in the leading workgroups of the gate/up and
+// down launches: token range v (kTokTile * tok_tiles tokens) of the batch is one work item,
+// like one routed expert's token list.
+struct SharedArgs {
+  const void* page;     // [3 * I * H] page in the routed layout; null when absent
+  int I;                // intermediate size of the shared expert (0 when absent)
+  void* act;            // [T, I] silu(gate)*up, row = token
+  float* part;          // [splits, T, H] fp32 partial down projections, row = token
+  int splits;           // K splits of its down projection
+  int split_steps;      // load steps per split
+  int tok_groups;       // token ranges
+  int gateup_blocks;    // leading workgroups of the gate/up launch that run it
+  int down_blocks;      // leading workgroups of the down launch that run it
 };
 
 struct ExpertArgs {
@@ -49,16 +64,22 @@ struct ExpertArgs {
   float* part;          // [splits, T*k, H] fp32 partial down projections, row = f
   int splits;           // K splits of the down projection
   int split_steps;      // load steps per split
+  SharedArgs sh;
 };
 
 struct CombineArgs {
   const float* part;
   const float* w;       // [T*k]
-  const int32_t* ids;   // [T*k]
-  const int64_t* e2s;
-  int64_t num_slots;
+  const int32_t* tmask; // [T] contributing assignments of each token (RouteBuffers::tmask)
   void* y;              // [T, H]
-  int T, H, k, E, splits;
+  int T, H, k, splits;
+  // Block form y = round(round(routed * scale) + s * shared), used when `block` is set.
+  int block;
+  float scale;               // routed scaling factor
+  const float* part_s;       // [splits_s, T, H] shared-expert partials, null when absent
+  int splits_s;
+  const void* sgate;         // [T] shared-expert gate logits (s = sigmoid), null: s = 1
+  int sgate_dtype;
 };
 
 hipError_t launch_topk_softmax(const void* logits, int ldt, int T, int E, int k, int renorm,

@@ -1,10 +1,13 @@
 """Drop-in MoE layer operators (the reference's specmoe/layers MoE surface)."""
 from .FusedMoE import FusedMoE, UnquantizedFusedMoEMethod, set_weight_attrs
-from .fused_moe_kernel import fused_moe_forward, moe_align_block_size, stack_fused_moe
+from .fused_moe_kernel import (fused_moe_forward, fused_moe_shared_forward, moe_align_block_size,
+                               stack_fused_moe)
 from .mixtral_moe import MixtralMoE
+from .shared_moe import DeepseekV2MoE, Qwen2MoeSparseMoeBlock, SharedExpertMoE
 from .topk import fused_topk, select_experts
 
 __all__ = [
     "FusedMoE", "UnquantizedFusedMoEMethod", "set_weight_attrs", "fused_moe_forward",
-    "moe_align_block_size", "stack_fused_moe", "MixtralMoE", "fused_topk", "select_experts",
+    "fused_moe_shared_forward", "moe_align_block_size", "stack_fused_moe", "MixtralMoE",
+    "SharedExpertMoE", "Qwen2MoeSparseMoeBlock", "DeepseekV2MoE", "fused_topk", "select_experts",
 ]

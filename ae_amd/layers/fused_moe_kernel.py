@@ -145,3 +145,69 @@ def fused_moe_forward(
     if return_routing:
         return out, w, ids
     return out
+
+
+def fused_moe_shared_forward(
+    hidden_states: torch.Tensor,
+    router_logits: torch.Tensor,
+    w1: torch.Tensor,
+    indicies: torch.Tensor,
+    top_k: int,
+    renormalize: bool,
+    shared_w: Optional[torch.Tensor],
+    shared_gate_logits: Optional[torch.Tensor] = None,
+    routed_scaling_factor: float = 1.0,
+    inplace: bool = True,
+    return_routing: bool = False,
+):
+    """A MoE block with an always-active shared expert, in one library call.
+
+    ``y = round(round(routed * routed_scaling_factor) + s * shared)`` where ``routed`` is
+    :func:`fused_moe_forward`'s result, ``shared`` the SwiGLU MLP whose weights are packed in
+    ``shared_w`` like one pool page (``[W1s | W3s | W2s]``, ``3*Is*H`` elements) and ``s`` is
+    ``sigmoid(shared_gate_logits)`` (``[T]`` or ``[T,1]``) or 1. The reference has no shared
+    expert; this is the block of Qwen1.5-MoE (gated shared expert) and DeepSeek-V2 (ungated,
+    ``n_shared * I`` columns, scaled routed output) over the routed path of
+    specmoe/layers/FusedMoE.py:155-196.
+    """
+    assert hidden_states.shape[0] == router_logits.shape[0], "Number of tokens mismatch"
+    assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
+    assert w1.is_contiguous(), "Expert weights1 must be contiguous"
+    assert hidden_states.dtype in [torch.float32, torch.float16, torch.bfloat16]
+    assert w1.dtype == hidden_states.dtype, "expert pool and hidden states dtypes differ"
+    require_gpu(hidden_states, router_logits, w1, indicies, shared_w, shared_gate_logits)
+    H, I = _pool_geometry(hidden_states, w1)
+    T, E = router_logits.shape
+    Is = 0
+    if shared_w is not None:
+        assert shared_w.is_contiguous(), "shared expert weights must be contiguous"
+        assert shared_w.dtype == hidden_states.dtype, "shared expert and hidden states dtypes differ"
+        assert shared_w.numel() % (3 * H) == 0, "shared expert page is not 3*Is*H elements"
+        Is = shared_w.numel() // (3 * H)
+    sgate = None
+    if shared_gate_logits is not None:
+        assert shared_w is not None, "a shared-expert gate needs a shared expert"
+        assert shared_gate_logits.numel() == T, "one shared-expert gate logit per token"
+        assert shared_gate_logits.dtype == router_logits.dtype, \
+            "shared-expert gate logits and router logits dtypes differ"
+        sgate = shared_gate_logits.contiguous()
+    logits = router_logits.contiguous()
+    out = hidden_states if inplace else torch.empty_like(hidden_states)
+    slots = _as_index(indicies, torch.int64)
+    dt = dtype_code(hidden_states.dtype)
+    nbytes = _lib.lib().smx_moe_shared_workspace_size(T, H, I, E, top_k, Is, dt)
+    if nbytes == 0 and T > 0:
+        raise ValueError(f"unsupported MoE shape T={T} H={H} I={I} E={E} top_k={top_k} "
+                         f"shared I={Is}")
+    ws = workspace(nbytes, hidden_states.device)
+    w = ids = None
+    if return_routing:
+        w = torch.empty((T, top_k), dtype=torch.float32, device=hidden_states.device)
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=hidden_states.device)
+    _lib.call("smx_fused_moe_shared_forward", ptr(hidden_states), ptr(out), dt, T, H, ptr(logits),
+              dtype_code(logits.dtype), E, top_k, int(bool(renormalize)), ptr(w1), w1.shape[0],
+              w1.shape[1], ptr(slots), ptr(shared_w), Is, ptr(sgate), float(routed_scaling_factor),
+              ptr(w), ptr(ids), ptr(ws), ws.numel(), stream_of(hidden_states))
+    if return_routing:
+        return out, w, ids
+    return out

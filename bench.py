@@ -7,11 +7,20 @@ through the C ABI, with inputs resident in HBM. Expert weights are N(0, 0.02), h
 N(0, 1), synthetic; two copies of the expert pool are rotated so no step finds the previous
 step's weights in a cache.
 
-Prints one JSON line: value = algorithmic HBM bytes of the layer / measured time (GB/s),
+Other workloads (--workload): the MoE blocks with a shared expert, one call each through
+smx_fused_moe_shared_forward -- qwen15 (Qwen1.5-MoE-A2.7B: hidden 2048, 60 experts of ffn
+1408, top-4, gated shared expert of ffn 5632, 64 tokens) and dsv2lite (DeepSeek-V2-Lite:
+hidden 2048, 64 experts of ffn 1408, top-6, shared ffn 2816); router logits 2*N(0,1), no
+renormalisation. --layers N runs a stack of N layers with distinct weights per step
+(DeepSeek-V2-Lite has 26), --sweep-tokens runs one line per token count, --graph replays
+each step from a HIP graph.
+
+Prints one JSON line per token count: value = algorithmic HBM bytes / measured time (GB/s),
 plus us per step, the roofline of the dominant kernel (gate/up) timed live with HIP events
 on the launch stream, and the CPU oracle timed on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu]
+    python bench.py --workload dsv2lite --layers 26 --sweep-tokens 1,2,4,8,16,32,64,128 --no-cpu
 """
 from __future__ import annotations
 
@@ -27,19 +36,36 @@ import torch
 METRIC = "MoE layer us/verify-step + achieved HBM GB/s (% peak), Mixtral shape, 8-64 tokens"
 HBM_PEAK_GBS = 8000.0
 
+WORKLOADS = {
+    "mixtral": dict(title="Mixtral-8x7B-shape MoE layer verify step", tokens=32, hidden=4096,
+                    ffn=14336, experts=8, topk=2, shared_ffn=0, gated=False, renormalize=True),
+    "qwen15": dict(title="Qwen1.5-MoE-A2.7B-shape MoE block (gated shared expert) verify step",
+                   tokens=64, hidden=2048, ffn=1408, experts=60, topk=4, shared_ffn=5632,
+                   gated=True, renormalize=False),
+    "dsv2lite": dict(title="DeepSeek-V2-Lite-shape MoE block (2 shared experts) verify step",
+                     tokens=32, hidden=2048, ffn=1408, experts=64, topk=6, shared_ffn=2816,
+                     gated=False, renormalize=False),
+}
+
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--tokens", type=int, default=32)
-    ap.add_argument("--hidden", type=int, default=4096)
-    ap.add_argument("--ffn", type=int, default=14336)
-    ap.add_argument("--experts", type=int, default=8)
-    ap.add_argument("--topk", type=int, default=2)
-    ap.add_argument("--zipf", type=float, default=1.2, help="gate bias exponent (0 = unbiased)")
-    ap.add_argument("--rotate", type=int, default=2, help="expert pool copies rotated per step")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="mixtral")
+    ap.add_argument("--tokens", type=int, default=None)
+    ap.add_argument("--sweep-tokens", type=str, default=None,
+                    help="comma-separated token counts, one JSON line each")
+    ap.add_argument("--hidden", type=int, default=None)
+    ap.add_argument("--ffn", type=int, default=None)
+    ap.add_argument("--experts", type=int, default=None)
+    ap.add_argument("--topk", type=int, default=None)
+    ap.add_argument("--layers", type=int, default=1, help="layers with distinct weights per step")
+    ap.add_argument("--graph", action="store_true", help="replay each step from a HIP graph")
+    ap.add_argument("--zipf", type=float, default=1.2,
+                    help="Mixtral gate bias exponent (0 = unbiased)")
+    ap.add_argument("--rotate", type=int, default=2, help="copies of the weights rotated per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-calls", type=int, default=2, help="CPU baseline sample: layer calls")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -64,9 +90,11 @@ def copy_calibration():
                       "launches": 10}), flush=True)
 
 
-def measured_traffic(T, H, I, E, k):
+def measured_traffic(T, H, I, E, k, workload):
     """HBM bytes per gateup_kernel launch measured with rocprofv3 counters for this workload
     (committed under profiles/), or None."""
+    if workload != "mixtral":
+        return None
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
@@ -75,6 +103,202 @@ def measured_traffic(T, H, I, E, k):
     if t.get("workload") != {"tokens": T, "hidden": H, "ffn": I, "experts": E, "top_k": k}:
         return None
     return t.get("bytes_per_launch")
+
+
+class Layer:
+    """One MoE layer's weights in HBM: `copies` expert pools (and shared pages) to rotate."""
+
+    def __init__(self, g, dev, H, I, E, Is, copies, dtype):
+        self.pools, self.shared = [], []
+        for _ in range(copies):
+            pool = torch.empty((E, 3 * I * H), dtype=dtype, device=dev)
+            for e in range(E):  # fill page by page to bound the fp32 temporary
+                pool[e] = (torch.randn(3 * I * H, generator=g, device=dev) * 0.02).to(dtype)
+            self.pools.append(pool)
+            if Is:
+                self.shared.append((torch.randn(3 * Is * H, generator=g, device=dev) * 0.02).to(dtype))
+
+
+def run_tokens(args, wl, T, layers, L, dev):
+    from ae_amd import _lib
+    from ae_amd.layers._torch import ptr
+
+    H, I, E, k, Is = args.hidden, args.ffn, args.experts, args.topk, wl["shared_ffn"]
+    dtype, es = torch.bfloat16, 2
+    g = torch.Generator(device=dev).manual_seed(1000 + T)
+    x = torch.randn((T, H), generator=g, device=dev).to(dtype)
+    if args.workload == "mixtral":
+        wg = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(dtype)
+        if args.zipf > 0:
+            p = torch.arange(1, E + 1, dtype=torch.float64) ** (-args.zipf)
+            bias = torch.log(p / p.sum()).to(device=dev, dtype=dtype)
+        else:
+            bias = torch.zeros(E, dtype=dtype, device=dev)
+        logits = torch.nn.functional.linear(x, wg) + bias
+        routing = f"zipf s={args.zipf}" if args.zipf > 0 else "unbiased"
+    else:
+        logits = (torch.randn((T, E), generator=g, device=dev) * 2.0).to(dtype)
+        routing = "logits 2*N(0,1)"
+    sgate = torch.randn((T, 1), generator=g, device=dev).to(dtype) if wl["gated"] else None
+    y = torch.empty_like(x)
+    w_out = torch.empty((T, k), dtype=torch.float32, device=dev)
+    ids_out = torch.empty((T, k), dtype=torch.int32, device=dev)
+    if Is:
+        nbytes = L.smx_moe_shared_workspace_size(T, H, I, E, k, Is, _lib.SMX_BF16)
+    else:
+        nbytes = L.smx_moe_workspace_size(T, H, I, E, k, _lib.SMX_BF16)
+    if nbytes == 0:
+        raise SystemExit(f"unsupported shape T={T} H={H} I={I} E={E} k={k} shared={Is}")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    renorm = 1 if wl["renormalize"] else 0
+
+    def call(layer, c, stream):
+        sp = ctypes.c_void_p(stream.cuda_stream)
+        pool = layer.pools[c]
+        if Is:
+            rc = L.smx_fused_moe_shared_forward(
+                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(logits), _lib.SMX_BF16, E, k, renorm,
+                ptr(pool), E, 3 * I * H, ptr(slots), ptr(layer.shared[c]), Is, ptr(sgate), 1.0,
+                ptr(w_out), ptr(ids_out), ptr(ws), nbytes, sp)
+            _lib.check("smx_fused_moe_shared_forward", rc)
+        else:
+            rc = L.smx_fused_moe_forward(
+                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(logits), _lib.SMX_BF16, E, k, renorm,
+                ptr(pool), E, 3 * I * H, ptr(slots), ptr(w_out), ptr(ids_out), ptr(ws), nbytes, sp)
+            _lib.check("smx_fused_moe_forward", rc)
+
+    slots = torch.arange(E, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    copies = len(layers[0].pools)
+
+    def step(i, s=None):
+        for layer in layers:
+            call(layer, i % copies, s or stream)
+
+    # ---- routing facts for the algorithmic byte count (same logits for every layer)
+    call(layers[0], 0, stream)
+    torch.cuda.synchronize()
+    ids_np = ids_out.cpu().numpy()
+    active = sorted(set(int(v) for v in ids_np.reshape(-1)))
+    counts = [int((ids_np == e).sum()) for e in range(E)]
+    weight_bytes = len(active) * 3 * H * I * es + 3 * H * Is * es
+    layer_bytes = (weight_bytes + 2 * T * H * es + T * E * es + T * k * 8
+                   + (T * es if wl["gated"] else 0))
+    step_bytes = layer_bytes * len(layers)
+    gateup_bytes = ((len(active) * 2 * H * I + 2 * H * Is) * es + T * H * es
+                    + (T * k * I + T * Is) * es)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    graphs = None
+    if args.graph:
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(stream)
+        graphs = []
+        with torch.cuda.stream(side):
+            for c in range(copies):
+                step(c, side)  # warm the capture stream
+        torch.cuda.synchronize()
+        for c in range(copies):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                step(c, torch.cuda.current_stream(dev))
+            graphs.append(gr)
+        for c in range(copies):
+            graphs[c].replay()
+        torch.cuda.synchronize()
+
+    # ---- timed region: K steps; per-kernel HIP events on the launch stream (eager, 1 layer)
+    per_kernel = graphs is None and len(layers) == 1
+    ev = handles = None
+    if per_kernel:
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+        for row in ev:  # materialise the event handles
+            for e_ in row:
+                e_.record(stream)
+        handles = [(ctypes.c_void_p * 5)(*[e_.cuda_event for e_ in row]) for row in ev]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for i in range(args.steps):
+        if graphs is not None:
+            graphs[i % copies].replay()
+        else:
+            if per_kernel:
+                _lib.check("smx_set_profile_events", L.smx_set_profile_events(handles[i], 5))
+            step(i)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    if per_kernel:
+        _lib.check("smx_set_profile_events", L.smx_set_profile_events(None, 0))
+
+    ms_step = t_start.elapsed_time(t_end) / args.steps
+    us_step = 1000.0 * ms_step
+    value = step_bytes / (us_step * 1e-6) / 1e9
+    config = {
+        "workload": f"{wl['title']}, {T} tokens" + (f", {len(layers)} layers" if len(layers) > 1 else ""),
+        "tokens": T, "hidden": H, "ffn": I, "experts": E, "top_k": k,
+        "routing": routing, "active_experts": len(active), "tokens_per_expert": counts,
+        "pool_copies_rotated": copies,
+    }
+    if Is:
+        config.update({"shared_ffn": Is, "shared_gate": wl["gated"]})
+    if len(layers) > 1:
+        config["layers"] = len(layers)
+    if graphs is not None:
+        config["hip_graph"] = True
+    out = {
+        "metric": METRIC if args.workload == "mixtral" else
+        f"MoE {'stack' if len(layers) > 1 else 'layer'} us/verify-step + achieved HBM GB/s, {args.workload}",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: N(0,0.02) expert weights, N(0,1) hidden states, "
+                + ("gate N(0,0.02) + Zipf bias" if args.workload == "mixtral" else "router logits 2*N(0,1)"),
+        "config": config,
+        "us_per_step": round(us_step, 2),
+        "layer_hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes": step_bytes,
+        "wall_s_timed": round(wall, 4),
+        "roofline": None,
+        "cpu_baseline": None,
+    }
+    if per_kernel:
+        stage = [0.0] * 4
+        for row in ev:
+            for s in range(4):
+                stage[s] += row[s].elapsed_time(row[s + 1])
+        stage_us = [1000.0 * v / args.steps for v in stage]
+        gateup_gbs = gateup_bytes / (stage_us[1] * 1e-6) / 1e9
+        out["stage_us"] = {"route": round(stage_us[0], 2), "gate_up": round(stage_us[1], 2),
+                           "down": round(stage_us[2], 2), "combine": round(stage_us[3], 2)}
+        out["roofline"] = {
+            "kernel": "gateup_kernel (W1/W3 stream + SiLU*up epilogue)",
+            "bound": "hbm",
+            "achieved": round(gateup_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gateup_gbs / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(T, H, I, E, k, args.workload),
+            "algorithmic_bytes": gateup_bytes,
+            "us_per_launch": round(stage_us[1], 2),
+        }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(args, wl, x, logits, sgate, layers[0], slots,
+                                           layer_bytes)
+    print(json.dumps(out), flush=True)
 
 
 def main():
@@ -89,154 +313,56 @@ def main():
         return
 
     from ae_amd import _lib
-    from ae_amd.layers._torch import ptr
 
+    wl = WORKLOADS[args.workload]
+    for key in ("hidden", "ffn", "experts", "topk"):
+        if getattr(args, key) is None:
+            setattr(args, key, wl[key])
+    tokens = ([int(v) for v in args.sweep_tokens.split(",")] if args.sweep_tokens
+              else [args.tokens if args.tokens is not None else wl["tokens"]])
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
-    T, H, I, E, k = args.tokens, args.hidden, args.ffn, args.experts, args.topk
-    dtype = torch.bfloat16
     L = _lib.lib()
-
-    # ---- synthetic inputs, resident in HBM
     g = torch.Generator(device=dev).manual_seed(0)
-    pools = []
-    for r in range(args.rotate):
-        pool = torch.empty((E, 3 * I * H), dtype=dtype, device=dev)
-        for e in range(E):  # fill page by page to bound the fp32 temporary
-            pool[e] = (torch.randn(3 * I * H, generator=g, device=dev) * 0.02).to(dtype)
-        pools.append(pool)
-    slots = torch.arange(E, dtype=torch.int64, device=dev)
-    x = torch.randn((T, H), generator=g, device=dev).to(dtype)
-    wg = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(dtype)
-    if args.zipf > 0:
-        p = torch.arange(1, E + 1, dtype=torch.float64) ** (-args.zipf)
-        bias = torch.log(p / p.sum()).to(device=dev, dtype=dtype)
-    else:
-        bias = torch.zeros(E, dtype=dtype, device=dev)
-    logits = torch.nn.functional.linear(x, wg) + bias
-    y = torch.empty_like(x)
-    w_out = torch.empty((T, k), dtype=torch.float32, device=dev)
-    ids_out = torch.empty((T, k), dtype=torch.int32, device=dev)
-    nbytes = L.smx_moe_workspace_size(T, H, I, E, k, _lib.SMX_BF16)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    stream = torch.cuda.current_stream(dev)
-    sp = ctypes.c_void_p(stream.cuda_stream)
-
-    def step(i):
-        pool = pools[i % len(pools)]
-        _lib.check("smx_fused_moe_forward", L.smx_fused_moe_forward(
-            ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(logits), _lib.SMX_BF16, E, k, 1,
-            ptr(pool), E, 3 * I * H, ptr(slots), ptr(w_out), ptr(ids_out), ptr(ws), nbytes, sp))
-
-    # ---- routing facts for the algorithmic byte count
-    step(0)
-    torch.cuda.synchronize()
-    ids_np = ids_out.cpu().numpy()
-    active = sorted(set(int(v) for v in ids_np.reshape(-1)))
-    counts = [int((ids_np == e).sum()) for e in range(E)]
-    es = 2
-    weight_bytes = len(active) * 3 * H * I * es
-    layer_bytes = (weight_bytes + 2 * T * H * es + T * E * es + T * k * 8)
-    gateup_bytes = len(active) * 2 * H * I * es + T * H * es + T * k * I * es
-
-    # ---- warmup
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-
-    # ---- timed region: K steps, per-kernel HIP events recorded on the launch stream
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
-    for row in ev:  # materialise the event handles
-        for e_ in row:
-            e_.record(stream)
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
-    handles = [(ctypes.c_void_p * 5)(*[e_.cuda_event for e_ in row]) for row in ev]
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    t_start.record(stream)
-    for i in range(args.steps):
-        _lib.check("smx_set_profile_events", L.smx_set_profile_events(handles[i], 5))
-        step(i)
-    t_end.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    _lib.check("smx_set_profile_events", L.smx_set_profile_events(None, 0))
-
-    ms_total = t_start.elapsed_time(t_end)
-    ms_step = ms_total / args.steps
-    stage = [0.0] * 4
-    for row in ev:
-        for s in range(4):
-            stage[s] += row[s].elapsed_time(row[s + 1])
-    stage_us = [1000.0 * v / args.steps for v in stage]
-    us_step = 1000.0 * ms_step
-    value = layer_bytes / (us_step * 1e-6) / 1e9
-    gateup_gbs = gateup_bytes / (stage_us[1] * 1e-6) / 1e9
-
-    out = {
-        "metric": METRIC,
-        "value": round(value, 1),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) expert weights, N(0,1) hidden states, gate N(0,0.02) + Zipf bias",
-        "config": {
-            "workload": f"Mixtral-8x7B-shape MoE layer verify step, {T} tokens",
-            "tokens": T, "hidden": H, "ffn": I, "experts": E, "top_k": k,
-            "routing": f"zipf s={args.zipf}" if args.zipf > 0 else "unbiased",
-            "active_experts": len(active), "tokens_per_expert": counts,
-            "pool_copies_rotated": len(pools),
-        },
-        "us_per_step": round(us_step, 2),
-        "layer_hbm_frac": round(value / HBM_PEAK_GBS, 4),
-        "algorithmic_bytes": layer_bytes,
-        "stage_us": {"route": round(stage_us[0], 2), "gate_up": round(stage_us[1], 2),
-                     "down": round(stage_us[2], 2), "combine": round(stage_us[3], 2)},
-        "wall_s_timed": round(wall, 4),
-        "roofline": {
-            "kernel": "gateup_kernel (W1/W3 stream + SiLU*up epilogue)",
-            "bound": "hbm",
-            "achieved": round(gateup_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gateup_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(T, H, I, E, k),
-            "algorithmic_bytes": gateup_bytes,
-            "us_per_launch": round(stage_us[1], 2),
-        },
-        "cpu_baseline": None,
-    }
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(args, x, logits, pools[0], slots, layer_bytes)
-    print(json.dumps(out), flush=True)
+    copies = args.rotate if args.layers == 1 else 1  # a stack of layers is its own rotation
+    layers = [Layer(g, dev, args.hidden, args.ffn, args.experts, wl["shared_ffn"], copies,
+                    torch.bfloat16) for _ in range(args.layers)]
+    for T in tokens:
+        run_tokens(args, wl, T, layers, L, dev)
 
 
-def cpu_baseline(args, x, logits, pool, slots, layer_bytes):
-    """The numpy oracle on the host cores, on the same workload; a bounded sample of
-    --cpu-calls layer calls (inputs copied to host memory before timing)."""
+def cpu_baseline(args, wl, x, logits, sgate, layer, slots, layer_bytes):
+    """The numpy oracle on the host cores, on the same workload (one layer); a bounded sample
+    of --cpu-calls layer calls (inputs copied to host memory before timing)."""
     import numpy as np
     from oracle import moe_ref as ref
 
-    xb = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    def bits(t):
+        return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+    xb = bits(x)
     lf = logits.float().cpu().numpy()
-    pb = pool.cpu().view(torch.int16).numpy().view(np.uint16)
+    pb = bits(layer.pools[0])
     sl = slots.cpu().numpy()
+    shared = bits(layer.shared[0]) if layer.shared else None
+    sg = sgate.float().cpu().numpy().reshape(-1) if sgate is not None else None
+    renorm = wl["renormalize"]
+
+    def run(n):
+        if shared is None:
+            return ref.fused_moe_forward(xb[:n], lf[:n], pb, sl, args.topk, renorm, ref.BF16)
+        return ref.fused_moe_shared_forward(xb[:n], lf[:n], pb, sl, args.topk, renorm, ref.BF16,
+                                            shared, None if sg is None else sg[:n])
+
     try:
         from threadpoolctl import threadpool_info
         cores = max(int(i["num_threads"]) for i in threadpool_info() if i.get("user_api") == "blas")
     except Exception:
         cores = len(os.sched_getaffinity(0))
-    ref.fused_moe_forward(xb[:1], lf[:1], pb, sl, args.topk, True, ref.BF16)  # warm BLAS
+    run(1)  # warm BLAS
     t0 = time.perf_counter()
     for _ in range(args.cpu_calls):
-        ref.fused_moe_forward(xb, lf, pb, sl, args.topk, True, ref.BF16)
+        run(xb.shape[0])
     dt = (time.perf_counter() - t0) / args.cpu_calls
     cpu_model = ""
     try:

@@ -40,7 +40,7 @@ enum smx_status {
 /* Limits: 1 <= E <= 256; 1 <= top_k <= min(E, 16); T*top_k <= 16384;
  * H and I multiples of 128 for 16-bit types and of 64 for fp32 (a weight row is a whole
  * number of 256-byte chunks); H, I <= 2^20; T*H and T*top_k*I activation bytes < 2^31;
- * page_elems <= 2^30.
+ * page_elems <= 2^30 and page bytes < 2^32.
  * T == 0 is a no-op. Shapes outside these limits return SMX_ERR_UNSUPPORTED. */
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -116,6 +116,38 @@ int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, i
                           const int64_t* expert_to_slot,
                           float* topk_weights_out, int32_t* topk_ids_out,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace smx_fused_moe_shared_forward needs (shared_I = 0: no shared expert). */
+size_t smx_moe_shared_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
+                                     int64_t shared_I, int dtype);
+
+/*
+ * A whole MoE block with an always-active shared expert, in one call:
+ *   y[t] = round( round(routed[t] * routed_scaling_factor) + s[t] * shared[t] )
+ *   routed[t] = round(sum_j round(w[t,j] * W2_e(...)))     as in smx_fused_moe_forward
+ *   shared[t] = round(W2s (round(silu(round(W1s x[t])) * round(W3s x[t]))))
+ *   s[t]      = round(sigmoid(shared_gate_logits[t])), or 1 when shared_gate_logits is NULL;
+ *               the product s*shared is rounded, and every round() is to `dtype`.
+ * This is the Qwen1.5-MoE / Qwen2-MoE block (gated shared expert, scale 1) and the
+ * DeepSeek-V2 MoE block (ungated shared experts fused into one MLP of n_shared*I columns,
+ * scaled routed output), with the rounding points of those blocks' unfused layers.
+ * No counterpart in the reference: it serves no model with shared experts (its Mixtral
+ * block is MixtralMoE.forward, specmoe/models/mixtral.py:106-115); the routed part is the
+ * FusedMoE path above and the shared expert runs as one more expert in the same launches.
+ *   shared_page [3*shared_I*H] of dtype, packed like a pool page: [W1s | W3s | W2s];
+ *               NULL with shared_I = 0 for no shared expert.
+ *   shared_gate_logits [T] of logits_dtype (the block's shared_expert_gate output) or NULL.
+ * shared_I obeys the limits on I.
+ */
+int smx_fused_moe_shared_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                                 const void* router_logits, int logits_dtype, int64_t E,
+                                 int64_t top_k, int renormalize,
+                                 const void* pool, int64_t num_slots, int64_t page_elems,
+                                 const int64_t* expert_to_slot,
+                                 const void* shared_page, int64_t shared_I,
+                                 const void* shared_gate_logits, float routed_scaling_factor,
+                                 float* topk_weights_out, int32_t* topk_ids_out,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records

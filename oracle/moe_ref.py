@@ -19,6 +19,12 @@ A plain numpy restatement of the reference's arithmetic:
             :248, is not reproduced).
   page      FusedMoE.weight_loader, specmoe/layers/FusedMoE.py:485-505: one page per expert,
             [W1 (I x H) | W3 (I x H) | W2 (H x I)].
+  shared    no reference code (the reference serves only Mixtral). The MoE blocks of the
+            public Qwen1.5-MoE / Qwen2-MoE and DeepSeek-V2 architectures, with the rounding
+            points of their unfused layers: shared MLP d = round(round(silu(round(x W1s^T)) *
+            round(x W3s^T)) W2s^T); Qwen gate s = round(sigmoid(gate logit)), shared term
+            round(s * d); DeepSeek routed term round(y * routed_scaling_factor); block output
+            round(routed term + shared term).
 
 Routing arithmetic is restated operation for operation (same exp method, same summation
 tree, correctly rounded fp32 divide), so GPU routing weights match this oracle bit for bit.
@@ -27,8 +33,12 @@ GEMM accumulation order is not restated; outputs agree to a stated tolerance.
 Parity pinning (tests/test_oracle.py): the align docstring example; brute-force sorting;
 top-k against np.argsort/lexsort selection and hand-built tie cases; exp_nonpos against float64
 exp (<= 2 ulp); the expert math against a float64 textbook SwiGLU MoE built from separate
-gate/up/down matrices through the page packing. No reference test vectors exist beyond the
-align docstring example (the reference ships no tests).
+gate/up/down matrices through the page packing; the shared-expert block against a float64
+textbook block and its reductions (zero shared page -> routed result, zero routed pages ->
+dense MLP, saturated gate -> ungated / routed only). No reference test vectors exist beyond
+the align docstring example (the reference ships no tests). Parity of the shared-expert block
+with the reference is unpinned: the reference has no such block; it is pinned to the public
+architecture only.
 """
 from __future__ import annotations
 
@@ -121,7 +131,8 @@ _PER_LANE = 4  # experts per lane (E <= 256)
 def softmax_probs(logits: np.ndarray) -> np.ndarray:
     """fp32 softmax over the last axis with the kernel's summation order: expert e sits on
     lane e % 64 as its (e // 64)-th value; each lane sums its values in order, then lanes
-    are combined by halving (lane l + lane l+32, then +16, ...). p = ex * (1 / sum)."""
+    are combined pairwise by a butterfly with offsets 1, 2, 4, ..., 32 (lane l + lane l^1,
+    then + lane l^2, ...). p = ex * (1 / sum)."""
     x = np.asarray(logits, dtype=np.float32)
     T, E = x.shape
     if E > _LANES * _PER_LANE:
@@ -134,10 +145,8 @@ def softmax_probs(logits: np.ndarray) -> np.ndarray:
     s = lanes[:, 0, :].copy()
     for i in range(1, _PER_LANE):
         s = s + lanes[:, i, :]
-    half = _LANES // 2
-    while half >= 1:
-        s = s[:, :half] + s[:, half:2 * half]
-        half //= 2
+    while s.shape[1] > 1:  # after each level the lanes of a pair hold equal values
+        s = s[:, 0::2] + s[:, 1::2]
     inv = _f32(1.0) / s[:, 0]
     return ex * inv[:, None]
 
@@ -270,4 +279,43 @@ def fused_moe_forward(x, router_logits, pool, slots, top_k: int, renormalize: bo
     logits = np.asarray(router_logits, dtype=np.float32)
     w, ids = topk_softmax(logits, top_k, renormalize)
     y = stack_fused_moe(x, pool, slots, w, ids, dtype, num_experts=logits.shape[1])
+    return y, w, ids
+
+
+# ---------------------------------------------------------------------------------------------
+# shared expert blocks (Qwen1.5-MoE / Qwen2-MoE, DeepSeek-V2); no reference counterpart
+# ---------------------------------------------------------------------------------------------
+def shared_expert_mlp(x: np.ndarray, page: np.ndarray, dtype: str) -> np.ndarray:
+    """Dense SwiGLU MLP over every token with the weights of one page [W1s | W3s | W2s]:
+    round(round(silu(round(x W1s^T)) * round(x W3s^T)) W2s^T) -> [T,H] float32."""
+    xf = to_f32(x, dtype)
+    W1, W3, W2 = unpack_page(page, xf.shape[1], dtype)
+    g = round_to(xf @ W1.T, dtype)
+    u = round_to(xf @ W3.T, dtype)
+    a = round_to(silu(g) * u, dtype)
+    return round_to(a @ W2.T, dtype)
+
+
+def sigmoid(z: np.ndarray) -> np.ndarray:
+    z = np.asarray(z, dtype=np.float32)
+    with np.errstate(over="ignore"):  # exp(-z) = inf for z < -88.7: sigmoid = 0
+        return _f32(1.0) / (_f32(1.0) + np.exp(-z))
+
+
+def fused_moe_shared_forward(x, router_logits, pool, slots, top_k: int, renormalize: bool,
+                             dtype: str, shared_page=None, shared_gate_logits=None,
+                             routed_scaling_factor: float = 1.0):
+    """The MoE block with a shared expert -> (y, topk_weights, topk_ids):
+    y = round(round(routed * scale) + s * shared), s = round(sigmoid(gate logit)) or 1,
+    the product s * shared rounded; routed = fused_moe_forward's result."""
+    y, w, ids = fused_moe_forward(x, router_logits, pool, slots, top_k, renormalize, dtype)
+    if routed_scaling_factor != 1.0:
+        y = round_to(y * _f32(routed_scaling_factor), dtype)
+    if shared_page is not None:
+        d = shared_expert_mlp(x, shared_page, dtype)
+        if shared_gate_logits is not None:
+            sg = np.asarray(shared_gate_logits, dtype=np.float32).reshape(-1)
+            s = round_to(sigmoid(sg), dtype)
+            d = round_to(s[:, None] * d, dtype)
+        y = round_to(y + d, dtype)
     return y, w, ids

@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 8, names
+    assert len(names) == 10, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -120,3 +120,36 @@ def test_python_error_mapping():
         _lib.check("smx_stack_fused_moe", _lib.SMX_ERR_WORKSPACE)
     assert ei.value.code == _lib.SMX_ERR_WORKSPACE
     assert "workspace" in str(ei.value)
+
+
+def test_shared_workspace_size():
+    ws, sws = L.smx_moe_workspace_size, L.smx_moe_shared_workspace_size
+    assert sws(64, 2048, 1408, 60, 4, 0, 2) == ws(64, 2048, 1408, 60, 4, 2)
+    assert sws(64, 2048, 1408, 60, 4, 5632, 2) > ws(64, 2048, 1408, 60, 4, 2)
+    assert sws(128, 2048, 1408, 64, 6, 2816, 2) > sws(64, 2048, 1408, 64, 6, 2816, 2)
+    assert sws(64, 2048, 1408, 60, 4, 100, 2) == 0    # shared I not a multiple of 128
+    assert sws(64, 2048, 1408, 60, 4, -1, 2) == 0
+
+
+def _shared(**kw):
+    a = dict(hidden=A, out=A, dtype=2, T=4, H=256, logits=A, ldt=2, E=4, k=2, renorm=0, pool=A,
+             slots=4, page=3 * 256 * 256, e2s=A, spage=A, sI=256, sgate=VP(0), scale=1.0,
+             w=VP(0), ids=VP(0), ws=A, wsb=1 << 30, stream=VP(0))
+    a.update(kw)
+    return L.smx_fused_moe_shared_forward(
+        a["hidden"], a["out"], a["dtype"], a["T"], a["H"], a["logits"], a["ldt"], a["E"], a["k"],
+        a["renorm"], a["pool"], a["slots"], a["page"], a["e2s"], a["spage"], a["sI"], a["sgate"],
+        a["scale"], a["w"], a["ids"], a["ws"], a["wsb"], a["stream"])
+
+
+def test_shared_forward_rejects_before_launch():
+    assert _shared(sI=-1) == _lib.SMX_ERR_INVALID_ARG
+    assert _shared(spage=VP(0)) == _lib.SMX_ERR_INVALID_ARG              # I > 0 without a page
+    assert _shared(sI=0) == _lib.SMX_ERR_INVALID_ARG                     # page without I
+    assert _shared(sI=0, spage=VP(0), sgate=A) == _lib.SMX_ERR_INVALID_ARG  # gate, no expert
+    assert _shared(scale=float("inf")) == _lib.SMX_ERR_INVALID_ARG
+    assert _shared(scale=float("nan")) == _lib.SMX_ERR_INVALID_ARG
+    assert _shared(spage=VP(0x10008)) == _lib.SMX_ERR_MISALIGNED
+    assert _shared(sI=100) == _lib.SMX_ERR_UNSUPPORTED                   # not a multiple of 128
+    assert _shared(wsb=16) == _lib.SMX_ERR_WORKSPACE
+    assert _shared(T=0) == _lib.SMX_OK

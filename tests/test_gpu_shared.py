@@ -1,0 +1,197 @@
+"""GPU parity of the MoE block with a shared expert (smx_fused_moe_shared_forward) against the
+oracle, through the C ABI: Qwen1.5-MoE-style gated shared expert, DeepSeek-V2-style ungated
+shared experts with a routed scaling factor, and the block modules."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as ref
+from ae_amd.layers import (DeepseekV2MoE, Qwen2MoeSparseMoeBlock, fused_moe_forward,
+                           fused_moe_shared_forward, set_weight_attrs)
+from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _inputs(T, H, E, dtype, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dtype)
+    logits = (torch.randn((T, E), generator=g, device=DEV) * 2.0).to(dtype)
+    sgate = (torch.randn((T, 1), generator=g, device=DEV) * 2.0).to(dtype)
+    return x, logits, sgate
+
+
+def _shared_page(H, Is, dtype, seed, scale=0.02):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn((3 * Is * H,), generator=g, device=DEV) * scale).to(dtype)
+
+
+def _oracle(x, logits, pool, slots, k, renorm, page, sgate, scale):
+    dt = TORCH_TO_ORACLE[x.dtype]
+    return ref.fused_moe_shared_forward(
+        to_oracle(x), f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, renorm, dt,
+        shared_page=None if page is None else to_oracle(page),
+        shared_gate_logits=None if sgate is None else f32_of(sgate), routed_scaling_factor=scale)
+
+
+def _check(x, logits, pool, slots, k, renorm, page, sgate, scale):
+    y, w, ids = fused_moe_shared_forward(x.clone(), logits, pool, slots, k, renorm, page, sgate,
+                                         scale, inplace=False, return_routing=True)
+    torch.cuda.synchronize()
+    y_ref, w_ref, ids_ref = _oracle(x, logits, pool, slots, k, renorm, page, sgate, scale)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    err = max_rel_err(f32_of(y), y_ref)
+    assert err <= TOL[x.dtype], err
+    return y
+
+
+CASES = [
+    # T, H, I, E, k, Is
+    (1, 128, 128, 4, 2, 256),
+    (5, 256, 128, 8, 2, 384),
+    (33, 256, 256, 16, 4, 128),
+    (64, 128, 128, 8, 2, 512),
+    (70, 256, 128, 8, 2, 256),     # two token ranges of the shared expert
+    (130, 128, 256, 6, 3, 256),    # three token ranges
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("gated", [True, False])
+@pytest.mark.parametrize("T,H,I,E,k,Is", CASES)
+def test_shared_block_matches_oracle(dtype, gated, T, H, I, E, k, Is):
+    x, logits, sgate = _inputs(T, H, E, dtype, seed=T + Is)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=E + 2, seed=E + 1)
+    page = _shared_page(H, Is, dtype, seed=Is)
+    _check(x, logits, pool, slots, k, gated, page, sgate if gated else None,
+           1.0 if gated else 2.5)
+
+
+def test_no_shared_expert_is_scaled_routed():
+    T, H, I, E, k = 16, 256, 128, 8, 2
+    x, logits, _ = _inputs(T, H, E, torch.bfloat16, seed=21)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=22)
+    _check(x, logits, pool, slots, k, False, None, None, 16.0)
+    y1 = fused_moe_shared_forward(x.clone(), logits, pool, slots, k, True, None, None, 1.0,
+                                  inplace=False)
+    y2 = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
+def test_qwen15_moe_shape():
+    """Qwen1.5-MoE-A2.7B block: H 2048, 60 experts of I 1408, top-4 without renormalisation,
+    gated shared expert of I 5632, 64 verify tokens; router logits 2*N(0,1)."""
+    T, H, I, E, k, Is = 64, 2048, 1408, 60, 4, 5632
+    x, logits, sgate = _inputs(T, H, E, torch.bfloat16, seed=31)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, num_slots=E, seed=32)
+    page = _shared_page(H, Is, torch.bfloat16, seed=33)
+    _check(x, logits, pool, slots, k, False, page, sgate, 1.0)
+
+
+@pytest.mark.parametrize("T", [1, 8, 32, 128])
+def test_deepseek_v2_lite_shape(T):
+    """DeepSeek-V2-Lite block: H 2048, 64 experts of I 1408, top-6 without renormalisation,
+    2 shared experts fused into one MLP of I 2816, routed scaling 1.0."""
+    H, I, E, k, Is = 2048, 1408, 64, 6, 2816
+    x, logits, _ = _inputs(T, H, E, torch.bfloat16, seed=40 + T)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, num_slots=E, seed=41)
+    page = _shared_page(H, Is, torch.bfloat16, seed=42)
+    _check(x, logits, pool, slots, k, False, page, None, 1.0)
+
+
+def test_shared_block_deterministic_bitwise():
+    T, H, I, E, k, Is = 48, 256, 256, 8, 2, 512
+    x, logits, sgate = _inputs(T, H, E, torch.bfloat16, seed=51)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=52)
+    page = _shared_page(H, Is, torch.bfloat16, seed=53)
+    outs = [fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page, sgate,
+                                     inplace=False) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+
+
+def _load_block(block, E, H, I, Is, seed):
+    g = torch.Generator().manual_seed(seed)
+    dt = block.gate.weight.dtype
+    with torch.no_grad():
+        block.gate.weight.copy_(torch.randn(block.gate.weight.shape, generator=g) * 0.02)
+        if block.shared_expert_gate is not None:
+            block.shared_expert_gate.weight.copy_(torch.randn((1, H), generator=g) * 0.05)
+    for e in range(E):
+        for name, shape in (("w1", (I, H)), ("w3", (I, H)), ("w2", (H, I))):
+            wt = (torch.randn(shape, generator=g) * 0.02).to(dt)
+            block.experts.weight_loader(block.experts.ws, wt, f"experts.{e}.{name}.weight", name, e)
+    gp, up = (torch.randn((Is, H), generator=g) * 0.02).to(dt), (torch.randn((Is, H), generator=g) * 0.02).to(dt)
+    dp = (torch.randn((H, Is), generator=g) * 0.02).to(dt)
+    block.load_shared_weights(gp, up, dp)
+    block.to(DEV)
+    pool = block.experts.ws.data.to(DEV)
+    set_weight_attrs(block.experts.ws, {"gpu_cache": pool})
+    return pool
+
+
+@pytest.mark.parametrize("kind", ["qwen", "deepseek"])
+def test_block_modules_end_to_end(kind):
+    H, I, E, T = 256, 128, 8, 12
+    if kind == "qwen":
+        block = Qwen2MoeSparseMoeBlock(num_experts=E, top_k=4, hidden_size=H,
+                                       moe_intermediate_size=I, shared_expert_intermediate_size=384,
+                                       params_dtype=torch.bfloat16, tp_size=1)
+        Is = 384
+    else:
+        block = DeepseekV2MoE(n_routed_experts=E, num_experts_per_tok=3, hidden_size=H,
+                              moe_intermediate_size=I, n_shared_experts=2,
+                              routed_scaling_factor=2.0, params_dtype=torch.bfloat16, tp_size=1)
+        Is = 2 * I
+    pool = _load_block(block, E, H, I, Is, seed=61)
+    mapping = torch.arange(E, dtype=torch.int64, device=DEV)
+    x = torch.randn((2, T // 2, H), generator=torch.Generator(device=DEV).manual_seed(62),
+                    device=DEV).to(torch.bfloat16)
+    x_in = x.clone()
+    with torch.no_grad():
+        logits = block.gate(x.view(-1, H))
+        sg = block.shared_expert_gate(x.view(-1, H)) if kind == "qwen" else None
+        y = block(x_in, mapping)
+    torch.cuda.synchronize()
+    assert y.shape == x.shape
+    y_ref, _, _ = _oracle(x.view(-1, H), logits, pool, mapping, block.top_k, False,
+                          block.shared_ws.data, sg, block.routed_scaling_factor)
+    assert max_rel_err(f32_of(y.view(-1, H)), y_ref) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("shared", [False, True])
+def test_hip_graph_replays_match_eager(shared):
+    """The whole call captured in a HIP graph: every replay, with eager work and host
+    synchronisations between replays, equals the eager result bit for bit."""
+    T, H, I, E, k, Is = 20, 256, 128, 8, 2, 256
+    x, logits, sgate = _inputs(T, H, E, torch.bfloat16, seed=71)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=72)
+    page = _shared_page(H, Is, torch.bfloat16, seed=73) if shared else None
+    out = torch.empty_like(x)
+
+    def run():
+        if shared:
+            return fused_moe_shared_forward(x, logits, pool, slots, k, False, page, sgate,
+                                            inplace=False)
+        return fused_moe_forward(x, logits, pool, slots, k, True, inplace=False)
+
+    eager = run()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out.copy_(run())
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        run()  # eager work between replays
+        torch.cuda.synchronize()

@@ -85,8 +85,9 @@ def test_softmax_against_float64():
 
 
 def test_softmax_sum_order_is_the_lane_tree():
-    # 70 experts: lanes 0..5 hold two values each. A sequential sum and the lane tree differ
-    # for these magnitudes; the oracle must follow the tree (lane sums, then halving).
+    # 70 experts: lanes 0..5 hold two values each. A sequential sum, a halving tree and the
+    # lane butterfly differ for these magnitudes; the oracle must follow the butterfly (lane
+    # sums, then lane l + lane l^1, then l^2, ... l^32).
     x = np.full((1, 70), -15.0, dtype=np.float32)
     x[0, 0] = 0.0
     x[0, 64] = -0.5
@@ -96,12 +97,23 @@ def test_softmax_sum_order_is_the_lane_tree():
     lane = pad[:64].copy()
     for i in range(1, 4):
         lane = lane + pad[64 * i:64 * i + 64]
-    h = 32
-    while h:
-        lane = lane[:h] + lane[h:2 * h]
-        h //= 2
-    want = ex[0] * (np.float32(1.0) / lane[0])
+    tree = lane.copy()
+    off = 1
+    while off < 64:  # every lane of the butterfly, explicitly
+        tree = tree + tree[np.arange(64) ^ off]
+        off *= 2
+    assert np.all(tree == tree[0])
+    want = ex[0] * (np.float32(1.0) / tree[0])
     np.testing.assert_array_equal(ref.softmax_probs(x)[0], want)
+    h, halving = 32, lane.copy()
+    while h:
+        halving = halving[:h] + halving[h:2 * h]
+        h //= 2
+    seq = np.float32(0)
+    for v in ex[0]:
+        seq = np.float32(seq + v)
+    # the magnitudes make the three orders distinguishable
+    assert len({float(tree[0]), float(halving[0]), float(seq)}) == 3
 
 
 # --------------------------------------------------------------------------------------- top-k
@@ -278,3 +290,73 @@ def test_invalid_ids_and_slots_contribute_nothing():
     bad[ids[0, 0]] = 1000
     y3 = ref.stack_fused_moe(x, pool, bad, w, ids, ref.F32)
     assert not np.allclose(y3, base)
+
+
+# ------------------------------------------------------------------------ shared-expert blocks
+def _textbook_block(x, w1s, w3s, w2s, w, ids, sg1, sg3, sg2, gate_w=None, scale=1.0):
+    """float64 MoE block with a shared expert: scale * routed + s * W2s(silu(W1s x) * W3s x),
+    s = sigmoid(gate_w . x) or 1."""
+    y = _textbook(x, w1s, w3s, w2s, w, ids) * scale
+    xd = x.astype(np.float64)
+    g, u = xd @ sg1.T.astype(np.float64), xd @ sg3.T.astype(np.float64)
+    d = (g / (1 + np.exp(-g)) * u) @ sg2.T.astype(np.float64)
+    if gate_w is not None:
+        d = d / (1 + np.exp(-(xd @ gate_w.astype(np.float64))))[:, None]
+    return y + d
+
+
+def _shared_mats(rng, H, Is, dtype):
+    mk = lambda shape: ref.round_to((rng.standard_normal(shape) * 0.05).astype(np.float32), dtype)
+    return mk((Is, H)), mk((Is, H)), mk((H, Is))
+
+
+@pytest.mark.parametrize("dtype,rtol", [(ref.F32, 2e-5), (ref.BF16, 3e-2), (ref.F16, 4e-3)])
+@pytest.mark.parametrize("gated", [True, False])
+def test_shared_block_against_textbook(dtype, rtol, gated):
+    rng = np.random.default_rng(21)
+    T, H, I, E, k, Is = 7, 64, 32, 6, 3, 96
+    x, w1s, w3s, w2s, slots, pool, logits = _make_layer(rng, T, H, I, E, k, 8, dtype)
+    s1, s3, s2 = _shared_mats(rng, H, Is, dtype)
+    gw = ref.round_to((rng.standard_normal(H) * 0.2).astype(np.float32), dtype) if gated else None
+    sgl = ref.round_to(x @ gw, dtype) if gated else None
+    scale = 1.0 if gated else 2.5
+    y, w, ids = ref.fused_moe_shared_forward(x, logits, pool, slots, k, False, dtype,
+                                             ref.pack_page(s1, s3, s2), sgl, scale)
+    want = _textbook_block(x, w1s, w3s, w2s, w, ids, s1, s3, s2, gw, scale)
+    err = np.abs(y - want).max() / np.abs(want).max()
+    assert err < rtol, err
+    # a swapped shared gate/up or a dropped gate is far outside the tolerance
+    bad = _textbook_block(x, w1s, w3s, w2s, w, ids, s3, s1, s2, gw, scale)
+    assert np.abs(y - bad).max() / np.abs(bad).max() > 0.05
+    if gated:
+        ungated = _textbook_block(x, w1s, w3s, w2s, w, ids, s1, s3, s2, None, scale)
+        assert np.abs(y - ungated).max() / np.abs(ungated).max() > 0.05
+
+
+def test_shared_block_reductions():
+    """Zero shared page -> the routed result; zero routed pages -> the dense shared MLP;
+    a saturated gate logit -> gate 1 (ungated) or 0 (routed only)."""
+    rng = np.random.default_rng(22)
+    T, H, I, E, k, Is = 6, 64, 32, 4, 2, 64
+    dt = ref.BF16
+    x, w1s, w3s, w2s, slots, pool, logits = _make_layer(rng, T, H, I, E, k, 4, dt)
+    s1, s3, s2 = _shared_mats(rng, H, Is, dt)
+    page = ref.pack_page(s1, s3, s2)
+    routed, _, _ = ref.fused_moe_forward(x, logits, pool, slots, k, False, dt)
+    y0, _, _ = ref.fused_moe_shared_forward(x, logits, pool, slots, k, False, dt,
+                                            np.zeros_like(page), None, 1.0)
+    np.testing.assert_array_equal(y0, routed)
+    dense = ref.shared_expert_mlp(x, page, dt)
+    y1, _, _ = ref.fused_moe_shared_forward(x, logits, np.zeros_like(pool), slots, k, False, dt,
+                                            page, None, 1.0)
+    np.testing.assert_array_equal(y1, dense)
+    g, u = x @ s1.T, x @ s3.T
+    np.testing.assert_allclose(dense, (g / (1 + np.exp(-g)) * u) @ s2.T, rtol=3e-2,
+                               atol=3e-2 * np.abs(dense).max())
+    ungated, _, _ = ref.fused_moe_shared_forward(x, logits, pool, slots, k, False, dt, page, None)
+    hi, _, _ = ref.fused_moe_shared_forward(x, logits, pool, slots, k, False, dt, page,
+                                            np.full(T, 100.0, np.float32))
+    np.testing.assert_array_equal(hi, ungated)
+    lo, _, _ = ref.fused_moe_shared_forward(x, logits, pool, slots, k, False, dt, page,
+                                            np.full(T, -100.0, np.float32))
+    np.testing.assert_array_equal(lo, routed)
