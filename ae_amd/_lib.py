@@ -39,6 +39,14 @@ SIGNATURES = [
      [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,
       _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, ctypes.c_float,
       _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
+    ("smx_add_rmsnorm_gate", ctypes.c_int,
+     [_c_void_p, _c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, ctypes.c_float, _c_void_p,
+      _i64, _c_void_p, _c_void_p]),
+    ("smx_moe_layer_workspace_size", _sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
+    ("smx_moe_layer_forward", ctypes.c_int,
+     [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, ctypes.c_float, _c_void_p, _i64, _i64,
+      _i32, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, ctypes.c_float,
+      _c_void_p, _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

@@ -44,6 +44,8 @@ struct Plan {
   // shared expert (Is > 0)
   int Is = 0, s_splits = 1, s_split_steps = 0, s_tok_groups = 0, s_gateup_blocks = 0, s_down_blocks = 0;
   size_t act_s = 0, part_s = 0;
+  // whole-layer form: router logits and shared-expert gate logits
+  size_t logits = 0, sgl = 0;
 };
 
 // Shape limits shared by the workspace query and the entry points.
@@ -70,7 +72,6 @@ int64_t divisor_at_most(int64_t n, int64_t want) {
   return s;
 }
 
-// Is = intermediate size of the always-active shared expert, 0 when there is none.
 // Limits of the shared expert's intermediate size (the routed limits on I, plus 32-bit
 // offsets into its page and activations).
 int check_shared(int64_t T, int64_t H, int64_t Is, int dtype) {
@@ -83,7 +84,18 @@ int check_shared(int64_t T, int64_t H, int64_t Is, int dtype) {
   return SMX_OK;
 }
 
-Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype, int64_t Is = 0) {
+// Limits of the residual-add + RMSNorm + gate kernel: whole 16-byte vectors per row and one
+// row staged in LDS.
+int check_norm(int64_t H, int dtype) {
+  if (H <= 0 || !valid_dtype(dtype)) return SMX_ERR_INVALID_ARG;
+  if ((H * dtype_bytes(dtype)) % 16 != 0 || H > kNormMaxH) return SMX_ERR_UNSUPPORTED;
+  return SMX_OK;
+}
+
+// Is = intermediate size of the always-active shared expert, 0 when there is none; `layer`
+// adds the buffers of the whole-layer form (router logits, shared-expert gate logits).
+Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype, int64_t Is = 0,
+               bool layer = false) {
   Plan p;
   p.N = static_cast<int>(T * k);
   p.max_active = static_cast<int>(E < p.N ? E : p.N);
@@ -126,6 +138,10 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
   if (Is > 0) {
     p.act_s = o;    o = align_up(o + static_cast<size_t>(eb) * T * Is);
     p.part_s = o;   o = align_up(o + sizeof(float) * static_cast<size_t>(p.s_splits) * T * H);
+  }
+  if (layer) {
+    p.logits = o;   o = align_up(o + static_cast<size_t>(eb) * T * E);
+    p.sgl = o;      o = align_up(o + static_cast<size_t>(eb) * T);
   }
   p.total = o;
   return p;
@@ -377,6 +393,114 @@ int smx_fused_moe_shared_forward(const void* hidden, void* out, int dtype, int64
   return fused_forward(hidden, out, dtype, T, H, router_logits, logits_dtype, E, top_k, renormalize,
                        pool, num_slots, page_elems, expert_to_slot, shared_I, bt, topk_weights_out,
                        topk_ids_out, workspace, workspace_bytes, stream);
+}
+
+int smx_add_rmsnorm_gate(const void* hidden, void* residual, void* normed_out, int dtype, int64_t T,
+                         int64_t H, const void* norm_weight, float eps, const void* gate_weight,
+                         int64_t E, void* router_logits, void* stream) {
+  if (T < 0 || !std::isfinite(eps) || eps < 0.0f) return SMX_ERR_INVALID_ARG;
+  int rc = check_norm(H, dtype);
+  if (rc != SMX_OK) return rc;
+  if (gate_weight && (E <= 0 || !router_logits)) return SMX_ERR_INVALID_ARG;
+  if (gate_weight && E > kMaxExperts) return SMX_ERR_UNSUPPORTED;
+  if (T == 0) return SMX_OK;
+  if (!hidden || !normed_out || !norm_weight) return SMX_ERR_INVALID_ARG;
+  if (!aligned16(hidden) || !aligned16(normed_out) || !aligned16(norm_weight) ||
+      (residual && !aligned16(residual)) || (gate_weight && !aligned16(gate_weight)))
+    return SMX_ERR_MISALIGNED;
+  NormGateArgs a{};
+  a.x = hidden;
+  a.residual = residual;
+  a.xn = normed_out;
+  a.norm_w = norm_weight;
+  a.eps = eps;
+  a.gate_w = gate_weight;
+  a.logits = router_logits;
+  a.T = static_cast<int>(T);
+  a.H = static_cast<int>(H);
+  a.E = gate_weight ? static_cast<int>(E) : 0;
+  a.dtype = dtype;
+  return static_cast<int>(launch_norm_gate(a, static_cast<hipStream_t>(stream)));
+}
+
+size_t smx_moe_layer_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
+                                    int64_t shared_I, int dtype) {
+  if (check_shape(T, H, I, E, top_k, dtype) != SMX_OK || check_shared(T, H, shared_I, dtype) != SMX_OK ||
+      check_norm(H, dtype) != SMX_OK)
+    return 0;
+  return make_plan(T, H, I, E, top_k, dtype, shared_I, true).total;
+}
+
+int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, int64_t H,
+                          const void* norm_weight, float eps, const void* gate_weight, int64_t E,
+                          int64_t top_k, int renormalize, const void* pool, int64_t num_slots,
+                          int64_t page_elems, const int64_t* expert_to_slot,
+                          const void* shared_page, int64_t shared_I,
+                          const void* shared_gate_weight, float routed_scaling_factor,
+                          void* router_logits_out, float* topk_weights_out,
+                          int32_t* topk_ids_out, void* workspace, size_t workspace_bytes,
+                          void* stream) {
+  if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype) ||
+      !std::isfinite(eps) || eps < 0.0f || !std::isfinite(routed_scaling_factor))
+    return SMX_ERR_INVALID_ARG;
+  if (shared_I < 0 || (shared_I == 0) != (shared_page == nullptr) ||
+      (shared_I == 0 && shared_gate_weight != nullptr))
+    return SMX_ERR_INVALID_ARG;
+  if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
+  int64_t I = 0;
+  int rc = check_pool(hidden, hidden, pool, num_slots, page_elems, expert_to_slot, H, dtype, &I);
+  if (rc != SMX_OK) return rc;
+  rc = check_shape(T, H, I, E, top_k, dtype);
+  if (rc != SMX_OK) return rc;
+  rc = check_shared(T, H, shared_I, dtype);
+  if (rc != SMX_OK) return rc;
+  rc = check_norm(H, dtype);
+  if (rc != SMX_OK) return rc;
+  if (!residual || !norm_weight || !gate_weight || !workspace) return SMX_ERR_INVALID_ARG;
+  if (!aligned16(residual) || !aligned16(norm_weight) || !aligned16(gate_weight) ||
+      (shared_page && !aligned16(shared_page)) ||
+      (shared_gate_weight && !aligned16(shared_gate_weight)))
+    return SMX_ERR_MISALIGNED;
+  const Plan p = make_plan(T, H, I, E, top_k, dtype, shared_I, true);
+  if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
+  char* b = static_cast<char*>(workspace);
+  float* w = topk_weights_out ? topk_weights_out : reinterpret_cast<float*>(b + p.w);
+  int32_t* ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t*>(b + p.ids);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mark(0, s);
+  NormGateArgs g{};
+  g.x = hidden;
+  g.residual = residual;
+  g.xn = hidden;
+  g.norm_w = norm_weight;
+  g.eps = eps;
+  g.gate_w = gate_weight;
+  g.sgate_w = shared_gate_weight;
+  g.logits = router_logits_out ? router_logits_out : static_cast<void*>(b + p.logits);
+  g.sgate_logits = b + p.sgl;
+  g.topk_w = w;
+  g.topk_ids = ids;
+  g.T = static_cast<int>(T);
+  g.H = static_cast<int>(H);
+  g.E = static_cast<int>(E);
+  g.k = static_cast<int>(top_k);
+  g.renorm = renormalize;
+  g.dtype = dtype;
+  hipError_t err = launch_norm_gate(g, s);
+  if (err != hipSuccess) return static_cast<int>(err);
+  err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k), 0,
+                     nullptr, nullptr, ids, expert_to_slot, num_slots, carve(p, workspace), s);
+  if (err != hipSuccess) return static_cast<int>(err);
+  mark(1, s);
+  BlockTerms bt;
+  bt.block = shared_I > 0 || routed_scaling_factor != 1.0f;
+  bt.scale = routed_scaling_factor;
+  bt.shared_page = shared_page;
+  bt.sgate = shared_gate_weight ? b + p.sgl : nullptr;
+  bt.sgate_dtype = dtype;
+  return run_experts(p, dtype, hidden, hidden, T, H, I, E, top_k, pool, num_slots, page_elems,
+                     expert_to_slot, w, ids, workspace, s, bt);
 }
 
 int smx_set_profile_events(void* const* events, int count) {

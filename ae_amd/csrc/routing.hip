@@ -541,6 +541,151 @@ __global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
+// Post-attention residual add + RMSNorm + router gate, one workgroup per token.
+//   s        = x + residual                      (fp32)
+//   residual = round(s)
+//   xn       = round(s * (1 / sqrt(sum(s^2) / H + eps)) * norm_w)
+//   logits   = round(xn . gate_w[e]) for every expert (fp32 accumulation), and the
+//              shared-expert gate row; then, optionally, the token's top-k from the rounded
+//              logits (exactly what the routing kernels compute from stored logits).
+// Reference: RMSNorm.forward_native (specmoe/layers/layernorm.py:36-52; forward_cuda at :23-33
+// calls sglang's fused_add_rmsnorm with the same semantics), the bias-free router gate of
+// MixtralMoE (specmoe/models/mixtral.py:84-91, applied at :111), called in order at
+// specmoe/models/mixtral.py:310-313.
+// ---------------------------------------------------------------------------------------
+// RB = router rows per batch (8, 16 or 32).
+template <int DT, int G, int PL, int RB>
+__global__ __launch_bounds__(kNormThreads) void norm_gate_kernel(NormGateArgs a) {
+  static_assert(RB == 8 || RB == 16 || RB == 32, "P = 256 / RB lanes reduce a row");
+  using S = typename Elem<DT>::S;
+  constexpr int V = 16 / static_cast<int>(sizeof(S));  // elements per 16-byte vector
+  __shared__ float sb[kNormMaxH];
+  __shared__ float red[kNormWaves];
+  __shared__ float lg[kMaxExperts];
+  __shared__ RankScratch rs;
+  const int t = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = tid / kWave;
+  const int H = a.H;
+  const int nv = H / V;
+  const int64_t row = static_cast<int64_t>(t) * H;
+  const u32x4* xv = reinterpret_cast<const u32x4*>(static_cast<const S*>(a.x) + row);
+  u32x4* rv = a.residual ? reinterpret_cast<u32x4*>(static_cast<S*>(a.residual) + row) : nullptr;
+  u32x4* ov = reinterpret_cast<u32x4*>(static_cast<S*>(a.xn) + row);
+  const u32x4* wv = static_cast<const u32x4*>(a.norm_w);
+
+  float ss = 0.0f;
+  for (int c = tid; c < nv; c += kNormThreads) {
+    u32x4 xr = xv[c];
+    float f[V];
+    const S* xe = reinterpret_cast<const S*>(&xr);
+#pragma unroll
+    for (int i = 0; i < V; ++i) f[i] = Elem<DT>::to_f32(xe[i]);
+    if (rv) {
+      u32x4 rr = rv[c];
+      S* re = reinterpret_cast<S*>(&rr);
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        f[i] = f[i] + Elem<DT>::to_f32(re[i]);
+        re[i] = Elem<DT>::from_f32(f[i]);
+      }
+      rv[c] = rr;
+    }
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      sb[c * V + i] = f[i];
+      ss = ss + f[i] * f[i];
+    }
+  }
+  ss = group_reduce<kWave>(ss, [](float p, float q) { return p + q; });
+  if (lane == 0) red[wave] = ss;
+  __syncthreads();
+  float tot = red[0];
+#pragma unroll
+  for (int w = 1; w < kNormWaves; ++w) tot = tot + red[w];
+  const float rcp = 1.0f / sqrtf(tot / static_cast<float>(H) + a.eps);
+  for (int c = tid; c < nv; c += kNormThreads) {
+    u32x4 wr = wv[c];
+    const S* we = reinterpret_cast<const S*>(&wr);
+    u32x4 o;
+    S* oe = reinterpret_cast<S*>(&o);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float v = Elem<DT>::round((sb[c * V + i] * rcp) * Elem<DT>::to_f32(we[i]));
+      oe[i] = Elem<DT>::from_f32(v);
+      sb[c * V + i] = v;
+    }
+    ov[c] = o;
+  }
+  if (!a.gate_w) return;
+  __syncthreads();
+
+  // Router gate, RB rows at a time (row E is the shared-expert gate): P = 256 / RB adjacent
+  // threads take one row, thread `part` the vectors part, part + P, ... with 8 loads in
+  // flight; the P partial dots are summed by a butterfly (fixed order). Threads past the last
+  // row reload it and drop the sum.
+  constexpr int P = kNormThreads / RB;
+  constexpr int kInFlight = 8;
+  const int rows = a.E + (a.sgate_w ? 1 : 0);
+  const int rr = tid / P, part = tid % P;
+  for (int e0 = 0; e0 < rows; e0 += RB) {
+    const int e = min(e0 + rr, rows - 1);
+    const u32x4* gr = reinterpret_cast<const u32x4*>(
+        e < a.E ? static_cast<const S*>(a.gate_w) + static_cast<int64_t>(e) * H : static_cast<const S*>(a.sgate_w));
+    float acc = 0.0f;
+    int c = part;
+    for (; c + (kInFlight - 1) * P < nv; c += kInFlight * P) {
+      u32x4 g[kInFlight];
+#pragma unroll
+      for (int u = 0; u < kInFlight; ++u) g[u] = gr[c + u * P];
+#pragma unroll
+      for (int u = 0; u < kInFlight; ++u) {
+        const S* ge = reinterpret_cast<const S*>(&g[u]);
+#pragma unroll
+        for (int i = 0; i < V; ++i) acc += sb[(c + u * P) * V + i] * Elem<DT>::to_f32(ge[i]);
+      }
+    }
+    for (; c < nv; c += P) {
+      const u32x4 g = gr[c];
+      const S* ge = reinterpret_cast<const S*>(&g);
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc += sb[c * V + i] * Elem<DT>::to_f32(ge[i]);
+    }
+    acc = group_reduce<P>(acc, [](float x0, float x1) { return x0 + x1; });
+    if (part == 0 && e0 + rr < rows) {
+      const float lv = Elem<DT>::round(acc);
+      if (e < a.E) {
+        lg[e] = lv;
+        static_cast<S*>(a.logits)[static_cast<int64_t>(t) * a.E + e] = Elem<DT>::from_f32(lv);
+      } else {
+        static_cast<S*>(a.sgate_logits)[t] = Elem<DT>::from_f32(lv);
+      }
+    }
+  }
+  if (!a.topk_w) return;
+  __syncthreads();
+  if (wave != 0) return;
+  // every lane group of the wave runs the same token; group 0 writes
+  float v[1][PL];
+  const int j = lane % G;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) v[0][i] = (j + G * i < a.E) ? lg[j + G * i] : -__builtin_inff();
+  float w[1];
+  int id[1], slot[1];
+  if constexpr (PL == 1) {
+    group_topk_rank<G, 1>(v, a.E, a.k, a.renorm != 0, rs, w, id, slot);
+  } else {
+    group_topk_softmax<G, PL, 1>(v, a.E, a.k, a.renorm != 0, w, id);
+    slot[0] = j < a.k ? j : -1;
+  }
+  if (lane < G && slot[0] >= 0) {
+    a.topk_w[static_cast<int64_t>(t) * a.k + slot[0]] = w[0];
+    a.topk_ids[static_cast<int64_t>(t) * a.k + slot[0]] = id[0];
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Host-side launchers
 // ---------------------------------------------------------------------------------------
 // Largest T*E whose top-k runs inside the single routing workgroup.
@@ -657,6 +802,35 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
     case kF32: route_launch_g<kF32>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
     case kF16: route_launch_g<kF16>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
     default: route_launch_g<kBF16>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+  }
+  return hipGetLastError();
+}
+
+template <int DT, int G, int PL, int RB>
+static void norm_gate_launch(const NormGateArgs& a, hipStream_t s) {
+  norm_gate_kernel<DT, G, PL, RB><<<a.T, kNormThreads, 0, s>>>(a);
+}
+
+// Top-k lane groups from E; router rows per batch from the row count (E + shared-gate row).
+template <int DT>
+static void norm_gate_launch_g(const NormGateArgs& a, hipStream_t s) {
+  const int rows = a.E + (a.sgate_w ? 1 : 0);
+  const int g = a.topk_w ? group_for(a.E) : 8;
+  if (g == 8 && rows <= 8) norm_gate_launch<DT, 8, 1, 8>(a, s);
+  else if (g == 8 && rows <= 16) norm_gate_launch<DT, 8, 1, 16>(a, s);
+  else if (g == 8) norm_gate_launch<DT, 8, 1, 32>(a, s);  // norm only or gate without top-k
+  else if (g == 16 && rows <= 16) norm_gate_launch<DT, 16, 1, 16>(a, s);
+  else if (g == 16) norm_gate_launch<DT, 16, 1, 32>(a, s);
+  else if (g == 32) norm_gate_launch<DT, 32, 1, 32>(a, s);
+  else if (a.E <= kWave) norm_gate_launch<DT, 64, 1, 32>(a, s);
+  else norm_gate_launch<DT, 64, kMaxExpertsPerLane, 32>(a, s);
+}
+
+hipError_t launch_norm_gate(const NormGateArgs& a, hipStream_t s) {
+  switch (a.dtype) {
+    case kF32: norm_gate_launch_g<kF32>(a, s); break;
+    case kF16: norm_gate_launch_g<kF16>(a, s); break;
+    default: norm_gate_launch_g<kBF16>(a, s); break;
   }
   return hipGetLastError();
 }

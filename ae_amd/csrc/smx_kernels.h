@@ -82,6 +82,28 @@ struct CombineArgs {
   int sgate_dtype;
 };
 
+// Post-attention residual add + RMSNorm + router gate (+ shared-expert gate row, + top-k).
+constexpr int kNormThreads = 256;
+constexpr int kNormWaves = kNormThreads / kWave;
+constexpr int kNormMaxH = 16384;  // one token's fp32 row is staged in LDS
+
+struct NormGateArgs {
+  const void* x;          // [T, H] hidden states
+  void* residual;         // [T, H] in/out (null: no residual add)
+  void* xn;               // [T, H] normalized out (may alias x)
+  const void* norm_w;     // [H]
+  float eps;
+  const void* gate_w;     // [E, H] router gate (null: norm only)
+  const void* sgate_w;    // [H] shared-expert gate row (null: none)
+  void* logits;           // [T, E] router logits out (dtype)
+  void* sgate_logits;     // [T] shared-expert gate logits out (dtype)
+  float* topk_w;          // [T, k] top-k weights out (null: no top-k)
+  int32_t* topk_ids;      // [T, k]
+  int T, H, E, k, renorm, dtype;
+};
+
+hipError_t launch_norm_gate(const NormGateArgs& a, hipStream_t s);
+
 hipError_t launch_topk_softmax(const void* logits, int ldt, int T, int E, int k, int renorm,
                                float* w, int32_t* ids, hipStream_t s);
 hipError_t launch_align(const int32_t* ids, int N, int E, int bm, int32_t* sorted_ids,

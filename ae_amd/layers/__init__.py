@@ -2,7 +2,9 @@
 from .FusedMoE import FusedMoE, UnquantizedFusedMoEMethod, set_weight_attrs
 from .fused_moe_kernel import (fused_moe_forward, fused_moe_shared_forward, moe_align_block_size,
                                stack_fused_moe)
+from .layernorm import RMSNorm, add_rmsnorm_gate
 from .mixtral_moe import MixtralMoE
+from .moe_layer import PostAttentionMoE, moe_layer_forward
 from .shared_moe import DeepseekV2MoE, Qwen2MoeSparseMoeBlock, SharedExpertMoE
 from .topk import fused_topk, select_experts
 
@@ -10,4 +12,5 @@ __all__ = [
     "FusedMoE", "UnquantizedFusedMoEMethod", "set_weight_attrs", "fused_moe_forward",
     "fused_moe_shared_forward", "moe_align_block_size", "stack_fused_moe", "MixtralMoE",
     "SharedExpertMoE", "Qwen2MoeSparseMoeBlock", "DeepseekV2MoE", "fused_topk", "select_experts",
+    "RMSNorm", "add_rmsnorm_gate", "PostAttentionMoE", "moe_layer_forward",
 ]

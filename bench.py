@@ -16,8 +16,10 @@ renormalisation. --layers N runs a stack of N layers with distinct weights per s
 each step from a HIP graph.
 
 Prints one JSON line per token count: value = algorithmic HBM bytes / measured time (GB/s),
-plus us per step, the roofline of the dominant kernel (gate/up) timed live with HIP events
-on the launch stream, and the CPU oracle timed on a bounded sample of the same workload.
+with us per step timed by HIP events around the K steps only; then the roofline of the
+dominant kernel (gate/up), timed in a second pass of K steps with HIP events that the
+library records on the launch stream around each kernel; and the CPU oracle timed on a
+bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu]
     python bench.py --workload dsv2lite --layers 26 --sweep-tokens 1,2,4,8,16,32,64,128 --no-cpu
@@ -63,6 +65,10 @@ def parse():
     ap.add_argument("--topk", type=int, default=None)
     ap.add_argument("--layers", type=int, default=1, help="layers with distinct weights per step")
     ap.add_argument("--graph", action="store_true", help="replay each step from a HIP graph")
+    ap.add_argument("--layer", action="store_true",
+                    help="time the whole post-attention layer call (residual add + RMSNorm + "
+                         "router gate + top-k + MoE, smx_moe_layer_forward) and, beside it, the "
+                         "unfused sequence (norm kernel, torch gate GEMM, MoE call)")
     ap.add_argument("--zipf", type=float, default=1.2,
                     help="Mixtral gate bias exponent (0 = unbiased)")
     ap.add_argument("--rotate", type=int, default=2, help="copies of the weights rotated per step")
@@ -151,19 +157,39 @@ def run_tokens(args, wl, T, layers, L, dev):
         raise SystemExit(f"unsupported shape T={T} H={H} I={I} E={E} k={k} shared={Is}")
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     renorm = 1 if wl["renormalize"] else 0
+    if args.layer:
+        residual = torch.randn((T, H), generator=g, device=dev).to(dtype)
+        norm_w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(dtype)
+        gate_w = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(dtype)
+        sgate_w = (torch.randn(H, generator=g, device=dev) * 0.02).to(dtype) if wl["gated"] else None
+        lbytes = L.smx_moe_layer_workspace_size(T, H, I, E, k, Is, _lib.SMX_BF16)
+        lws = torch.empty(lbytes, dtype=torch.uint8, device=dev)
 
     def call(layer, c, stream):
+        if args.layer:
+            sp = ctypes.c_void_p(stream.cuda_stream)
+            rc = L.smx_moe_layer_forward(
+                ptr(x), ptr(residual), _lib.SMX_BF16, T, H, ptr(norm_w), 1e-5, ptr(gate_w), E, k,
+                renorm, ptr(layer.pools[c]), E, 3 * I * H, ptr(slots),
+                ptr(layer.shared[c] if Is else None), Is, ptr(sgate_w), 1.0, None, ptr(w_out),
+                ptr(ids_out), ptr(lws), lbytes, sp)
+            _lib.check("smx_moe_layer_forward", rc)
+            return
+        call_moe(layer, c, stream)
+
+    def call_moe(layer, c, stream, lg=None):
         sp = ctypes.c_void_p(stream.cuda_stream)
         pool = layer.pools[c]
+        lg = logits if lg is None else lg
         if Is:
             rc = L.smx_fused_moe_shared_forward(
-                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(logits), _lib.SMX_BF16, E, k, renorm,
+                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(lg), _lib.SMX_BF16, E, k, renorm,
                 ptr(pool), E, 3 * I * H, ptr(slots), ptr(layer.shared[c]), Is, ptr(sgate), 1.0,
                 ptr(w_out), ptr(ids_out), ptr(ws), nbytes, sp)
             _lib.check("smx_fused_moe_shared_forward", rc)
         else:
             rc = L.smx_fused_moe_forward(
-                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(logits), _lib.SMX_BF16, E, k, renorm,
+                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(lg), _lib.SMX_BF16, E, k, renorm,
                 ptr(pool), E, 3 * I * H, ptr(slots), ptr(w_out), ptr(ids_out), ptr(ws), nbytes, sp)
             _lib.check("smx_fused_moe_forward", rc)
 
@@ -184,6 +210,8 @@ def run_tokens(args, wl, T, layers, L, dev):
     weight_bytes = len(active) * 3 * H * I * es + 3 * H * Is * es
     layer_bytes = (weight_bytes + 2 * T * H * es + T * E * es + T * k * 8
                    + (T * es if wl["gated"] else 0))
+    if args.layer:  # residual read + write, the in-place normalized states, norm and gate weights
+        layer_bytes += 3 * T * H * es + H * es + E * H * es + (H * es if wl["gated"] else 0)
     step_bytes = layer_bytes * len(layers)
     gateup_bytes = ((len(active) * 2 * H * I + 2 * H * Is) * es + T * H * es
                     + (T * k * I + T * Is) * es)
@@ -210,15 +238,8 @@ def run_tokens(args, wl, T, layers, L, dev):
             graphs[c].replay()
         torch.cuda.synchronize()
 
-    # ---- timed region: K steps; per-kernel HIP events on the launch stream (eager, 1 layer)
-    per_kernel = graphs is None and len(layers) == 1
-    ev = handles = None
-    if per_kernel:
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
-        for row in ev:  # materialise the event handles
-            for e_ in row:
-                e_.record(stream)
-        handles = [(ctypes.c_void_p * 5)(*[e_.cuda_event for e_ in row]) for row in ev]
+    # ---- timed region: K steps, HIP events only before and after (no per-kernel events: each
+    # event recorded between kernels costs the stream several microseconds)
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -228,17 +249,49 @@ def run_tokens(args, wl, T, layers, L, dev):
         if graphs is not None:
             graphs[i % copies].replay()
         else:
-            if per_kernel:
-                _lib.check("smx_set_profile_events", L.smx_set_profile_events(handles[i], 5))
             step(i)
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    if per_kernel:
-        _lib.check("smx_set_profile_events", L.smx_set_profile_events(None, 0))
-
     ms_step = t_start.elapsed_time(t_end) / args.steps
     us_step = 1000.0 * ms_step
+
+    # ---- stage pass (eager, 1 layer): the same steps again with HIP events recorded by the
+    # library on the launch stream before routing and after each kernel
+    per_kernel = graphs is None and len(layers) == 1
+    ev = None
+    if per_kernel:
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+        for row in ev:  # materialise the event handles
+            for e_ in row:
+                e_.record(stream)
+        handles = [(ctypes.c_void_p * 5)(*[e_.cuda_event for e_ in row]) for row in ev]
+        torch.cuda.synchronize()
+        for i in range(args.steps):
+            _lib.check("smx_set_profile_events", L.smx_set_profile_events(handles[i], 5))
+            step(i)
+        torch.cuda.synchronize()
+        _lib.check("smx_set_profile_events", L.smx_set_profile_events(None, 0))
+    unfused_us = None
+    if args.layer:
+        from ae_amd.layers import add_rmsnorm_gate
+
+        def unfused(i):
+            add_rmsnorm_gate(x, residual, norm_w, 1e-5)
+            lg = torch.nn.functional.linear(x, gate_w)
+            call_moe(layers[0], i % copies, stream, lg)
+
+        for i in range(args.warmup):
+            unfused(i)
+        u0 = torch.cuda.Event(enable_timing=True)
+        u1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        u0.record(stream)
+        for i in range(args.steps):
+            unfused(i)
+        u1.record(stream)
+        torch.cuda.synchronize()
+        unfused_us = 1000.0 * u0.elapsed_time(u1) / args.steps
     value = step_bytes / (us_step * 1e-6) / 1e9
     config = {
         "workload": f"{wl['title']}, {T} tokens" + (f", {len(layers)} layers" if len(layers) > 1 else ""),
@@ -252,9 +305,12 @@ def run_tokens(args, wl, T, layers, L, dev):
         config["layers"] = len(layers)
     if graphs is not None:
         config["hip_graph"] = True
+    if args.layer:
+        config["layer_call"] = "residual add + RMSNorm + router gate + top-k + MoE"
     out = {
-        "metric": METRIC if args.workload == "mixtral" else
-        f"MoE {'stack' if len(layers) > 1 else 'layer'} us/verify-step + achieved HBM GB/s, {args.workload}",
+        "metric": METRIC if args.workload == "mixtral" and not args.layer else
+        f"{'post-attention layer call (add+RMSNorm+gate+top-k+MoE)' if args.layer else 'MoE'} "
+        f"{'stack' if len(layers) > 1 else 'layer'} us/verify-step + achieved HBM GB/s, {args.workload}",
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -275,6 +331,8 @@ def run_tokens(args, wl, T, layers, L, dev):
         "roofline": None,
         "cpu_baseline": None,
     }
+    if args.layer:
+        out["unfused_us_per_step"] = round(unfused_us, 2)
     if per_kernel:
         stage = [0.0] * 4
         for row in ev:

@@ -150,6 +150,49 @@ int smx_fused_moe_shared_forward(const void* hidden, void* out, int dtype, int64
                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Post-attention residual add + RMSNorm + router gate in one kernel (one workgroup per token):
+ *   s = hidden + residual (fp32; residual == NULL: s = hidden)
+ *   residual      = round(s)                                      (in place, when given)
+ *   normed_out    = round(s * (1 / sqrt(mean(s^2) + eps)) * norm_weight)   (may == hidden)
+ *   router_logits = round(normed_out . gate_weight^T)   [T, E] of dtype, fp32 accumulation
+ * gate_weight NULL: norm only (E and router_logits ignored).
+ * Replaces RMSNorm.forward with a residual (specmoe/layers/layernorm.py:23-52; sglang's
+ * fused_add_rmsnorm at :31) followed by MixtralMoE's router gate (specmoe/models/mixtral.py:
+ * 84-91, 111), as called at specmoe/models/mixtral.py:310-313.
+ * Limits: H * element size a multiple of 16 bytes, H <= 16384, E <= 256.
+ */
+int smx_add_rmsnorm_gate(const void* hidden, void* residual, void* normed_out, int dtype,
+                         int64_t T, int64_t H, const void* norm_weight, float eps,
+                         const void* gate_weight, int64_t E, void* router_logits, void* stream);
+
+/* Bytes of workspace smx_moe_layer_forward needs. */
+size_t smx_moe_layer_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
+                                    int64_t shared_I, int dtype);
+
+/*
+ * The post-attention half of a decoder layer in one call: smx_add_rmsnorm_gate (with the
+ * token's top-k computed in the same kernel from the rounded logits) and then the MoE block
+ * on the normalized states, written back into `hidden`:
+ *   residual <- round(hidden + residual);  x = RMSNorm(...);  hidden <- MoE(x)
+ * where MoE is smx_fused_moe_forward, or smx_fused_moe_shared_forward's block form when
+ * shared_I > 0 or routed_scaling_factor != 1 (shared_gate_weight [H] gives the shared-expert
+ * gate logit as one more row of the router gate; NULL: ungated).
+ * Replaces MixtralDecoderLayer's post-attention step (specmoe/models/mixtral.py:310-313:
+ * post_attention_layernorm then block_sparse_moe -> MixtralMoE.forward :106-115 ->
+ * FusedMoE.forward, specmoe/layers/FusedMoE.py:508-532).
+ *   router_logits_out [T, E] dtype, topk_weights_out / topk_ids_out [T, top_k]: optional.
+ */
+int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, int64_t H,
+                          const void* norm_weight, float eps, const void* gate_weight, int64_t E,
+                          int64_t top_k, int renormalize,
+                          const void* pool, int64_t num_slots, int64_t page_elems,
+                          const int64_t* expert_to_slot,
+                          const void* shared_page, int64_t shared_I,
+                          const void* shared_gate_weight, float routed_scaling_factor,
+                          void* router_logits_out, float* topk_weights_out, int32_t* topk_ids_out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
  * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
  * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and

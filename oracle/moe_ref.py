@@ -19,6 +19,9 @@ A plain numpy restatement of the reference's arithmetic:
             :248, is not reproduced).
   page      FusedMoE.weight_loader, specmoe/layers/FusedMoE.py:485-505: one page per expert,
             [W1 (I x H) | W3 (I x H) | W2 (H x I)].
+  norm      RMSNorm.forward_native, specmoe/layers/layernorm.py:36-52 (residual add in fp32,
+            mean of squares, x * rsqrt(var + eps) * weight rounded once); router gate
+            round(x W_g^T), specmoe/models/mixtral.py:84-91; called in order at :310-313.
   shared    no reference code (the reference serves only Mixtral). The MoE blocks of the
             public Qwen1.5-MoE / Qwen2-MoE and DeepSeek-V2 architectures, with the rounding
             points of their unfused layers: shared MLP d = round(round(silu(round(x W1s^T)) *
@@ -319,3 +322,49 @@ def fused_moe_shared_forward(x, router_logits, pool, slots, top_k: int, renormal
             d = round_to(s[:, None] * d, dtype)
         y = round_to(y + d, dtype)
     return y, w, ids
+
+
+# ---------------------------------------------------------------------------------------------
+# post-attention residual add + RMSNorm + router gate; the whole post-attention layer half
+# ---------------------------------------------------------------------------------------------
+def add_rmsnorm(x, residual, weight, eps: float, dtype: str):
+    """RMSNorm.forward_native (specmoe/layers/layernorm.py:36-52) -> (normed, new_residual):
+    s = fp32(x) [+ fp32(residual)], new_residual = round(s) (None without a residual),
+    normed = round((s * (1 / sqrt(mean(s^2) + eps))) * weight). The mean of squares is taken
+    exactly (float64) and rounded to fp32; the kernel's fp32 summation may differ from it in
+    the last bits, so normed values agree to one rounding step."""
+    s = to_f32(x, dtype)
+    new_res = None
+    if residual is not None:
+        s = (s + to_f32(residual, dtype)).astype(np.float32)
+        new_res = round_to(s, dtype)
+    H = s.shape[-1]
+    var = (np.square(s.astype(np.float64)).sum(axis=-1, keepdims=True) / H).astype(np.float32)
+    rcp = (_f32(1.0) / np.sqrt(var + _f32(eps))).astype(np.float32)
+    w = to_f32(weight, dtype).reshape(1, -1)
+    return round_to((s * rcp) * w, dtype), new_res
+
+
+def router_logits(xn, gate_weight, dtype: str):
+    """The bias-free router gate (specmoe/models/mixtral.py:84-91): round(xn . W^T), fp32
+    accumulation."""
+    return round_to(to_f32(xn, dtype) @ to_f32(gate_weight, dtype).T, dtype)
+
+
+def moe_layer_forward(x, residual, norm_weight, eps: float, gate_weight, pool, slots, top_k: int,
+                      renormalize: bool, dtype: str, shared_page=None, shared_gate_weight=None,
+                      routed_scaling_factor: float = 1.0, logits=None, shared_gate_logits=None):
+    """Post-attention half of a MoE decoder layer (specmoe/models/mixtral.py:310-313) ->
+    (y, new_residual, router_logits, topk_weights, topk_ids). `logits` / `shared_gate_logits`
+    override the gate outputs (to route on given logit bits)."""
+    xn, new_res = add_rmsnorm(x, residual, norm_weight, eps, dtype)
+    lg = router_logits(xn, gate_weight, dtype) if logits is None else np.asarray(logits, np.float32)
+    sgl = shared_gate_logits
+    if sgl is None and shared_gate_weight is not None:
+        sgl = router_logits(xn, np.asarray(shared_gate_weight).reshape(1, -1), dtype).reshape(-1)
+    if shared_page is None and routed_scaling_factor == 1.0:
+        y, w, ids = fused_moe_forward(xn, lg, pool, slots, top_k, renormalize, dtype)
+    else:
+        y, w, ids = fused_moe_shared_forward(xn, lg, pool, slots, top_k, renormalize, dtype,
+                                             shared_page, sgl, routed_scaling_factor)
+    return y, new_res, lg, w, ids

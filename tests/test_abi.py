@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 10, names
+    assert len(names) == 13, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -153,3 +153,51 @@ def test_shared_forward_rejects_before_launch():
     assert _shared(sI=100) == _lib.SMX_ERR_UNSUPPORTED                   # not a multiple of 128
     assert _shared(wsb=16) == _lib.SMX_ERR_WORKSPACE
     assert _shared(T=0) == _lib.SMX_OK
+
+
+def test_norm_gate_rejects_before_launch():
+    f = L.smx_add_rmsnorm_gate
+    #       hidden res out dt T  H    normw eps   gate E  logits stream
+    base = [A, A, A, 2, 4, 256, A, 1e-6, A, 8, A, VP(0)]
+
+    def call(**kw):
+        a = list(base)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return f(*a)
+    assert call(a3=7) == _lib.SMX_ERR_INVALID_ARG              # bad dtype
+    assert call(a5=100) == _lib.SMX_ERR_UNSUPPORTED            # 200 bytes: not whole 16-byte vectors
+    assert call(a5=32768) == _lib.SMX_ERR_UNSUPPORTED          # above the LDS-staged row limit
+    assert call(a7=-1.0) == _lib.SMX_ERR_INVALID_ARG           # negative eps
+    assert call(a7=float("nan")) == _lib.SMX_ERR_INVALID_ARG
+    assert call(a9=0) == _lib.SMX_ERR_INVALID_ARG              # gate without experts
+    assert call(a10=VP(0)) == _lib.SMX_ERR_INVALID_ARG         # gate without a logits buffer
+    assert call(a9=300) == _lib.SMX_ERR_UNSUPPORTED
+    assert call(a0=VP(0x10008)) == _lib.SMX_ERR_MISALIGNED
+    assert call(a0=VP(0)) == _lib.SMX_ERR_INVALID_ARG
+    assert call(a4=0) == _lib.SMX_OK
+
+
+def test_layer_forward_rejects_before_launch():
+    f = L.smx_moe_layer_forward
+    #       hid res dt T H    nw eps  gw E k ren pool slots page e2s spage sI sgw scale lg w ids ws wsb stream
+    base = [A, A, 2, 4, 256, A, 1e-6, A, 4, 2, 1, A, 4, 3 * 256 * 256, A, VP(0), 0, VP(0), 1.0,
+            VP(0), VP(0), VP(0), A, 1 << 30, VP(0)]
+
+    def call(**kw):
+        a = list(base)
+        for i, v in kw.items():
+            a[int(i[1:])] = v
+        return f(*a)
+    assert call(a9=5) == _lib.SMX_ERR_INVALID_ARG               # top_k > E
+    assert call(a16=256) == _lib.SMX_ERR_INVALID_ARG            # shared I without a page
+    assert call(a17=A) == _lib.SMX_ERR_INVALID_ARG              # shared gate without an expert
+    assert call(a18=float("inf")) == _lib.SMX_ERR_INVALID_ARG
+    assert call(a1=VP(0)) == _lib.SMX_ERR_INVALID_ARG           # the layer form needs a residual
+    assert call(a7=VP(0)) == _lib.SMX_ERR_INVALID_ARG           # and a router gate
+    assert call(a1=VP(0x10008)) == _lib.SMX_ERR_MISALIGNED
+    assert call(a23=16) == _lib.SMX_ERR_WORKSPACE
+    assert call(a3=0) == _lib.SMX_OK
+    assert L.smx_moe_layer_workspace_size(32, 4096, 14336, 8, 2, 0, 2) > \
+        L.smx_moe_workspace_size(32, 4096, 14336, 8, 2, 2)
+    assert L.smx_moe_layer_workspace_size(32, 32768, 14336, 8, 2, 0, 2) == 0  # H above the norm limit

@@ -1,0 +1,187 @@
+"""GPU parity of the residual-add + RMSNorm + router-gate kernel (smx_add_rmsnorm_gate) and of
+the whole post-attention layer call (smx_moe_layer_forward) against the oracle, through the
+C ABI."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as ref
+from ae_amd.layers import (MixtralMoE, PostAttentionMoE, Qwen2MoeSparseMoeBlock, RMSNorm,
+                           add_rmsnorm_gate, moe_layer_forward, set_weight_attrs)
+from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _rand(shape, dtype, seed, scale=1.0):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    return (torch.randn(shape, generator=g, device=DEV) * scale).to(dtype)
+
+
+def _check_normed(a: torch.Tensor, b: np.ndarray, dtype) -> None:
+    """Normalized states agree to one rounding step of a 16-bit type (the scale 1/rms may
+    differ in its last fp32 bits between two summation orders); fp32 outputs carry that
+    difference directly, so they are compared to a relative bound instead."""
+    if dtype == torch.float32:
+        err = np.abs(f32_of(a).astype(np.float64) - b) / np.maximum(np.abs(b), 1e-30)
+        assert err.max() <= 2e-6, err.max()
+        return
+    ulp = _ulps(a, b, dtype)
+    assert ulp.max() <= 1 and (ulp > 0).mean() < 0.02, (ulp.max(), (ulp > 0).mean())
+
+
+def _ulps(a: torch.Tensor, b: np.ndarray, dtype) -> np.ndarray:
+    """Distance in units of the last place between a GPU tensor and oracle float values."""
+    if dtype == torch.float32:
+        ai = a.cpu().numpy().view(np.int32).astype(np.int64)
+        bi = b.astype(np.float32).view(np.int32).astype(np.int64)
+    else:
+        ai = a.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.int64)
+        if dtype == torch.bfloat16:
+            bi = ref.f32_to_bf16_bits(b).astype(np.int64)
+        else:
+            bi = np.asarray(b, np.float32).astype(np.float16).view(np.uint16).astype(np.int64)
+    return np.abs(ai - bi)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("T,H", [(1, 128), (5, 2048), (64, 4096), (3, 16384)])
+@pytest.mark.parametrize("with_residual", [True, False])
+def test_add_rmsnorm_matches_oracle(dtype, T, H, with_residual):
+    x = _rand((T, H), dtype, seed=T + H, scale=3.0)
+    r = _rand((T, H), dtype, seed=T + H + 1) if with_residual else None
+    w = _rand((H,), dtype, seed=H, scale=0.2) + 1
+    x0, r0 = x.clone(), (r.clone() if r is not None else None)
+    out = torch.empty_like(x)
+    add_rmsnorm_gate(x, r, w, 1e-6, out=out)
+    torch.cuda.synchronize()
+    dt = TORCH_TO_ORACLE[dtype]
+    xn_ref, res_ref = ref.add_rmsnorm(to_oracle(x0), None if r0 is None else to_oracle(r0),
+                                      to_oracle(w), 1e-6, dt)
+    assert torch.equal(x, x0)  # out-of-place form leaves the input
+    if with_residual:
+        np.testing.assert_array_equal(f32_of(r), res_ref)
+    _check_normed(out, xn_ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,H,E", [(1, 128, 8), (32, 4096, 8), (64, 2048, 60), (7, 256, 256)])
+def test_router_gate_matches_oracle(dtype, T, H, E):
+    x = _rand((T, H), dtype, seed=E + T)
+    r = _rand((T, H), dtype, seed=E + T + 1)
+    w = torch.ones((H,), dtype=dtype, device=DEV)
+    gw = _rand((E, H), dtype, seed=E, scale=0.05)
+    x0, r0 = x.clone(), r.clone()
+    logits = add_rmsnorm_gate(x, r, w, 1e-5, gate_weight=gw)
+    torch.cuda.synchronize()
+    dt = TORCH_TO_ORACLE[dtype]
+    xn_ref, _ = ref.add_rmsnorm(to_oracle(x0), to_oracle(r0), to_oracle(w), 1e-5, dt)
+    _check_normed(x, xn_ref, dtype)  # in place
+    # the gate consumes the kernel's own normalized states
+    lg_ref = ref.router_logits(to_oracle(x), to_oracle(gw), dt)
+    assert max_rel_err(f32_of(logits), lg_ref) <= (1e-2 if dtype == torch.bfloat16 else 1e-5)
+
+
+def test_norm_inplace_and_module():
+    T, H = 9, 1024
+    x = _rand((2, T, H), torch.bfloat16, seed=3)
+    r = _rand((2, T, H), torch.bfloat16, seed=4)
+    norm = RMSNorm(H, eps=1e-6).to(device=DEV, dtype=torch.bfloat16)
+    x0, r0 = x.clone(), r.clone()
+    xo, ro = norm(x, r)
+    torch.cuda.synchronize()
+    assert xo.data_ptr() == x.data_ptr() and ro.data_ptr() == r.data_ptr()
+    xn_ref, res_ref = ref.add_rmsnorm(to_oracle(x0.view(-1, H)), to_oracle(r0.view(-1, H)),
+                                      to_oracle(norm.weight.data), 1e-6, ref.BF16)
+    np.testing.assert_array_equal(f32_of(r.view(-1, H)), res_ref)
+    _check_normed(x.view(-1, H), xn_ref, torch.bfloat16)
+    y = norm(x0)
+    assert y.shape == x0.shape and y.data_ptr() != x0.data_ptr()
+
+
+def _layer_case(T, H, I, E, k, renorm, Is=0, gated=False, scale=1.0, seed=0):
+    dt = torch.bfloat16
+    x = _rand((T, H), dt, seed=seed + 1)
+    r = _rand((T, H), dt, seed=seed + 2)
+    nw = _rand((H,), dt, seed=seed + 3, scale=0.1) + 1
+    gw = _rand((E, H), dt, seed=seed + 4, scale=0.05)
+    pool, slots = make_pool(E, H, I, dt, num_slots=E + 3, seed=seed + 5)
+    page = _rand((3 * Is * H,), dt, seed=seed + 6, scale=0.02) if Is else None
+    sgw = _rand((H,), dt, seed=seed + 7, scale=0.05) if gated else None
+    x0, r0 = x.clone(), r.clone()
+    y, (lg, w, ids) = moe_layer_forward(x, r, nw, 1e-6, gw, pool, slots, k, renorm, shared_w=page,
+                                        shared_gate_weight=sgw, routed_scaling_factor=scale,
+                                        return_routing=True)
+    torch.cuda.synchronize()
+    assert y.data_ptr() == x.data_ptr()
+    # route the oracle on the kernel's logit bits (and its shared-gate logits, recomputed from
+    # the kernel's normalized states), so that ids are comparable bit for bit
+    xn_ref, res_ref = ref.add_rmsnorm(to_oracle(x0), to_oracle(r0), to_oracle(nw), 1e-6, ref.BF16)
+    np.testing.assert_array_equal(f32_of(r), res_ref)
+    sgl = ref.router_logits(xn_ref, to_oracle(sgw).reshape(1, -1), ref.BF16).reshape(-1) if gated else None
+    y_ref, _, _, w_ref, ids_ref = ref.moe_layer_forward(
+        to_oracle(x0), to_oracle(r0), to_oracle(nw), 1e-6, to_oracle(gw), to_oracle(pool),
+        slots.cpu().numpy(), k, renorm, ref.BF16,
+        shared_page=None if page is None else to_oracle(page),
+        routed_scaling_factor=scale, logits=f32_of(lg), shared_gate_logits=sgl)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    lg_ref = ref.router_logits(xn_ref, to_oracle(gw), ref.BF16)
+    assert max_rel_err(f32_of(lg), lg_ref) <= 1e-2
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("T", [1, 17, 64])
+def test_layer_forward_mixtral_like(T):
+    _layer_case(T, 256, 256, 8, 2, True, seed=T)
+
+
+@pytest.mark.parametrize("T", [3, 64])
+def test_layer_forward_qwen_like(T):
+    _layer_case(T, 256, 128, 60, 4, False, Is=512, gated=True, seed=100 + T)
+
+
+def test_layer_forward_deepseek_like():
+    _layer_case(32, 256, 128, 64, 6, False, Is=256, scale=2.5, seed=200)
+
+
+def test_layer_forward_mixtral_full_size():
+    _layer_case(32, 4096, 14336, 8, 2, True, seed=300)
+
+
+@pytest.mark.parametrize("kind", ["mixtral", "qwen"])
+def test_post_attention_module(kind):
+    H, I, E, T = 256, 128, 8, 10
+    dt = torch.bfloat16
+    if kind == "mixtral":
+        blk = MixtralMoE(E, 2, H, I, params_dtype=dt, tp_size=1)
+    else:
+        blk = Qwen2MoeSparseMoeBlock(num_experts=E, top_k=4, hidden_size=H, moe_intermediate_size=I,
+                                     shared_expert_intermediate_size=256, params_dtype=dt, tp_size=1)
+    g = torch.Generator().manual_seed(5)
+    with torch.no_grad():
+        blk.gate.weight.copy_(torch.randn(blk.gate.weight.shape, generator=g) * 0.05)
+        blk.experts.ws.copy_(torch.randn(blk.experts.ws.shape, generator=g) * 0.02)
+        if kind == "qwen":
+            blk.shared_ws.copy_(torch.randn(blk.shared_ws.shape, generator=g) * 0.02)
+            blk.shared_expert_gate.weight.copy_(torch.randn((1, H), generator=g) * 0.05)
+    blk.to(DEV)
+    set_weight_attrs(blk.experts.ws, {"gpu_cache": blk.experts.ws.data})
+    norm = RMSNorm(H).to(device=DEV, dtype=dt)
+    layer = PostAttentionMoE(norm, blk)
+    mapping = torch.arange(E, dtype=torch.int64, device=DEV)
+    x = _rand((T, H), dt, seed=6)
+    r = _rand((T, H), dt, seed=7)
+    x0, r0 = x.clone(), r.clone()
+    with torch.no_grad():
+        y, res = layer(x, r, mapping)
+        torch.cuda.synchronize()
+        # the unfused sequence with the same modules: norm, then the block on the normed states
+        xs, rs = norm(x0.clone(), r0.clone())
+        y2 = blk(xs, mapping)
+    torch.cuda.synchronize()
+    assert torch.equal(res, rs)
+    # the two paths compute router logits with different accumulation orders (gate kernel vs
+    # torch GEMM); compare against each other to the output tolerance
+    assert max_rel_err(f32_of(y), f32_of(y2)) <= 2 * TOL[dt]

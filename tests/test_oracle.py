@@ -360,3 +360,67 @@ def test_shared_block_reductions():
     lo, _, _ = ref.fused_moe_shared_forward(x, logits, pool, slots, k, False, dt, page,
                                             np.full(T, -100.0, np.float32))
     np.testing.assert_array_equal(lo, routed)
+
+
+# ----------------------------------------------------------------- residual add + RMSNorm + gate
+def _bf16(a):
+    return ref.f32_to_bf16_bits(np.asarray(a, np.float32))
+
+
+def test_add_rmsnorm_against_torch_native_formula():
+    """The reference's forward_native (layernorm.py:36-52) is torch arithmetic; evaluate it with
+    torch on the CPU (its own reduction order and rsqrt) and compare: the residual is exact,
+    the normalized values agree to one bf16 rounding step."""
+    import torch
+    rng = np.random.default_rng(31)
+    T, H, eps = 7, 512, 1e-6
+    x, r = _bf16(rng.standard_normal((T, H)) * 3), _bf16(rng.standard_normal((T, H)))
+    w = _bf16(1 + 0.1 * rng.standard_normal(H))
+    xn, res = ref.add_rmsnorm(x, r, w, eps, ref.BF16)
+    tx = torch.from_numpy(ref.to_f32(x, ref.BF16)).to(torch.bfloat16)
+    tr = torch.from_numpy(ref.to_f32(r, ref.BF16)).to(torch.bfloat16)
+    tw = torch.from_numpy(ref.to_f32(w, ref.BF16)).to(torch.bfloat16)
+    s = tx.to(torch.float32) + tr.to(torch.float32)
+    t_res = s.to(torch.bfloat16)
+    var = s.pow(2).mean(dim=-1, keepdim=True)
+    t_xn = ((s * torch.rsqrt(var + eps)) * tw).to(torch.bfloat16)
+    np.testing.assert_array_equal(res, t_res.float().numpy())
+    ulp = np.abs(ref.f32_to_bf16_bits(xn).astype(np.int64) -
+                 t_xn.view(torch.int16).numpy().astype(np.uint16).astype(np.int64))
+    assert ulp.max() <= 1 and (ulp > 0).mean() < 0.01
+
+
+def test_rmsnorm_unit_rms_and_float64():
+    rng = np.random.default_rng(32)
+    T, H, eps = 5, 1024, 1e-5
+    x = (rng.standard_normal((T, H)) * 7).astype(np.float32)
+    xn, res = ref.add_rmsnorm(x, None, np.ones(H, np.float32), eps, ref.F32)
+    assert res is None
+    rms = np.sqrt(np.mean(xn.astype(np.float64) ** 2, axis=-1))
+    np.testing.assert_allclose(rms, 1.0, rtol=1e-5)
+    w = rng.standard_normal(H).astype(np.float32)
+    xn2, _ = ref.add_rmsnorm(x, None, w, eps, ref.F32)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + eps) * w
+    np.testing.assert_allclose(xn2, want, rtol=2e-6, atol=2e-6 * np.abs(want).max())
+
+
+def test_router_logits_and_layer_composition():
+    """The layer restatement is norm -> gate -> MoE: with the logits given it equals the MoE
+    oracle applied to the normalized states; the gate matches a float64 product."""
+    rng = np.random.default_rng(33)
+    T, H, I, E, k = 6, 64, 32, 4, 2
+    dt = ref.BF16
+    x, r = _bf16(rng.standard_normal((T, H))), _bf16(rng.standard_normal((T, H)))
+    nw = _bf16(np.ones(H))
+    gw = _bf16(rng.standard_normal((E, H)) * 0.2)
+    pool = _bf16(rng.standard_normal((E, 3 * I * H)) * 0.05)
+    slots = np.arange(E)
+    y, res, lg, w, ids = ref.moe_layer_forward(x, r, nw, 1e-6, gw, pool, slots, k, True, dt)
+    xn, res2 = ref.add_rmsnorm(x, r, nw, 1e-6, dt)
+    np.testing.assert_array_equal(res, res2)
+    want = xn.astype(np.float64) @ ref.to_f32(gw, dt).T.astype(np.float64)
+    assert np.abs(lg - want).max() <= 8e-3 * np.abs(want).max()
+    y2, w2, ids2 = ref.fused_moe_forward(ref.f32_to_bf16_bits(xn), lg, pool, slots, k, True, dt)
+    np.testing.assert_array_equal(y, y2)
+    np.testing.assert_array_equal(ids, ids2)
