@@ -17,6 +17,9 @@ SMX_ERR_INVALID_ARG = 1000
 SMX_ERR_UNSUPPORTED = 1001
 SMX_ERR_WORKSPACE = 1002
 SMX_ERR_MISALIGNED = 1003
+SMX_ERR_TIMEOUT = 1004
+SMX_ERR_NOT_FOUND = 1005
+SMX_H2D_HIDDEN, SMX_H2D_KV_CACHE, SMX_H2D_DRAFT_KV_CACHE, SMX_H2D_WEIGHT = 1, 2, 3, 4
 
 # (name, restype, argtypes) of every exported entry point, in header order.
 _c_void_p, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_size_t
@@ -47,6 +50,18 @@ SIGNATURES = [
      [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, ctypes.c_float, _c_void_p, _i64, _i64,
       _i32, _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _i64, _c_void_p, ctypes.c_float,
       _c_void_p, _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
+    ("smx_host_alloc", ctypes.c_int, [_sz, ctypes.POINTER(_c_void_p)]),
+    ("smx_host_free", ctypes.c_int, [_c_void_p]),
+    ("smx_h2d_engine_create", ctypes.c_int, [ctypes.POINTER(_c_void_p)]),
+    ("smx_h2d_engine_destroy", ctypes.c_int, [_c_void_p]),
+    ("smx_h2d_submit", ctypes.c_int,
+     [_c_void_p, _i32, ctypes.c_char_p, _c_void_p, _c_void_p, _sz, _sz, _i64, _i64, _c_void_p]),
+    ("smx_h2d_wait", ctypes.c_int,
+     [_c_void_p, ctypes.c_char_p, ctypes.c_double, ctypes.POINTER(ctypes.c_double)]),
+    ("smx_h2d_has_task", ctypes.c_int, [_c_void_p, ctypes.c_char_p]),
+    ("smx_h2d_clear", ctypes.c_int, [_c_void_p, ctypes.c_char_p]),
+    ("smx_h2d_set_enabled", ctypes.c_int, [_c_void_p, _i32]),
+    ("smx_h2d_pending", ctypes.c_int, [_c_void_p]),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

@@ -252,6 +252,8 @@ const char* smx_error_string(int code) {
     case SMX_ERR_UNSUPPORTED: return "shape outside the supported limits";
     case SMX_ERR_WORKSPACE: return "workspace too small";
     case SMX_ERR_MISALIGNED: return "tensor base not 16-byte aligned";
+    case SMX_ERR_TIMEOUT: return "timed out waiting for a transfer task";
+    case SMX_ERR_NOT_FOUND: return "no such transfer task";
     default: return hipGetErrorString(static_cast<hipError_t>(code));
   }
 }

@@ -74,6 +74,10 @@ def parse():
     ap.add_argument("--rotate", type=int, default=2, help="copies of the weights rotated per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-calls", type=int, default=2, help="CPU baseline sample: layer calls")
+    ap.add_argument("--h2d", action="store_true",
+                    help="measure host -> device streaming of expert pages through the transfer "
+                         "engine (pinned host memory, chunked copies), alone and beside the MoE "
+                         "kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy 10 times (HBM counter calibration)")
     return ap.parse_args()
@@ -369,6 +373,9 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
+    if args.h2d:
+        h2d_bench(args)
+        return
 
     from ae_amd import _lib
 
@@ -387,6 +394,135 @@ def main():
                     torch.bfloat16) for _ in range(args.layers)]
     for T in tokens:
         run_tokens(args, wl, T, layers, L, dev)
+
+
+PCIE_GEN5_X16_GBS = 64.0  # host link of one MI355X, per direction, before protocol overhead
+
+
+def h2d_bench(args):
+    """Expert pages (Mixtral shape: 3*14336*4096 bf16 = 352 MB each) streamed from pinned host
+    memory into pool slots: the transfer engine at several chunk counts, torch's pinned copy and
+    a pageable copy for comparison, and the engine while the MoE kernels run on another stream."""
+    from ae_amd import _lib
+    from ae_amd.backend import HtoDTransferEngine, free_pinned_tensor, make_pinned_tensor
+    from ae_amd.layers._torch import ptr
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    torch.zeros(1, device=dev)
+    H, I, E = 4096, 14336, 8
+    page = 3 * I * H
+    n_pages = 4
+    page_bytes = page * 2
+    host, hp = make_pinned_tensor(n_pages * page_bytes, torch.bfloat16)
+    out = {}
+    try:
+        host = host.view(n_pages, page)
+        host.copy_(torch.randint(-1000, 1000, (n_pages, page), dtype=torch.int16).view(torch.bfloat16))
+        pool = torch.empty((2 * n_pages, page), dtype=torch.bfloat16, device=dev)
+        stream = torch.cuda.Stream(dev)
+        eng = HtoDTransferEngine()
+        eng.start()
+        for e in range(n_pages):  # warm-up: first touch of the destination pages
+            eng.submit_weight_loading_task(host[e], pool[2 * e], stream, f"warm{e}", 1, 1)
+        for e in range(n_pages):
+            assert eng.wait_for_completion(f"warm{e}")[0]
+        rates = {}
+        for chunks in (1, 4, 16):
+            t0 = time.perf_counter()
+            for e in range(n_pages):
+                eng.submit_weight_loading_task(host[e], pool[2 * e], stream, f"c{chunks}p{e}", chunks, 1)
+            for e in range(n_pages):
+                assert eng.wait_for_completion(f"c{chunks}p{e}")[0]
+            dt = time.perf_counter() - t0
+            rates[chunks] = n_pages * page_bytes / dt / 1e9
+            eng.clear_condition([f"c{chunks}p{e}" for e in range(n_pages)])
+        ok = all(torch.equal(pool[2 * e].cpu().view(torch.int16), host[e].view(torch.int16))
+                 for e in range(n_pages))  # bit patterns (random ones include NaN encodings)
+        # torch's copy from the same pinned memory
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for e in range(n_pages):
+            pool[2 * e + 1].copy_(host[e], non_blocking=True)
+        torch.cuda.synchronize()
+        torch_rate = n_pages * page_bytes / (time.perf_counter() - t0) / 1e9
+        # pageable source, one page
+        pageable = host[0].clone()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        pool[1].copy_(pageable)
+        torch.cuda.synchronize()
+        pageable_rate = page_bytes / (time.perf_counter() - t0) / 1e9
+        del pageable
+        # engine beside the MoE kernels (Mixtral layer, 32 tokens, on the default stream)
+        T, k = 32, 2
+        g = torch.Generator(device=dev).manual_seed(0)
+        epool = torch.empty((E, page), dtype=torch.bfloat16, device=dev)
+        for e in range(E):
+            epool[e] = (torch.randn(page, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        x = torch.randn((T, H), generator=g, device=dev).to(torch.bfloat16)
+        logits = torch.randn((T, E), generator=g, device=dev).to(torch.bfloat16)
+        y = torch.empty_like(x)
+        slots = torch.arange(E, dtype=torch.int64, device=dev)
+        L = _lib.lib()
+        nb = L.smx_moe_workspace_size(T, H, I, E, k, _lib.SMX_BF16)
+        ws = torch.empty(nb, dtype=torch.uint8, device=dev)
+        cs = torch.cuda.current_stream(dev)
+        sp = ctypes.c_void_p(cs.cuda_stream)
+
+        def moe():
+            _lib.check("smx_fused_moe_forward", L.smx_fused_moe_forward(
+                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(logits), _lib.SMX_BF16, E, k, 1,
+                ptr(epool), E, page, ptr(slots), None, None, ptr(ws), nb, sp))
+
+        for _ in range(5):
+            moe()
+        torch.cuda.synchronize()
+        steps = 40
+        a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a0.record(cs)
+        for _ in range(steps):
+            moe()
+        a1.record(cs)
+        torch.cuda.synchronize()
+        moe_alone_us = 1000.0 * a0.elapsed_time(a1) / steps
+        t0 = time.perf_counter()
+        for e in range(n_pages):
+            eng.submit_weight_loading_task(host[e], pool[2 * e], stream, f"ov{e}", 4, 1)
+        a0.record(cs)
+        for _ in range(steps):
+            moe()
+        a1.record(cs)
+        for e in range(n_pages):
+            assert eng.wait_for_completion(f"ov{e}")[0]
+        h2d_dt = time.perf_counter() - t0
+        torch.cuda.synchronize()
+        moe_beside_us = 1000.0 * a0.elapsed_time(a1) / steps
+        eng.stop()
+        value = rates[4]
+        out = {
+            "metric": "host -> device expert page streaming GB/s (pinned host memory, transfer engine)",
+            "value": round(value, 2),
+            "unit": "GB/s",
+            "n_gpus": 1,
+            "higher_is_better": True,
+            "dtype": "bf16",
+            "data": "synthetic bf16 expert pages",
+            "config": {"workload": "Mixtral-8x7B expert pages (352 MB each) into pool slots",
+                       "pages": n_pages, "page_bytes": page_bytes},
+            "roofline": {"bound": "pcie", "achieved": round(value, 2), "peak": PCIE_GEN5_X16_GBS,
+                         "unit": "GB/s", "frac": round(value / PCIE_GEN5_X16_GBS, 4)},
+            "engine_gbs_by_chunks": {str(c): round(r, 2) for c, r in rates.items()},
+            "torch_pinned_copy_gbs": round(torch_rate, 2),
+            "pageable_copy_gbs": round(pageable_rate, 2),
+            "bit_exact": ok,
+            "overlap": {"moe_us_alone": round(moe_alone_us, 2),
+                        "moe_us_beside_h2d": round(moe_beside_us, 2),
+                        "h2d_gbs_beside_moe": round(n_pages * page_bytes / h2d_dt / 1e9, 2)},
+        }
+    finally:
+        free_pinned_tensor(hp)
+    print(json.dumps(out), flush=True)
 
 
 def cpu_baseline(args, wl, x, logits, sgate, layer, slots, layer_bytes):

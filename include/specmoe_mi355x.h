@@ -2,7 +2,8 @@
  * specmoe_mi355x.h -- C ABI of the MI355X (gfx950) MoE verify-step hot path.
  *
  * One shared library, libspecmoe_mi355x.so, built with hipcc --offload-arch=gfx950.
- * Every entry point:
+ * Every compute entry point (all but the host-memory and transfer-engine services at the
+ * end, which allocate host memory and block the calling thread where stated):
  *   - takes plain device pointers and sizes (no framework types);
  *   - is stream-ordered on the hipStream_t passed as `stream` (NULL = default stream);
  *   - never synchronises the host and never allocates device memory: scratch space is the
@@ -34,7 +35,9 @@ enum smx_status {
   SMX_ERR_INVALID_ARG = 1000,     /* null pointer, negative size, top_k > E, ... */
   SMX_ERR_UNSUPPORTED = 1001,     /* shape outside the kernels' limits (see below) */
   SMX_ERR_WORKSPACE = 1002,       /* workspace smaller than smx_moe_workspace_size() */
-  SMX_ERR_MISALIGNED = 1003       /* a tensor base is not 16-byte aligned */
+  SMX_ERR_MISALIGNED = 1003,      /* a tensor base is not 16-byte aligned */
+  SMX_ERR_TIMEOUT = 1004,         /* smx_h2d_wait: the task did not finish in time */
+  SMX_ERR_NOT_FOUND = 1005        /* smx_h2d_wait: no such task id (or it was cleared) */
 };
 
 /* Limits: 1 <= E <= 256; 1 <= top_k <= min(E, 16); T*top_k <= 16384;
@@ -191,6 +194,50 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
                           const void* shared_gate_weight, float routed_scaling_factor,
                           void* router_logits_out, float* topk_weights_out, int32_t* topk_ids_out,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Host memory and host -> device streaming of expert pages.
+ * --------------------------------------------------------------------------------------- */
+
+/* Pinned (page-locked, portable) host memory via hipHostMalloc; free with smx_host_free.
+ * Replaces cuda_host_alloc / free_pinned_tensor (specmoe/backend/pin_memory_allocator.py:
+ * 7-28, 62-65), which hard-code libcudart's cudaMallocHost / cudaFreeHost. */
+int smx_host_alloc(size_t bytes, void** ptr);
+int smx_host_free(void* ptr);
+
+/* Transfer classes in priority order (most urgent first), as TransferTaskType /
+ * TASK_PRIORITY_MAPPING (specmoe/backend/htod_transfer_engine.py:16-30). */
+enum smx_h2d_type { SMX_H2D_HIDDEN = 1, SMX_H2D_KV_CACHE = 2, SMX_H2D_DRAFT_KV_CACHE = 3,
+                    SMX_H2D_WEIGHT = 4 };
+
+/*
+ * Asynchronous host -> device copy engine: one worker thread, a priority queue of chunk
+ * copies (class, then layer -- layer 0 last --, then chunk index, then submission order).
+ * A task's `bytes` (whole elements of `elem_bytes`) are split into `num_chunks` chunks, the
+ * first (elements % num_chunks) one element longer; each chunk is copied with hipMemcpyAsync
+ * on `stream` and waited for before the next chunk starts, so urgent tasks overtake long
+ * ones between chunks. smx_h2d_wait blocks until the task's last chunk has landed
+ * (timeout_s < 0: no limit) and returns its copy status; for SMX_H2D_WEIGHT tasks `seconds`
+ * receives the time from its first chunk's start to its last chunk's end (else -1).
+ * smx_h2d_clear forgets a task id (chunks already queued still run); resubmitting an id
+ * starts a new task. smx_h2d_set_enabled(0) pauses the worker between chunks.
+ * Replaces HtoDTransferEngine (specmoe/backend/htod_transfer_engine.py:73-520: start/stop,
+ * submit_weight_loading_task :297-308, _submit_chunked_task :321-369, wait_for_completion
+ * :375-411, clear_condition :413-420, the worker :405-489) for the weight streaming driven at
+ * specmoe/backend/execution_engine.py:143-154,549-588. Streams passed in must have the default
+ * priority.
+ */
+typedef struct smx_h2d_engine smx_h2d_engine;
+int smx_h2d_engine_create(smx_h2d_engine** engine);
+int smx_h2d_engine_destroy(smx_h2d_engine* engine);
+int smx_h2d_submit(smx_h2d_engine* engine, int task_type, const char* task_id, void* dst,
+                   const void* src, size_t bytes, size_t elem_bytes, int64_t num_chunks,
+                   int64_t layer_id, void* stream);
+int smx_h2d_wait(smx_h2d_engine* engine, const char* task_id, double timeout_s, double* seconds);
+int smx_h2d_has_task(smx_h2d_engine* engine, const char* task_id);
+int smx_h2d_clear(smx_h2d_engine* engine, const char* task_id);
+int smx_h2d_set_enabled(smx_h2d_engine* engine, int enabled);
+int smx_h2d_pending(smx_h2d_engine* engine);
 
 /*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records

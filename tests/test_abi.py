@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 13, names
+    assert len(names) == 23, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -201,3 +201,29 @@ def test_layer_forward_rejects_before_launch():
     assert L.smx_moe_layer_workspace_size(32, 4096, 14336, 8, 2, 0, 2) > \
         L.smx_moe_workspace_size(32, 4096, 14336, 8, 2, 2)
     assert L.smx_moe_layer_workspace_size(32, 32768, 14336, 8, 2, 0, 2) == 0  # H above the norm limit
+
+
+def test_transfer_entry_points_reject_bad_arguments():
+    vp = VP()
+    assert L.smx_host_alloc(0, ctypes.byref(vp)) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_host_free(None) == _lib.SMX_OK
+    assert L.smx_h2d_engine_create(None) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_h2d_engine_destroy(None) == _lib.SMX_OK
+    assert L.smx_h2d_submit(None, 4, b"t", A, A, 16, 2, 1, 0, VP(0)) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_h2d_wait(None, b"t", 0.0, None) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_h2d_has_task(None, b"t") == 0
+    assert L.smx_h2d_clear(None, b"t") == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_h2d_set_enabled(None, 1) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_h2d_pending(None) == 0
+    for code, word in [(1004, b"timed out"), (1005, b"no such")]:
+        assert word in L.smx_error_string(code)
+
+
+def test_transfer_engine_python_checks():
+    import torch
+    from ae_amd.backend import HtoDTransferEngine, TransferTaskType, TASK_PRIORITY_MAPPING
+    eng = HtoDTransferEngine()
+    assert not eng.has_task_id("x") and eng.wait_for_completion("x") is False
+    with pytest.raises(RuntimeError):
+        eng.submit_weight_loading_task(torch.zeros(4), torch.zeros(4), None, "t", 1, 0)
+    assert [TASK_PRIORITY_MAPPING[t] for t in TransferTaskType] == [1, 2, 3, 4]
