@@ -101,7 +101,7 @@ __device__ __forceinline__ void load_tokens(RawTokens<MT>& rb, const SharedToken
 template <int MT>
 __device__ __forceinline__ void store_tokens(const RawTokens<MT>& rb, u32x4* bt) {
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_id();
   u32x4* wr = bt + kPitch * (4 * wave + (lane >> 4)) + (lane & 15);
 #pragma unroll
   for (int j = 0; j < MT; ++j) wr[j * kTileSlots] = rb.v[j];
@@ -114,28 +114,58 @@ __device__ __forceinline__ void wg_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// One chunk: issue the next chunk's token loads, then its weight loads (so waiting for the
-// tokens never waits for the weights); transpose this chunk's weights through the
-// wave-private LDS tile; MFMAs against the shared token tile `bt`; publish the next chunk's
-// token tile into `bt_next`; barrier.
-template <int DT, int R, int MT, bool kPrefetch>
-__device__ __forceinline__ void wg_chunk(const Raw<R>& c, Raw<R>& next, RawTokens<MT>& rb,
-                                         u32x4* lds, const u32x4* bt, u32x4* bt_next,
-                                         const WeightStream& w, const SharedTokens<MT>& t,
-                                         int chunk, f32x4 (&acc)[R][MT]) {
-  const int lane = lane_id();
-  if constexpr (kPrefetch) {
-    load_tokens(rb, t, chunk + 1);
-    load_raw(next, w, chunk + 1);
+// Order in which a workgroup walks its K chunks: step c reads chunk (c + rot) mod n. The
+// accumulation order over K is then a fixed rotation per workgroup (deterministic run to run).
+struct ChunkOrder {
+  int n, rot;
+  __device__ __forceinline__ int at(int c) const {
+    const int p = c + rot;
+    return p >= n ? p - n : p;
   }
-  // Keep the scheduler from sinking loads into the MFMA sequence (which would shrink the
-  // prefetch distance) or from waiting on the prefetch early.
-  __builtin_amdgcn_sched_barrier(0);
+};
+
+// Gate/up workgroups start their K walk at different chunks. W1/W3 rows have a pitch of H
+// elements, a power of two in bytes for the common hidden sizes (4096 and 8192 bytes in
+// bf16): workgroups that sit at the same chunk at the same moment, as they do when they start
+// together, then stream addresses that agree in their low 12-13 bits. Rotating the start by
+// blockIdx / 4 measured 5.6 -> 6.1 TB/s on the H = 2048 gate/up stream and 6.3 -> 6.7 TB/s
+// on H = 4096 (other rotations tried: blockIdx mod n, which keeps each XCD's workgroups on a
+// few residues, was slower than none at H = 4096). The down projection's rows (pitch I) are
+// walked in order: its K splits already start at different chunks, and rotating them
+// measured no gain.
+__device__ __forceinline__ ChunkOrder rotated_order(int n) {
+  return ChunkOrder{n, static_cast<int>(blockIdx.x >> 2) % n};
+}
+
+// One step of the workgroup's two-deep pipeline, for chunk c. On entry this chunk's weights
+// are in `cur` (issued two steps back), chunk c+1's weights are in flight in the other
+// register set, this chunk's token tile is published in `bt` and chunk c+1's token rows are
+// in flight in `tnext`. Writing `cur` into the wave's LDS tile frees it at once, so chunk
+// c+2's token rows (into `tfree`) and weights (into `cur`; `issue_chunk` is where step c+2
+// falls in the workgroup's chunk order) are issued before the MFMAs: two
+// chunks of weights stay in flight while this one is multiplied. Then chunk c+1's token rows,
+// issued a step ago, are published into `bt_next`; barrier. Token loads are issued before
+// weight loads, so waiting for a token chunk never waits for the weights issued with it.
+template <int DT, int R, int MT, bool kIssue, bool kNext>
+__device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT>& tnext,
+                                        RawTokens<MT>& tfree, u32x4* lds, const u32x4* bt,
+                                        u32x4* bt_next, const WeightStream& w,
+                                        const SharedTokens<MT>& t, int issue_chunk,
+                                        f32x4 (&acc)[R][MT]) {
+  const int lane = lane_id();
   u32x4* wr = lds + kPitch * (lane >> 4) + (lane & 15);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int r = 0; r < R; ++r) wr[r * kTileSlots + 4 * kPitch * i] = c.v[i][r];
+    for (int r = 0; r < R; ++r) wr[r * kTileSlots + 4 * kPitch * i] = cur.v[i][r];
+  // Keep the refill after the LDS writes (so it reuses `cur`'s registers) and ahead of the
+  // MFMA sequence (so it is in flight while they run).
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kIssue) {
+    load_tokens(tfree, t, issue_chunk);
+    load_raw(cur, w, issue_chunk);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   const u32x4* rd = lds + kPitch * (lane & 15) + (lane >> 4);
   const u32x4* brd = bt + kPitch * (lane & 15) + (lane >> 4);
 #pragma unroll
@@ -151,34 +181,49 @@ __device__ __forceinline__ void wg_chunk(const Raw<R>& c, Raw<R>& next, RawToken
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (kPrefetch) store_tokens(rb, bt_next);
+  if constexpr (kNext) store_tokens(tnext, bt_next);
   wg_barrier();
 }
 
+// Issue the first two weight chunks of a stream (they need only the expert page, so they go
+// out before the token rows are looked up).
+template <int R>
+__device__ __forceinline__ void issue_weights(Raw<R>& a, Raw<R>& b, const WeightStream& w,
+                                              const ChunkOrder& ord) {
+  load_raw(a, w, ord.at(0));
+  if (ord.n > 1) load_raw(b, w, ord.at(1));
+}
+
 // acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt, the workgroup streaming the token
-// chunks through `bsh` (two buffers of MT tiles) while each wave streams its own weights.
+// chunks through `bsh` (two buffers of MT tiles) while each wave streams its own weights;
+// chunks 0 and 1 of the weights are already in flight in `a` and `b` (issue_weights).
 template <int DT, int R, int MT>
 __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTokens<MT>& t,
-                                          int nchunks, u32x4* lds, u32x4* bsh,
-                                          f32x4 (&acc)[R][MT]) {
-  Raw<R> c0, c1;
-  RawTokens<MT> rb;
+                                          const ChunkOrder& ord, u32x4* lds, u32x4* bsh,
+                                          f32x4 (&acc)[R][MT], Raw<R>& a, Raw<R>& b) {
+  RawTokens<MT> t0, t1;
   u32x4* b0 = bsh;
   u32x4* b1 = bsh + MT * kTileSlots;
-  load_tokens(rb, t, 0);
-  load_raw(c0, w, 0);
-  store_tokens(rb, b0);
+  const int nchunks = ord.n;
+  load_tokens(t0, t, ord.at(0));
+  if (nchunks > 1) load_tokens(t1, t, ord.at(1));
+  store_tokens(t0, b0);
   wg_barrier();
   int c = 0;
-  for (; c + 2 < nchunks; c += 2) {
-    wg_chunk<DT, R, MT, true>(c0, c1, rb, lds, b0, b1, w, t, c, acc);
-    wg_chunk<DT, R, MT, true>(c1, c0, rb, lds, b1, b0, w, t, c + 1, acc);
+  for (; c + 3 < nchunks; c += 2) {
+    wg_step<DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
+    wg_step<DT, R, MT, true, true>(b, t0, t1, lds, b1, b0, w, t, ord.at(c + 3), acc);
   }
-  if (c + 1 < nchunks) {
-    wg_chunk<DT, R, MT, true>(c0, c1, rb, lds, b0, b1, w, t, c, acc);
-    wg_chunk<DT, R, MT, false>(c1, c0, rb, lds, b1, b0, w, t, c + 1, acc);
+  const int rem = nchunks - c;  // 1, 2 or 3 chunks left
+  if (rem == 3) {
+    wg_step<DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
+    wg_step<DT, R, MT, false, true>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
+    wg_step<DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+  } else if (rem == 2) {
+    wg_step<DT, R, MT, false, true>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<DT, R, MT, false, false>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
   } else {
-    wg_chunk<DT, R, MT, false>(c0, c1, rb, lds, b0, b1, w, t, c, acc);
+    wg_step<DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
   }
 }
 
@@ -263,7 +308,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
                                               bool owner, u32x4* lds, u32x4* bsh) {
   using S = typename Elem<DT>::S;
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_id();
   const int r = lane & 15, g = lane >> 4;
   const int H = a.H, I = it.I, off = it.off, m = it.m;
   const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
@@ -273,9 +318,11 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   ws.tile_stride = static_cast<uint32_t>(I * row_bytes);
   ws.row4 = static_cast<uint32_t>(4 * row_bytes);
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
-  const int nchunks = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
+  const ChunkOrder ord = rotated_order(static_cast<int>(row_bytes / (kStepBytes * kUnroll)));
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
+    Raw<2> wa, wb;
+    issue_weights(wa, wb, ws, ord);
     SharedTokens<MT> tb;
     tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
     tb.base = 0;
@@ -290,7 +337,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<DT, 2, MT>(ws, tb, nchunks, lds, bsh, acc);
+    stream_wg<DT, 2, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -315,7 +362,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
 // one tile of 16 tokens.
 template <int DT, int MT>
 __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_id();
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
   const int Iw = in_shared ? a.sh.I : a.I;
   const int tiles = Iw / kRowTile;
@@ -343,7 +390,7 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
   using S = typename Elem<DT>::S;
   constexpr int R = kDownRows;
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_id();
   const int r = lane & 15, g = lane >> 4;
   const int H = a.H, I = it.I, off = it.off, m = it.m;
   const int rows = it.shared ? a.T : a.T * a.k;  // rows of act and of one split of part
@@ -357,7 +404,10 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
   const void* act = it.shared ? a.sh.act : a.act;
   float* part = it.shared ? a.sh.part : a.part;
+  const ChunkOrder ord{split_steps / kUnroll, 0};
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
+    Raw<R> wa, wb;
+    issue_weights(wa, wb, ws, ord);
     SharedTokens<MT> tb;
     tb.rsrc = make_rsrc(act, static_cast<uint32_t>(static_cast<int64_t>(rows) * row_bytes));
     tb.base = static_cast<uint32_t>(k0_bytes);
@@ -371,7 +421,7 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<DT, R, MT>(ws, tb, split_steps / kUnroll, lds, bsh, acc);
+    stream_wg<DT, R, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -391,7 +441,7 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
 // per pass as in gateup_kernel.
 template <int DT, int MT>
 __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_id();
   const int rtiles = a.H / (kRowTile * kDownRows);
   const int groups = (rtiles + kExpertWaves - 1) / kExpertWaves;
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.down_blocks;
@@ -451,7 +501,7 @@ template <int DT>
 __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(CombineArgs c) {
   __shared__ f32x4 terms[kMaxTopK + 1][kWave];
   const int lane = lane_id();
-  const int wave = threadIdx.x / kWave;
+  const int wave = wave_id();
   const int waves = blockDim.x / kWave;
   const int chunks = (c.H + 4 * kWave - 1) / (4 * kWave);
   const int t = blockIdx.x / chunks;

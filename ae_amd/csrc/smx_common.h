@@ -143,6 +143,11 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 
+// Wave index within the workgroup, in a scalar register: the compiler cannot see that
+// threadIdx.x / 64 is the same across a wave, and values derived from it (buffer offsets)
+// would otherwise be treated as per-lane.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); }
+
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
 }  // namespace smx
