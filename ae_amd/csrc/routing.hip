@@ -541,6 +541,94 @@ __global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
 }
 
 // ---------------------------------------------------------------------------------------
+// Routing of a small batch (T*k <= 64 assignments, E <= 64) by one wave, without workgroup
+// barriers: the top-k of every token (all logits loaded up front, one latency), then lane f
+// takes assignment f and the sort is done with ballots. For each lane the lanes with the same
+// expert and the lanes with a smaller expert are found bit by bit from the top id bit down
+// (eq: lanes agreeing on the bits so far; a lane whose id has a 1 where an eq lane has a 0
+// ranks that lane below it); the sorted position is (#smaller) + (#same below this lane), so
+// within an expert assignments stay in ascending f, and the active-expert index is the number
+// of smaller experts present. Outputs are those of route_kernel (same order, same values).
+// ---------------------------------------------------------------------------------------
+constexpr int kSmallRoutePasses = 16;  // token passes of 64/G tokens (T * G <= 1024)
+
+template <int LDT, int G>
+__global__ __launch_bounds__(kWave) void route_small_kernel(
+    const void* __restrict__ logits, int T, int E, int k, int renorm,
+    float* __restrict__ w_out, int32_t* __restrict__ ids_out, const int32_t* __restrict__ ids_in,
+    const int64_t* __restrict__ e2s, int64_t num_slots, AlignOutputs out) {
+  constexpr int TPW = kWave / G;  // tokens per pass
+  __shared__ RankScratch rs;
+  __shared__ int ids_l[kWave];
+  __shared__ int64_t slot_l[kWave];
+  const int lane = lane_id();
+  const int N = T * k;
+  const int64_t my_slot = lane < E ? e2s[lane] : -1;
+  int e = -2;
+  if (logits != nullptr) {
+    const int passes = (T + TPW - 1) / TPW;
+    float v[kSmallRoutePasses][1];
+#pragma unroll
+    for (int ps = 0; ps < kSmallRoutePasses; ++ps)
+      if (ps < passes) load_logits<LDT, G, 1>(logits, ps * TPW + lane / G, T, E, v[ps]);
+#pragma unroll
+    for (int ps = 0; ps < kSmallRoutePasses; ++ps) {
+      if (ps >= passes) break;
+      float pv[1][1] = {{v[ps][0]}};
+      float w[1];
+      int id[1], slot[1];
+      group_topk_rank<G, 1>(pv, E, k, renorm != 0, rs, w, id, slot);
+      const int t = ps * TPW + lane / G;
+      if (t < T && slot[0] >= 0) {
+        const int f = t * k + slot[0];
+        if (w_out) w_out[f] = w[0];
+        if (ids_out) ids_out[f] = id[0];
+        ids_l[f] = id[0];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < N) e = ids_l[lane];
+  } else if (lane < N) {
+    const int x = ids_in[lane];
+    e = (x >= 0 && x < E) ? x : -2;
+  }
+  slot_l[lane] = (my_slot >= 0 && my_slot < num_slots) ? my_slot : -1;
+  __builtin_amdgcn_wave_barrier();
+  const int64_t sl = e >= 0 ? slot_l[e] : -1;
+  const bool ok = e >= 0 && sl >= 0;
+  const uint64_t okm = ballot(ok);
+  const bool bad = ballot(lane < N && !ok) != 0;
+  if (out.tmask && lane < T)
+    out.tmask[lane] = static_cast<int32_t>((okm >> (lane * k)) & ((1ull << k) - 1));
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  uint64_t eq = okm, less = 0;
+  for (int b = nbits - 1; b >= 0; --b) {
+    const bool bit = ok && ((e >> b) & 1);
+    const uint64_t m1 = ballot(bit);
+    if (bit) less |= eq & ~m1;
+    eq &= bit ? m1 : (okm & ~m1);
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  const int rank = __popcll(eq & below);
+  const int nless = __popcll(less);
+  const uint64_t first = ballot(ok && rank == 0);
+  if (ok) {
+    if (out.sorted_f) out.sorted_f[nless + rank] = lane;
+    if (rank == 0 && out.act_expert) {
+      const int ai = __popcll(less & first);
+      out.act_expert[ai] = e;
+      out.act_off[ai] = nless;
+      out.act_cnt[ai] = __popcll(eq);
+      out.act_slot[ai] = sl;
+    }
+  }
+  if (lane == 0 && out.hdr) {
+    out.hdr[0] = __popcll(first);
+    out.hdr[1] = bad ? 1 : 0;
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Post-attention residual add + RMSNorm + router gate, one workgroup per token.
 //   s        = x + residual                      (fp32)
 //   residual = round(s)
@@ -772,6 +860,18 @@ static void route_launch_g(const void* logits, int T, int E, int k, int renorm, 
   }
 }
 
+template <int LDT>
+static void small_route_launch_g(const void* logits, int T, int E, int k, int renorm, float* w_out,
+                                 int32_t* ids_out, const int32_t* ids_in, const int64_t* e2s,
+                                 int64_t num_slots, const AlignOutputs& out, hipStream_t s) {
+  switch (group_for(E)) {
+    case 8: route_small_kernel<LDT, 8><<<1, kWave, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    case 16: route_small_kernel<LDT, 16><<<1, kWave, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    case 32: route_small_kernel<LDT, 32><<<1, kWave, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+    default: route_small_kernel<LDT, 64><<<1, kWave, 0, s>>>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out); break;
+  }
+}
+
 hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int renorm,
                         float* w_out, int32_t* ids_out, const int32_t* ids_in,
                         const int64_t* e2s, int64_t num_slots, const RouteBuffers& rb,
@@ -785,9 +885,11 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
   out.sorted_f = rb.sorted_f;
   out.tmask = rb.tmask;
   out.bm = 1;
+  const bool small = static_cast<int64_t>(T) * k <= kWave && E <= kWave;
   // the ids-given form needs no top-k: one instantiation serves every E
   if (logits == nullptr) {
-    route_launch<kF32, 8, 1>(nullptr, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s);
+    if (small) route_small_kernel<kF32, 8><<<1, kWave, 0, s>>>(nullptr, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out);
+    else route_launch<kF32, 8, 1>(nullptr, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s);
     return hipGetLastError();
   }
   // Large batches: the top-k runs over many workgroups first (one workgroup would be bound by
@@ -796,6 +898,15 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
     hipError_t err = launch_topk_softmax(logits, ldt, T, E, k, renorm, w_out, ids_out, s);
     if (err != hipSuccess) return err;
     route_launch<kF32, 8, 1>(nullptr, T, E, k, renorm, nullptr, nullptr, ids_out, e2s, num_slots, out, s);
+    return hipGetLastError();
+  }
+  // Small batches: one wave does the top-k and the sort.
+  if (small && static_cast<int64_t>(T) * group_for(E) <= kWave * kSmallRoutePasses) {
+    switch (ldt) {
+      case kF32: small_route_launch_g<kF32>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+      case kF16: small_route_launch_g<kF16>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+      default: small_route_launch_g<kBF16>(logits, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out, s); break;
+    }
     return hipGetLastError();
   }
   switch (ldt) {
