@@ -509,15 +509,22 @@ __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(Combi
   const bool live = h < c.H;
   const uint32_t vm = static_cast<uint32_t>(c.tmask[t]);
   const int items = c.k + (c.part_s != nullptr ? 1 : 0);
+  // the shared-expert gate logit, loaded with everything else (used by wave 0 at the end)
+  const bool gated = c.block && c.part_s != nullptr && c.sgate != nullptr;
+  const float z = gated && wave == 0 ? load_scalar(c.sgate, c.sgate_dtype, t) : 0.0f;
   for (int i = wave; i < items; i += waves) {
     f32x4 term = {0.f, 0.f, 0.f, 0.f};
     if (i < c.k) {
-      if (live && ((vm >> i) & 1u)) {
+      // The partials and the weight are loaded together with the token's mask (no dependent
+      // round trip); a dropped assignment's rows were not written by this call and are
+      // discarded by the select below.
+      if (live) {
         const int64_t f = static_cast<int64_t>(t) * c.k + i;
         const f32x4 v = split_sum(c.part + f * c.H + h, static_cast<int64_t>(c.T) * c.k * c.H, c.splits);
         const float wf = c.w[f];
+        const bool routed = (vm >> i) & 1u;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) term[e] = Elem<DT>::round(v[e] * wf);
+        for (int e = 0; e < 4; ++e) term[e] = routed ? Elem<DT>::round(v[e] * wf) : 0.0f;
       }
     } else if (live) {
       term = split_sum(c.part_s + static_cast<int64_t>(t) * c.H + h, static_cast<int64_t>(c.T) * c.H, c.splits_s);
@@ -539,14 +546,11 @@ __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(Combi
     if (c.part_s) {
       const f32x4 d = terms[c.k][lane];
       float gs = 1.0f;
-      if (c.sgate) {
-        const float z = load_scalar(c.sgate, c.sgate_dtype, t);
-        gs = Elem<DT>::round(1.0f / (1.0f + __expf(-z)));
-      }
+      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + __expf(-z)));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float sh = Elem<DT>::round(d[e]);
-        if (c.sgate) sh = Elem<DT>::round(gs * sh);
+        if (gated) sh = Elem<DT>::round(gs * sh);
         y[e] += sh;
       }
     }

@@ -550,7 +550,9 @@ __global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
 // within an expert assignments stay in ascending f, and the active-expert index is the number
 // of smaller experts present. Outputs are those of route_kernel (same order, same values).
 // ---------------------------------------------------------------------------------------
-constexpr int kSmallRoutePasses = 16;  // token passes of 64/G tokens (T * G <= 1024)
+// Token passes of 64/G tokens (T * G <= 256): each pass is a dependent chain of group
+// reductions, so beyond a few passes the multi-wave kernel is faster.
+constexpr int kSmallRoutePasses = 4;
 
 template <int LDT, int G>
 __global__ __launch_bounds__(kWave) void route_small_kernel(

@@ -35,11 +35,12 @@ CASES = [
     (64, 128, 256, 16, 4, 20),
     (70, 128, 128, 8, 2, 8),      # > 64 tokens on one expert: several token groups
     (130, 256, 128, 3, 3, 3),     # every expert sees every token
-    # up to 64 assignments over up to 64 experts: routed by one wave
+    # up to 64 assignments over up to 64 experts in up to 4 top-k passes: routed by one wave
     (1, 256, 128, 64, 6, 64),
-    (8, 256, 128, 64, 6, 70),
-    (16, 128, 128, 32, 4, 32),    # exactly 64 assignments
+    (4, 256, 128, 64, 6, 70),
+    (8, 128, 128, 32, 8, 32),     # exactly 64 assignments
     (3, 128, 128, 60, 16, 60),
+    (8, 256, 128, 64, 6, 70),     # 8 passes: the multi-wave kernel
 ]
 
 
