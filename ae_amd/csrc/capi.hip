@@ -34,11 +34,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 struct Plan {
   int N = 0;
-  int max_active = 0;
+  int max_active = 0;  // experts that can be active: min(E, T*k)
+  int span = 0;        // sorted positions per work range: the tokens of one kernel pass
+  int max_ranges = 0;  // work ranges at most: every active expert, plus one per further span
   int tok_tiles = 1;
   int splits = 1;
   int split_steps = 0;
-  size_t hdr = 0, act_expert = 0, act_off = 0, act_cnt = 0, act_slot = 0, sorted_f = 0, w = 0, ids = 0;
+  size_t hdr = 0, ranges = 0, sorted_f = 0, w = 0, ids = 0;
   size_t tmask = 0;
   size_t act = 0, part = 0, total = 0;
   // shared expert (Is > 0)
@@ -101,6 +103,8 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
   p.max_active = static_cast<int>(E < p.N ? E : p.N);
   const int64_t tiles = (T + kTokTile - 1) / kTokTile;
   p.tok_tiles = static_cast<int>(tiles < 1 ? 1 : (tiles > kMaxTokTiles ? kMaxTokTiles : tiles));
+  p.span = kTokTile * p.tok_tiles;
+  p.max_ranges = p.max_active + p.N / p.span;
   const int64_t eb = dtype_bytes(dtype);
   const int64_t nchunks = I * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
   const int64_t units = static_cast<int64_t>(p.max_active > 0 ? p.max_active : 1) * (H / (kRowTile * kDownRows));
@@ -125,10 +129,7 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
   }
   size_t o = 0;
   p.hdr = o;        o = align_up(o + 64);
-  p.act_expert = o; o = align_up(o + sizeof(int32_t) * E);
-  p.act_off = o;    o = align_up(o + sizeof(int32_t) * E);
-  p.act_cnt = o;    o = align_up(o + sizeof(int32_t) * E);
-  p.act_slot = o;   o = align_up(o + sizeof(int64_t) * E);
+  p.ranges = o;     o = align_up(o + sizeof(RangeRec) * static_cast<size_t>(p.max_ranges > 0 ? p.max_ranges : 1));
   p.sorted_f = o;   o = align_up(o + sizeof(int32_t) * p.N);
   p.tmask = o;      o = align_up(o + sizeof(int32_t) * T);
   p.w = o;          o = align_up(o + sizeof(float) * p.N);
@@ -151,12 +152,10 @@ RouteBuffers carve(const Plan& p, void* ws) {
   char* b = static_cast<char*>(ws);
   RouteBuffers rb;
   rb.hdr = reinterpret_cast<int32_t*>(b + p.hdr);
-  rb.act_expert = reinterpret_cast<int32_t*>(b + p.act_expert);
-  rb.act_off = reinterpret_cast<int32_t*>(b + p.act_off);
-  rb.act_cnt = reinterpret_cast<int32_t*>(b + p.act_cnt);
+  rb.ranges = reinterpret_cast<RangeRec*>(b + p.ranges);
   rb.sorted_f = reinterpret_cast<int32_t*>(b + p.sorted_f);
-  rb.act_slot = reinterpret_cast<int64_t*>(b + p.act_slot);
   rb.tmask = reinterpret_cast<int32_t*>(b + p.tmask);
+  rb.span = p.span;
   return rb;
 }
 
@@ -200,10 +199,10 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
     a.sh.gateup_blocks = p.s_gateup_blocks;
     a.sh.down_blocks = p.s_down_blocks;
   }
-  hipError_t err = launch_gateup(dtype, a, p.max_active, p.tok_tiles, s);
+  hipError_t err = launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(2, s);
-  err = launch_down(dtype, a, p.max_active, p.tok_tiles, s);
+  err = launch_down(dtype, a, p.max_ranges, p.tok_tiles, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(3, s);
   CombineArgs c{};

@@ -62,7 +62,8 @@ struct WeightStream {
   uint32_t lane_off;            // per lane: row l/16, byte column 16*(l%16)
 };
 
-template <int R>
+// CP: cache policy of the weight loads (kNonTemporal when every weight byte is read once).
+template <int CP, int R>
 __device__ __forceinline__ void load_raw(Raw<R>& c, const WeightStream& w, int chunk) {
   const uint32_t cbase = w.base + static_cast<uint32_t>(chunk) * (kStepBytes * kUnroll);
 #pragma unroll
@@ -70,7 +71,7 @@ __device__ __forceinline__ void load_raw(Raw<R>& c, const WeightStream& w, int c
 #pragma unroll
     for (int r = 0; r < R; ++r)
       c.v[i][r] = __builtin_amdgcn_raw_buffer_load_b128(
-          w.rsrc, w.lane_off, cbase + r * w.tile_stride + i * w.row4, kNonTemporal);
+          w.rsrc, w.lane_off, cbase + r * w.tile_stride + i * w.row4, CP);
 }
 
 // Token operand, shared by the workgroup. The 4 waves of a workgroup work on the same expert
@@ -133,8 +134,8 @@ struct ChunkOrder {
 // few residues, was slower than none at H = 4096). The down projection's rows (pitch I) are
 // walked in order: its K splits already start at different chunks, and rotating them
 // measured no gain.
-__device__ __forceinline__ ChunkOrder rotated_order(int n) {
-  return ChunkOrder{n, static_cast<int>(blockIdx.x >> 2) % n};
+__device__ __forceinline__ ChunkOrder rotated_order(int n, int index) {
+  return ChunkOrder{n, (index >> 2) % n};
 }
 
 // One step of the workgroup's two-deep pipeline, for chunk c. On entry this chunk's weights
@@ -146,7 +147,7 @@ __device__ __forceinline__ ChunkOrder rotated_order(int n) {
 // chunks of weights stay in flight while this one is multiplied. Then chunk c+1's token rows,
 // issued a step ago, are published into `bt_next`; barrier. Token loads are issued before
 // weight loads, so waiting for a token chunk never waits for the weights issued with it.
-template <int DT, int R, int MT, bool kIssue, bool kNext>
+template <int CP, int DT, int R, int MT, bool kIssue, bool kNext>
 __device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT>& tnext,
                                         RawTokens<MT>& tfree, u32x4* lds, const u32x4* bt,
                                         u32x4* bt_next, const WeightStream& w,
@@ -163,7 +164,7 @@ __device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT>& tnext,
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (kIssue) {
     load_tokens(tfree, t, issue_chunk);
-    load_raw(cur, w, issue_chunk);
+    load_raw<CP>(cur, w, issue_chunk);
   }
   __builtin_amdgcn_sched_barrier(0);
   const u32x4* rd = lds + kPitch * (lane & 15) + (lane >> 4);
@@ -187,17 +188,17 @@ __device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT>& tnext,
 
 // Issue the first two weight chunks of a stream (they need only the expert page, so they go
 // out before the token rows are looked up).
-template <int R>
+template <int CP, int R>
 __device__ __forceinline__ void issue_weights(Raw<R>& a, Raw<R>& b, const WeightStream& w,
                                               const ChunkOrder& ord) {
-  load_raw(a, w, ord.at(0));
-  if (ord.n > 1) load_raw(b, w, ord.at(1));
+  load_raw<CP>(a, w, ord.at(0));
+  if (ord.n > 1) load_raw<CP>(b, w, ord.at(1));
 }
 
 // acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt, the workgroup streaming the token
 // chunks through `bsh` (two buffers of MT tiles) while each wave streams its own weights;
 // chunks 0 and 1 of the weights are already in flight in `a` and `b` (issue_weights).
-template <int DT, int R, int MT>
+template <int CP, int DT, int R, int MT>
 __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTokens<MT>& t,
                                           const ChunkOrder& ord, u32x4* lds, u32x4* bsh,
                                           f32x4 (&acc)[R][MT], Raw<R>& a, Raw<R>& b) {
@@ -211,19 +212,19 @@ __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTok
   wg_barrier();
   int c = 0;
   for (; c + 3 < nchunks; c += 2) {
-    wg_step<DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
-    wg_step<DT, R, MT, true, true>(b, t0, t1, lds, b1, b0, w, t, ord.at(c + 3), acc);
+    wg_step<CP, DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
+    wg_step<CP, DT, R, MT, true, true>(b, t0, t1, lds, b1, b0, w, t, ord.at(c + 3), acc);
   }
   const int rem = nchunks - c;  // 1, 2 or 3 chunks left
   if (rem == 3) {
-    wg_step<DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
-    wg_step<DT, R, MT, false, true>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
-    wg_step<DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
+    wg_step<CP, DT, R, MT, false, true>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
   } else if (rem == 2) {
-    wg_step<DT, R, MT, false, true>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
-    wg_step<DT, R, MT, false, false>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, false, true>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, false, false>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
   } else {
-    wg_step<DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
   }
 }
 
@@ -255,18 +256,21 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
 
 // The work item of one workgroup: an expert page and a list of m token rows starting at
 // position `off` (routed: sorted positions, token = sorted_f / k; shared expert: token rows
-// off.. directly). `tg` is the workgroup's index among the item's workgroups.
+// off.. directly). `tg` is the workgroup's index among the item's workgroups; `rot` is the
+// index the K-walk rotation derives from -- the same for every token range of one expert, so
+// that ranges streaming the same rows side by side read them in the same order.
 struct WorkItem {
   const char* page;
   int64_t page_bytes;
   int I;
-  int off, m, tg;
+  int off, m, tg, rot;
+  int nr;  // token ranges of the item's expert (1: its weights are read by this item only)
   bool shared;
 };
 
-// Leading `sh.*_blocks` workgroups run the shared expert (v = token range, then tg);
-// the rest run routed experts (ai = active-expert index, then tg). Returns false for a
-// workgroup whose routed expert is not active in this batch.
+// Leading `sh.*_blocks` workgroups run the shared expert (v = token range, then tg); the rest
+// run the routing's work ranges (j = range, then tg). Returns false for a workgroup past the
+// ranges of this batch.
 template <typename S>
 __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
                                           WorkItem& w) {
@@ -281,29 +285,59 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
     w.off = v * span;
     w.m = min(span, a.T - w.off);
     w.tg = b - v * per_item;
+    w.rot = w.tg;
+    w.nr = 1;
     w.shared = true;
     return true;
   }
   const int rb = b - shared_blocks;
-  const int ai = rb / per_item;  // uniform across the workgroup
-  // ai < max_active <= E, so the per-expert arrays may be read before the active count is
-  // known (the loads then share one latency); values past the active count are unused.
-  const int active = uniform(a.rb.hdr[0]);
-  w.off = uniform(a.rb.act_off[ai]);
-  w.m = uniform(a.rb.act_cnt[ai]);
-  const int64_t slot = uniform64(a.rb.act_slot[ai]);
+  const int j = rb / per_item;  // one of the expert's ranges; uniform across the workgroup
+  // j is below the launch's range bound, so the record may be read before the range count is
+  // known (the loads then share one latency); records past the count are unused.
+  const int nranges = uniform(a.rb.hdr[0]);
+  const RangeRec& rr = a.rb.ranges[j];
+  const int off = uniform(rr.off);
+  const int cnt = uniform(rr.cnt);
+  const int key = uniform(rr.key);
+  const int j0 = uniform(rr.j0);
+  const int nr = max(uniform(rr.nr), 1);
+  const int64_t slot = uniform64(rr.slot);
+  // The expert's nr * per_item items, numbered so that the nr ranges of weight group g are 8
+  // items apart: workgroups are dealt to the 8 XCDs round robin, so they run on one XCD, side
+  // by side, and share its L2 for the rows they all read. Groups past the last multiple of 8
+  // are numbered the same way with their own count as the spacing.
+  const int local = rb - j0 * per_item;
+  int g = local, r = 0;
+  if (nr > 1) {
+    const int full = per_item / 8 * 8 * nr;
+    if (local < full) {
+      const int blk = local / (8 * nr);
+      const int in = local - blk * 8 * nr;
+      r = in / 8;
+      g = blk * 8 + (in - r * 8);
+    } else {
+      const int rem = per_item % 8;
+      const int in = local - full;
+      r = in / rem;
+      g = per_item / 8 * 8 + (in - r * rem);
+    }
+  }
+  w.off = off + r * a.rb.span;
+  w.m = min(a.rb.span, cnt - r * a.rb.span);
   w.page_bytes = a.page_elems * elem;
   w.page = static_cast<const char*>(a.pool) + slot * w.page_bytes;
   w.I = a.I;
-  w.tg = rb - ai * per_item;
+  w.tg = g;
+  w.rot = (key + 1) * per_item + g;
+  w.nr = nr;
   w.shared = false;
-  return ai < active;
+  return j < nranges;
 }
 
 // The token passes of one gate/up workgroup with MT token tiles per pass: wave `wave` owns
 // weight-row tile p (gate rows [16p, 16p+16) and the matching up rows); `owner` is false for
 // a wave past the expert's last tile (it streams tile p again and stores nothing).
-template <int DT, int MT>
+template <int CP, int DT, int MT>
 __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkItem& it, int p,
                                               bool owner, u32x4* lds, u32x4* bsh) {
   using S = typename Elem<DT>::S;
@@ -318,11 +352,11 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   ws.tile_stride = static_cast<uint32_t>(I * row_bytes);
   ws.row4 = static_cast<uint32_t>(4 * row_bytes);
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
-  const ChunkOrder ord = rotated_order(static_cast<int>(row_bytes / (kStepBytes * kUnroll)));
+  const ChunkOrder ord = rotated_order(static_cast<int>(row_bytes / (kStepBytes * kUnroll)), it.rot);
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<2> wa, wb;
-    issue_weights(wa, wb, ws, ord);
+    issue_weights<CP>(wa, wb, ws, ord);
     SharedTokens<MT> tb;
     tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
     tb.base = 0;
@@ -337,7 +371,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<DT, 2, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
+    stream_wg<CP, DT, 2, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -360,7 +394,19 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
 // wave of a workgroup runs the same chunks and barriers. The token tiles per pass follow
 // the item's token count (up to MT): an expert with few tokens streams its weights with
 // one tile of 16 tokens.
-template <int DT, int MT>
+template <int CP, int DT, int MT>
+__device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem& it, int p,
+                                            bool owner, u32x4* lds, u32x4* bsh) {
+  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1>(a, it, p, owner, lds, bsh);
+  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1)>(a, it, p, owner, lds, bsh);
+  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1)>(a, it, p, owner, lds, bsh);
+  else gateup_passes<CP, DT, MT>(a, it, p, owner, lds, bsh);
+}
+
+// kMulti: the launch may hold experts split into several token ranges (T > span). Their
+// items load weights with normal caching (the ranges of a weight group read the same rows
+// side by side); every other item streams with the non-temporal hint.
+template <bool kMulti, int DT, int MT>
 __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   const int wave = wave_id();
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
@@ -375,15 +421,13 @@ __global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
   __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
   __shared__ u32x4 bsh[2 * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
-  if (MT == 1 || it.m <= kTokTile) gateup_passes<DT, 1>(a, it, p, owner, lds, bsh);
-  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<DT, (MT >= 2 ? 2 : 1)>(a, it, p, owner, lds, bsh);
-  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<DT, (MT >= 3 ? 3 : 1)>(a, it, p, owner, lds, bsh);
-  else gateup_passes<DT, MT>(a, it, p, owner, lds, bsh);
+  if (kMulti && it.nr > 1) gateup_item<0, DT, MT>(a, it, p, owner, lds, bsh);
+  else gateup_item<kNonTemporal, DT, MT>(a, it, p, owner, lds, bsh);
 }
 
 // The token passes of one down workgroup with MT token tiles per pass: wave `wave` owns W2
 // rows [32*rt, 32*rt + 32) over the K slice of split sp.
-template <int DT, int MT>
+template <int CP, int DT, int MT>
 __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem& it, int rt,
                                             bool owner, int sp, int split_steps, u32x4* lds,
                                             u32x4* bsh) {
@@ -407,7 +451,7 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
   const ChunkOrder ord{split_steps / kUnroll, 0};
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<R> wa, wb;
-    issue_weights(wa, wb, ws, ord);
+    issue_weights<CP>(wa, wb, ws, ord);
     SharedTokens<MT> tb;
     tb.rsrc = make_rsrc(act, static_cast<uint32_t>(static_cast<int64_t>(rows) * row_bytes));
     tb.base = static_cast<uint32_t>(k0_bytes);
@@ -421,7 +465,7 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<DT, R, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
+    stream_wg<CP, DT, R, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -439,7 +483,17 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
 // Workgroup = (work item, K split, 4 consecutive pairs of W2 row tiles): wave w owns rows
 // [32*(4*group + w), +32). Waves past the last pair repeat it and store nothing. Token tiles
 // per pass as in gateup_kernel.
-template <int DT, int MT>
+template <int CP, int DT, int MT>
+__device__ __forceinline__ void down_item(const ExpertArgs& a, const WorkItem& it, int rt,
+                                          bool owner, int sp, int split_steps, u32x4* lds,
+                                          u32x4* bsh) {
+  if (MT == 1 || it.m <= kTokTile) down_passes<CP, DT, 1>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else if (MT == 2 || it.m <= 2 * kTokTile) down_passes<CP, DT, (MT >= 2 ? 2 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else if (MT == 3 || it.m <= 3 * kTokTile) down_passes<CP, DT, (MT >= 3 ? 3 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else down_passes<CP, DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
+}
+
+template <bool kMulti, int DT, int MT>
 __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
   const int wave = wave_id();
   const int rtiles = a.H / (kRowTile * kDownRows);
@@ -457,10 +511,8 @@ __global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
   __shared__ u32x4 lds_all[kExpertWaves][kDownRows * kTileSlots];
   __shared__ u32x4 bsh[2 * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
-  if (MT == 1 || it.m <= kTokTile) down_passes<DT, 1>(a, it, rt, owner, sp, split_steps, lds, bsh);
-  else if (MT == 2 || it.m <= 2 * kTokTile) down_passes<DT, (MT >= 2 ? 2 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
-  else if (MT == 3 || it.m <= 3 * kTokTile) down_passes<DT, (MT >= 3 ? 3 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
-  else down_passes<DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  if (kMulti && it.nr > 1) down_item<0, DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else down_item<kNonTemporal, DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
 }
 
 __device__ __forceinline__ float load_scalar(const void* base, int dtype, int64_t i) {
@@ -558,46 +610,53 @@ __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(Combi
   store4<DT>(c.y, static_cast<int64_t>(t) * c.H + h, y[0], y[1], y[2], y[3]);
 }
 
-template <int DT, int MT>
-static hipError_t launch_stage_t(int stage, const ExpertArgs& a, int max_active, hipStream_t s) {
+template <bool kMulti, int DT, int MT>
+static void launch_stage_m(int stage, const ExpertArgs& a, int max_ranges, hipStream_t s) {
   if (stage == 0) {
     const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
-    const int64_t blocks = a.sh.gateup_blocks + max_active * groups;
-    gateup_kernel<DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
+    const int64_t blocks = a.sh.gateup_blocks + max_ranges * groups;
+    gateup_kernel<kMulti, DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   } else {
     const int64_t groups = (a.H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves;
-    const int64_t blocks = a.sh.down_blocks + max_active * groups * a.splits;
-    down_kernel<DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
+    const int64_t blocks = a.sh.down_blocks + max_ranges * groups * a.splits;
+    down_kernel<kMulti, DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   }
+}
+
+template <int DT, int MT>
+static hipError_t launch_stage_t(int stage, const ExpertArgs& a, int max_ranges, hipStream_t s) {
+  // no expert can have more tokens than one pass holds when T <= span
+  if (a.T <= a.rb.span) launch_stage_m<false, DT, MT>(stage, a, max_ranges, s);
+  else launch_stage_m<true, DT, MT>(stage, a, max_ranges, s);
   return hipGetLastError();
 }
 
 template <int DT>
-static hipError_t launch_stage_dt(int stage, const ExpertArgs& a, int max_active, int tok_tiles,
+static hipError_t launch_stage_dt(int stage, const ExpertArgs& a, int max_ranges, int tok_tiles,
                                   hipStream_t s) {
   switch (tok_tiles) {
-    case 1: return launch_stage_t<DT, 1>(stage, a, max_active, s);
-    case 2: return launch_stage_t<DT, 2>(stage, a, max_active, s);
-    case 3: return launch_stage_t<DT, 3>(stage, a, max_active, s);
-    default: return launch_stage_t<DT, 4>(stage, a, max_active, s);
+    case 1: return launch_stage_t<DT, 1>(stage, a, max_ranges, s);
+    case 2: return launch_stage_t<DT, 2>(stage, a, max_ranges, s);
+    case 3: return launch_stage_t<DT, 3>(stage, a, max_ranges, s);
+    default: return launch_stage_t<DT, 4>(stage, a, max_ranges, s);
   }
 }
 
-static hipError_t launch_stage(int stage, int dtype, const ExpertArgs& a, int max_active,
+static hipError_t launch_stage(int stage, int dtype, const ExpertArgs& a, int max_ranges,
                                int tok_tiles, hipStream_t s) {
   switch (dtype) {
-    case kF32: return launch_stage_dt<kF32>(stage, a, max_active, tok_tiles, s);
-    case kF16: return launch_stage_dt<kF16>(stage, a, max_active, tok_tiles, s);
-    default: return launch_stage_dt<kBF16>(stage, a, max_active, tok_tiles, s);
+    case kF32: return launch_stage_dt<kF32>(stage, a, max_ranges, tok_tiles, s);
+    case kF16: return launch_stage_dt<kF16>(stage, a, max_ranges, tok_tiles, s);
+    default: return launch_stage_dt<kBF16>(stage, a, max_ranges, tok_tiles, s);
   }
 }
 
-hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_active, int tok_tiles, hipStream_t s) {
-  return launch_stage(0, dtype, a, max_active, tok_tiles, s);
+hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles, hipStream_t s) {
+  return launch_stage(0, dtype, a, max_ranges, tok_tiles, s);
 }
 
-hipError_t launch_down(int dtype, const ExpertArgs& a, int max_active, int tok_tiles, hipStream_t s) {
-  return launch_stage(1, dtype, a, max_active, tok_tiles, s);
+hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles, hipStream_t s) {
+  return launch_stage(1, dtype, a, max_ranges, tok_tiles, s);
 }
 
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s) {

@@ -313,18 +313,16 @@ struct AlignShared {
   int cnt[kMaxExperts];
   int off[kMaxExperts + 1];               // compact exclusive prefix
   int seg[kMaxExperts + 1];               // block-padded exclusive prefix
-  int act[kMaxExperts + 1];               // active-expert exclusive prefix
   int64_t slot[kMaxExperts];              // pool slot per expert (-1: unmapped), route only
+  int nranges;                            // work ranges over all experts
   int bad;                                // an assignment was dropped
 };
 
 struct AlignOutputs {
   // compact lists for the expert kernels (may be null)
-  int32_t* hdr;         // [0] = number of active experts, [1] = dropped-assignment flag
-  int32_t* act_expert;  // [E]
-  int32_t* act_off;     // [E]
-  int32_t* act_cnt;     // [E]
-  int64_t* act_slot;    // [E]
+  int32_t* hdr;         // [0] = number of work ranges, [1] = dropped-assignment flag
+  RangeRec* ranges;     // [active experts + N / span]
+  int span;             // sorted positions per range
   int32_t* sorted_f;    // [N]
   int32_t* tmask;       // [T] per token: bit j set if assignment t*k+j is routable
   // reference-format outputs (may be null)
@@ -391,7 +389,8 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
   // active-expert table.
   if (wave == 0) {
     const int bm = out.bm > 0 ? out.bm : 1;
-    int c[4], sc = 0, sp = 0, sa = 0;
+    const int span = out.span > 0 ? out.span : 1;
+    int c[4], sc = 0, sp = 0, sa = 0, sr = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
@@ -407,38 +406,46 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
       sc += c[i];
       sp += (c[i] + bm - 1) / bm * bm;
       sa += c[i] > 0;
+      sr += (c[i] + span - 1) / span;
     }
-    int ic = sc, ip = sp, ia = sa;
+    int ic = sc, ip = sp, ia = sa, ir = sr;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
       const int tc = __shfl_up(ic, off, kWave);
       const int tp = __shfl_up(ip, off, kWave);
       const int ta = __shfl_up(ia, off, kWave);
-      if (lane >= off) { ic += tc; ip += tp; ia += ta; }
+      const int tr = __shfl_up(ir, off, kWave);
+      if (lane >= off) { ic += tc; ip += tp; ia += ta; ir += tr; }
     }
-    int bc = ic - sc, bp = ip - sp, ba = ia - sa;
+    if (lane == kWave - 1) sh.nranges = ir;
+    int bc = ic - sc, bp = ip - sp, ba = ia - sa, br = ir - sr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
-      if (e <= E) { sh.off[e] = bc; sh.seg[e] = bp; sh.act[e] = ba; }
+      if (e <= E) { sh.off[e] = bc; sh.seg[e] = bp; }
       if (e < E) {
         for (int w = 0; w < nw; ++w) sh.cntw[w][e] += bc;
-        if (out.act_expert && c[i] > 0) {
-          out.act_expert[ba] = e;
-          out.act_off[ba] = bc;
-          out.act_cnt[ba] = c[i];
-          if constexpr (kCheckSlots) out.act_slot[ba] = sh.slot[e];
+        if (out.ranges && c[i] > 0) {
+          RangeRec rec{};
+          rec.slot = kCheckSlots ? sh.slot[e] : -1;
+          rec.off = bc;
+          rec.cnt = c[i];
+          rec.key = ba;
+          rec.j0 = br;
+          rec.nr = (c[i] + span - 1) / span;
+          for (int r = 0; r < rec.nr; ++r) out.ranges[br + r] = rec;
         }
       }
       bc += c[i];
       bp += (c[i] + bm - 1) / bm * bm;
       ba += c[i] > 0;
+      br += (c[i] + span - 1) / span;
     }
-    if (E == 4 * kWave && lane == kWave - 1) { sh.off[E] = bc; sh.seg[E] = bp; sh.act[E] = ba; }
+    if (E == 4 * kWave && lane == kWave - 1) { sh.off[E] = bc; sh.seg[E] = bp; }
   }
   __syncthreads();
   if (tid == 0) {
-    if (out.hdr) { out.hdr[0] = sh.act[E]; out.hdr[1] = sh.bad; }
+    if (out.hdr) { out.hdr[0] = sh.nranges; out.hdr[1] = sh.bad; }
     if (out.ntp) out.ntp[0] = sh.seg[E];
   }
 
@@ -616,12 +623,16 @@ __global__ __launch_bounds__(kWave) void route_small_kernel(
   const uint64_t first = ballot(ok && rank == 0);
   if (ok) {
     if (out.sorted_f) out.sorted_f[nless + rank] = lane;
-    if (rank == 0 && out.act_expert) {
+    if (rank == 0 && out.ranges) {  // the host runs this kernel only when T <= span
       const int ai = __popcll(less & first);
-      out.act_expert[ai] = e;
-      out.act_off[ai] = nless;
-      out.act_cnt[ai] = __popcll(eq);
-      out.act_slot[ai] = sl;
+      RangeRec rec{};
+      rec.slot = sl;
+      rec.off = nless;
+      rec.cnt = __popcll(eq);
+      rec.key = ai;
+      rec.j0 = ai;
+      rec.nr = 1;
+      out.ranges[ai] = rec;
     }
   }
   if (lane == 0 && out.hdr) {
@@ -880,14 +891,12 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
                         hipStream_t s) {
   AlignOutputs out{};
   out.hdr = rb.hdr;
-  out.act_expert = rb.act_expert;
-  out.act_off = rb.act_off;
-  out.act_cnt = rb.act_cnt;
-  out.act_slot = rb.act_slot;
+  out.ranges = rb.ranges;
+  out.span = rb.span;
   out.sorted_f = rb.sorted_f;
   out.tmask = rb.tmask;
   out.bm = 1;
-  const bool small = static_cast<int64_t>(T) * k <= kWave && E <= kWave;
+  const bool small = static_cast<int64_t>(T) * k <= kWave && E <= kWave && T <= rb.span;
   // the ids-given form needs no top-k: one instantiation serves every E
   if (logits == nullptr) {
     if (small) route_small_kernel<kF32, 8><<<1, kWave, 0, s>>>(nullptr, T, E, k, renorm, w_out, ids_out, ids_in, e2s, num_slots, out);

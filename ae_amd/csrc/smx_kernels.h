@@ -27,14 +27,28 @@ constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 
 static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
               "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");
 
+// Work ranges of the expert kernels: up to `span` consecutive sorted positions of one active
+// expert. An expert with more tokens than one pass of the kernels holds is split into nr
+// ranges, numbered j0 .. j0 + nr - 1; each of them holds the same record (the expert's), so a
+// workgroup finds its expert from any range index in one load. The kernels number the items
+// of an expert (range r, weight group g) so that the nr ranges of one weight group run side
+// by side on one XCD and read the same rows at about the same time.
+struct RangeRec {
+  int64_t slot;  // pool slot of the expert
+  int32_t off;   // first sorted position of the expert
+  int32_t cnt;   // sorted positions of the expert
+  int32_t key;   // active-expert index
+  int32_t j0;    // first range of the expert
+  int32_t nr;    // ranges of the expert: ceil(cnt / span)
+  int32_t pad;
+};
+
 struct RouteBuffers {
-  int32_t* hdr;         // [0] active experts, [1] dropped-assignment flag
-  int32_t* act_expert;  // [E] expert id of each active expert (ascending)
-  int32_t* act_off;     // [E] first sorted position of each active expert
-  int32_t* act_cnt;     // [E] assignments routed to each active expert
+  int32_t* hdr;         // [0] ranges, [1] dropped-assignment flag
+  RangeRec* ranges;     // [max_ranges] in expert order, then range order
   int32_t* sorted_f;    // [T*k] flat assignment index f = t*k + j at each sorted position
-  int64_t* act_slot;    // [E] pool slot of each active expert
   int32_t* tmask;       // [T] bit j set: assignment t*k+j contributes (routable expert and slot)
+  int span;             // sorted positions per range (the tokens of one kernel pass)
 };
 
 // An always-active expert that every token passes through (the shared expert of the
@@ -112,9 +126,9 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
                         float* w_out, int32_t* ids_out, const int32_t* ids_in,
                         const int64_t* e2s, int64_t num_slots, const RouteBuffers& rb,
                         hipStream_t s);
-hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_active, int tok_tiles,
+hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
                          hipStream_t s);
-hipError_t launch_down(int dtype, const ExpertArgs& a, int max_active, int tok_tiles,
+hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
                        hipStream_t s);
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s);
 
