@@ -407,7 +407,7 @@ __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem&
 // items load weights with normal caching (the ranges of a weight group read the same rows
 // side by side); every other item streams with the non-temporal hint.
 template <bool kMulti, int DT, int MT>
-__global__ __launch_bounds__(kExpertThreads) void gateup_kernel(ExpertArgs a) {
+__global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a) {
   const int wave = wave_id();
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
   const int Iw = in_shared ? a.sh.I : a.I;
@@ -494,7 +494,7 @@ __device__ __forceinline__ void down_item(const ExpertArgs& a, const WorkItem& i
 }
 
 template <bool kMulti, int DT, int MT>
-__global__ __launch_bounds__(kExpertThreads) void down_kernel(ExpertArgs a) {
+__global__ __launch_bounds__(kExpertThreads, 2) void down_kernel(ExpertArgs a) {
   const int wave = wave_id();
   const int rtiles = a.H / (kRowTile * kDownRows);
   const int groups = (rtiles + kExpertWaves - 1) / kExpertWaves;
