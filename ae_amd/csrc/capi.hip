@@ -139,11 +139,10 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
     const int64_t per = nchunks / s;
     const int64_t ss = divisor_at_most(schunks, (schunks + per - 1) / per);
-    const int64_t span = T < kTokTile * kMaxTokTiles ? T : kTokTile * kMaxTokTiles;
     p.Is = static_cast<int>(Is);
     p.s_splits = static_cast<int>(ss);
     p.s_split_steps = static_cast<int>(schunks / ss * kUnroll);
-    p.s_tok_groups = static_cast<int>((T + span - 1) / span);
+    p.s_tok_groups = static_cast<int>((T + p.span - 1) / p.span);
     p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + kExpertWaves - 1) / kExpertWaves));
     p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves) * ss);
   }

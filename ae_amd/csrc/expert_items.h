@@ -1,0 +1,152 @@
+// Device helpers of the expert kernels: buffer resources, the workgroup barrier, the K-walk
+// rotation, output stores and the work-item decode.
+#pragma once
+
+#include "smx_kernels.h"
+
+namespace smx {
+
+constexpr int kBufDword3 = 0x00020000;            // gfx9 raw-buffer resource word 3
+constexpr int kNonTemporal = 2;                   // cache-policy bit: streaming (read once)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufDword3);
+}
+
+// Workgroup barrier ordering LDS only: in-flight global loads stay in flight.
+__device__ __forceinline__ void wg_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Order in which a workgroup walks its K chunks: step c reads chunk (c + rot) mod n. The
+// accumulation order over K is then a fixed rotation per workgroup (deterministic run to run).
+struct ChunkOrder {
+  int n, rot;
+  __device__ __forceinline__ int at(int c) const {
+    const int p = c + rot;
+    return p >= n ? p - n : p;
+  }
+};
+
+// Gate/up workgroups start their K walk at different chunks. W1/W3 rows have a pitch of H
+// elements, a power of two in bytes for the common hidden sizes (4096 and 8192 bytes in
+// bf16): workgroups that sit at the same chunk at the same moment, as they do when they start
+// together, then stream addresses that agree in their low 12-13 bits. Rotating the start by
+// (weight-group index) / 4 measured 5.6 -> 6.1 TB/s on the H = 2048 gate/up stream and 6.3 ->
+// 6.7 TB/s on H = 4096 (other rotations tried: index mod n, which keeps each XCD's workgroups
+// on a few residues, was slower than none at H = 4096). The down projection's rows (pitch I)
+// are walked in order: its K splits already start at different chunks, and rotating them
+// measured no gain.
+__device__ __forceinline__ ChunkOrder rotated_order(int n, int index) {
+  return ChunkOrder{n, (index >> 2) % n};
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+
+// Store 4 consecutive elements (one accumulator register group) of an output row.
+template <int DT>
+__device__ __forceinline__ void store4(void* base, int64_t idx, float v0, float v1, float v2, float v3) {
+  using S = typename Elem<DT>::S;
+  if constexpr (DT == kF32) {
+    f32x4 v = {v0, v1, v2, v3};
+    *reinterpret_cast<f32x4*>(static_cast<float*>(base) + idx) = v;
+  } else {
+    const uint32_t lo = static_cast<uint32_t>(Elem<DT>::from_f32(v0)) |
+                        (static_cast<uint32_t>(Elem<DT>::from_f32(v1)) << 16);
+    const uint32_t hi = static_cast<uint32_t>(Elem<DT>::from_f32(v2)) |
+                        (static_cast<uint32_t>(Elem<DT>::from_f32(v3)) << 16);
+    u32x2 v = {lo, hi};
+    *reinterpret_cast<u32x2*>(static_cast<S*>(base) + idx) = v;
+  }
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32));
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// The work item of one workgroup: an expert page and a list of m token rows starting at
+// position `off` (routed: sorted positions, token = sorted_f / k; shared expert: token rows
+// off.. directly). `tg` is the workgroup's index among the item's workgroups; `rot` is the
+// index the K-walk rotation derives from -- the same for every token range of one expert, so
+// that ranges streaming the same rows side by side read them in the same order.
+struct WorkItem {
+  const char* page;
+  int64_t page_bytes;
+  int I;
+  int off, m, tg, rot;
+  int nr;  // token ranges of the item's expert (1: its weights are read by this item only)
+  bool shared;
+};
+
+// Leading `sh.*_blocks` workgroups run the shared expert (v = token range, then tg); the rest
+// run the routing's work ranges (j = range, then tg). Returns false for a workgroup past the
+// ranges of this batch.
+template <typename S>
+__device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
+                                          WorkItem& w) {
+  const int64_t elem = static_cast<int64_t>(sizeof(S));
+  const int b = blockIdx.x;
+  if (b < shared_blocks) {
+    const int v = b / per_item;
+    const int span = a.rb.span;
+    w.page = static_cast<const char*>(a.sh.page);
+    w.page_bytes = 3 * static_cast<int64_t>(a.H) * a.sh.I * elem;
+    w.I = a.sh.I;
+    w.off = v * span;
+    w.m = min(span, a.T - w.off);
+    w.tg = b - v * per_item;
+    w.rot = w.tg;
+    w.nr = 1;
+    w.shared = true;
+    return true;
+  }
+  const int rb = b - shared_blocks;
+  const int j = rb / per_item;  // one of the expert's ranges; uniform across the workgroup
+  // j is below the launch's range bound, so the record may be read before the range count is
+  // known (the loads then share one latency); records past the count are unused.
+  const int nranges = uniform(a.rb.hdr[0]);
+  const RangeRec& rr = a.rb.ranges[j];
+  const int off = uniform(rr.off);
+  const int cnt = uniform(rr.cnt);
+  const int key = uniform(rr.key);
+  const int j0 = uniform(rr.j0);
+  const int nr = max(uniform(rr.nr), 1);
+  const int64_t slot = uniform64(rr.slot);
+  // The expert's nr * per_item items, numbered so that the nr ranges of weight group g are 8
+  // items apart: workgroups are dealt to the 8 XCDs round robin, so they run on one XCD, side
+  // by side, and share its L2 for the rows they all read. Groups past the last multiple of 8
+  // are numbered the same way with their own count as the spacing.
+  const int local = rb - j0 * per_item;
+  int g = local, r = 0;
+  if (nr > 1) {
+    const int full = per_item / 8 * 8 * nr;
+    if (local < full) {
+      const int blk = local / (8 * nr);
+      const int in = local - blk * 8 * nr;
+      r = in / 8;
+      g = blk * 8 + (in - r * 8);
+    } else {
+      const int rem = per_item % 8;
+      const int in = local - full;
+      r = in / rem;
+      g = per_item / 8 * 8 + (in - r * rem);
+    }
+  }
+  w.off = off + r * a.rb.span;
+  w.m = min(a.rb.span, cnt - r * a.rb.span);
+  w.page_bytes = a.page_elems * elem;
+  w.page = static_cast<const char*>(a.pool) + slot * w.page_bytes;
+  w.I = a.I;
+  w.tg = g;
+  w.rot = (key + 1) * per_item + g;
+  w.nr = nr;
+  w.shared = false;
+  return j < nranges;
+}
+
+}  // namespace smx

@@ -53,7 +53,7 @@ struct RouteBuffers {
 
 // An always-active expert that every token passes through (the shared expert of the
 // Qwen-MoE and DeepSeek-V2 MoE blocks). It runs in the leading workgroups of the gate/up and
-// down launches: token range v (kTokTile * tok_tiles tokens) of the batch is one work item,
+// down launches: token range v (`span` tokens) of the batch is one work item,
 // like one routed expert's token list.
 struct SharedArgs {
   const void* page;     // [3 * I * H] page in the routed layout; null when absent

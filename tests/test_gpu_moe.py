@@ -59,6 +59,31 @@ def test_fused_forward_matches_oracle(dtype, T, H, I, E, k, P):
     assert err <= TOL[dtype], err
 
 
+# Large batches: experts with several 64-token ranges (run side by side on one XCD).
+LARGE_CASES = [
+    # T, H, I, E, k, slots
+    (256, 256, 128, 8, 2, 8),
+    (300, 128, 256, 4, 2, 6),      # ragged last range of every expert
+    (520, 256, 128, 16, 4, 20),
+    (257, 128, 128, 3, 3, 3),      # every expert sees every token: 3 ranges each
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("T,H,I,E,k,P", LARGE_CASES)
+def test_large_batch_matches_oracle(dtype, T, H, I, E, k, P):
+    x, logits = _inputs(T, H, E, dtype, seed=T + H + I)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E)
+    y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                  return_routing=True)
+    torch.cuda.synchronize()
+    y_ref, w_ref, ids_ref = _oracle_forward(x, logits, pool, slots, k, True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    err = max_rel_err(f32_of(y), y_ref)
+    assert err <= TOL[dtype], err
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_stack_fused_moe_inplace_matches_oracle(dtype):
     T, H, I, E, k = 24, 256, 256, 8, 2

@@ -55,6 +55,7 @@ CASES = [
     (64, 128, 128, 8, 2, 512),
     (70, 256, 128, 8, 2, 256),     # two token ranges of the shared expert
     (130, 128, 256, 6, 3, 256),    # three token ranges
+    (300, 256, 128, 8, 2, 256),    # five token ranges
 ]
 
 
