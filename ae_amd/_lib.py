@@ -62,6 +62,8 @@ SIGNATURES = [
     ("smx_h2d_clear", ctypes.c_int, [_c_void_p, ctypes.c_char_p]),
     ("smx_h2d_set_enabled", ctypes.c_int, [_c_void_p, _i32]),
     ("smx_h2d_pending", ctypes.c_int, [_c_void_p]),
+    ("smx_set_tiled_min_tokens", ctypes.c_int, [_i64]),
+    ("smx_tiled_min_tokens", _i64, []),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

@@ -19,6 +19,13 @@ constexpr size_t kAlign = 256;
 // 143 us, 1 split 154 us) as long as the chip is covered (DeepSeek-V2-Lite T=1: 1 split
 // 14.1 us, 11 splits 12.2 us).
 constexpr int64_t kTargetDownWaves = 2048;
+// Tiled path (tiles.hip): its down workgroups to aim for (two per CU), and the default
+// expected tokens per active expert at which it takes over from the streaming kernels
+// (measured crossover: Mixtral 64 tokens per expert 613 vs 637 us, 32: 590 vs 502 us;
+// Qwen1.5-MoE 68: 378 vs 466 us, 34: 456 vs 293 us).
+constexpr int64_t kTileTargetDownBlocks = 512;
+constexpr int64_t kTileMinTokensDefault = 64;
+int64_t g_tile_min_tokens = kTileMinTokensDefault;
 
 // Optional measurement events (smx_set_profile_events): recorded on the launch stream
 // before routing and after each of the four kernels.
@@ -37,6 +44,7 @@ bool valid_dtype(int dt) { return dt == kF32 || dt == kF16 || dt == kBF16; }
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 struct Plan {
+  bool tiled = false;  // tiled expert kernels (many tokens per expert) instead of streaming
   int N = 0;
   int max_active = 0;  // experts that can be active: min(E, T*k)
   int span = 0;        // sorted positions per work range: the tokens of one kernel pass
@@ -112,39 +120,70 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
   Plan p;
   p.N = static_cast<int>(T * k);
   p.max_active = static_cast<int>(E < p.N ? E : p.N);
-  const int64_t tiles = (T + kTokTile - 1) / kTokTile;
-  p.tok_tiles = static_cast<int>(tiles < 1 ? 1 : (tiles > kMaxTokTiles ? kMaxTokTiles : tiles));
-  p.span = kTokTile * p.tok_tiles;
-  p.max_ranges = p.max_active + p.N / p.span;
   const int64_t eb = dtype_bytes(dtype);
-  const int64_t nchunks = I * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
   // Experts expected to be active under uniform routing, E * (1 - (1 - k/E)^T): small batches
   // activate fewer than min(E, T*k) experts (T=4, top-2 of 8: 5.5), and the split count is
-  // sized for the waves that will run.
+  // sized for the workgroups that will run.
   double active = static_cast<double>(E) * (1.0 - std::pow(1.0 - static_cast<double>(k) / E, static_cast<double>(T)));
   if (active > p.max_active) active = p.max_active;
   if (active < 1.0) active = 1.0;
-  const int64_t units = static_cast<int64_t>(active + 0.5) * (H / (kRowTile * kDownRows));
-  int64_t want = (kTargetDownWaves + units - 1) / units;
-  if (want < 1) want = 1;
-  // the fewest splits that reach the target, unless the chunk count's divisors overshoot it
-  // by more than 4x (a prime count leaves only 1 and itself)
-  int64_t s = divisor_at_least(nchunks, want);
-  if (s > 4 * want) s = divisor_at_most(nchunks, want);
-  p.splits = static_cast<int>(s);
-  p.split_steps = static_cast<int>(nchunks / s * kUnroll);
-  if (Is > 0) {
-    // The shared expert's down projection is split so that its waves stream about as many
-    // chunks as a routed wave; its token ranges match the kernel's token-tile span.
-    const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
-    const int64_t per = nchunks / s;
-    const int64_t ss = divisor_at_most(schunks, (schunks + per - 1) / per);
-    p.Is = static_cast<int>(Is);
-    p.s_splits = static_cast<int>(ss);
-    p.s_split_steps = static_cast<int>(schunks / ss * kUnroll);
-    p.s_tok_groups = static_cast<int>((T + p.span - 1) / p.span);
-    p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + kExpertWaves - 1) / kExpertWaves));
-    p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves) * ss);
+  p.tiled = p.N > 0 && static_cast<double>(p.N) / active >= static_cast<double>(g_tile_min_tokens);
+  int64_t s = 1;
+  if (p.tiled) {
+    p.span = kTileTok;
+    p.max_ranges = p.max_active + p.N / p.span;
+    // K steps of 128 bytes; the down projection's K is split into the fewest parts that give
+    // kTileTargetDownBlocks workgroups over the ranges expected
+    const int64_t nsteps = I * eb / 128;
+    // ranges expected under uniform routing: each active expert holds ceil(N / active / 128)
+    const int64_t ex = static_cast<int64_t>(active + 0.5);
+    const int64_t per_expert = (static_cast<int64_t>(p.N / active + 0.5) + kTileTok - 1) / kTileTok;
+    const int64_t ranges = ex * (per_expert < 1 ? 1 : per_expert);
+    const int64_t units = ranges * ((H + kTileDownRows - 1) / kTileDownRows);
+    const int64_t want = (kTileTargetDownBlocks + units - 1) / units;
+    s = divisor_at_least(nsteps, want);
+    if (s > 4 * want) s = divisor_at_most(nsteps, want);
+    p.splits = static_cast<int>(s);
+    p.split_steps = static_cast<int>(nsteps / s * 2);  // in 64-byte units
+    if (Is > 0) {
+      const int64_t ssteps = Is * eb / 128;
+      const int64_t per = nsteps / s;
+      const int64_t ss = divisor_at_most(ssteps, (ssteps + per - 1) / per);
+      p.Is = static_cast<int>(Is);
+      p.s_splits = static_cast<int>(ss);
+      p.s_split_steps = static_cast<int>(ssteps / ss * 2);
+      p.s_tok_groups = static_cast<int>((T + p.span - 1) / p.span);
+      p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is + kTileGateCols - 1) / kTileGateCols));
+      p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H + kTileDownRows - 1) / kTileDownRows) * ss);
+    }
+  } else {
+    const int64_t tiles = (T + kTokTile - 1) / kTokTile;
+    p.tok_tiles = static_cast<int>(tiles < 1 ? 1 : (tiles > kMaxTokTiles ? kMaxTokTiles : tiles));
+    p.span = kTokTile * p.tok_tiles;
+    p.max_ranges = p.max_active + p.N / p.span;
+    const int64_t nchunks = I * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+    const int64_t units = static_cast<int64_t>(active + 0.5) * (H / (kRowTile * kDownRows));
+    int64_t want = (kTargetDownWaves + units - 1) / units;
+    if (want < 1) want = 1;
+    // the fewest splits that reach the target, unless the chunk count's divisors overshoot it
+    // by more than 4x (a prime count leaves only 1 and itself)
+    s = divisor_at_least(nchunks, want);
+    if (s > 4 * want) s = divisor_at_most(nchunks, want);
+    p.splits = static_cast<int>(s);
+    p.split_steps = static_cast<int>(nchunks / s * kUnroll);
+    if (Is > 0) {
+      // The shared expert's down projection is split so that its waves stream about as many
+      // chunks as a routed wave; its token ranges match the kernel's token-tile span.
+      const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+      const int64_t per = nchunks / s;
+      const int64_t ss = divisor_at_most(schunks, (schunks + per - 1) / per);
+      p.Is = static_cast<int>(Is);
+      p.s_splits = static_cast<int>(ss);
+      p.s_split_steps = static_cast<int>(schunks / ss * kUnroll);
+      p.s_tok_groups = static_cast<int>((T + p.span - 1) / p.span);
+      p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + kExpertWaves - 1) / kExpertWaves));
+      p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves) * ss);
+    }
   }
   size_t o = 0;
   p.hdr = o;        o = align_up(o + 64);
@@ -218,10 +257,12 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
     a.sh.gateup_blocks = p.s_gateup_blocks;
     a.sh.down_blocks = p.s_down_blocks;
   }
-  hipError_t err = launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s);
+  hipError_t err = p.tiled ? launch_tile_gateup(dtype, a, p.max_ranges, s)
+                           : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(2, s);
-  err = launch_down(dtype, a, p.max_ranges, p.tok_tiles, s);
+  err = p.tiled ? launch_tile_down(dtype, a, p.max_ranges, s)
+                : launch_down(dtype, a, p.max_ranges, p.tok_tiles, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(3, s);
   CombineArgs c{};
@@ -522,6 +563,13 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
   return run_experts(p, dtype, hidden, hidden, T, H, I, E, top_k, pool, num_slots, page_elems,
                      expert_to_slot, w, ids, workspace, s, bt);
 }
+
+int smx_set_tiled_min_tokens(int64_t tokens_per_expert) {
+  g_tile_min_tokens = tokens_per_expert < 0 ? kTileMinTokensDefault : tokens_per_expert;
+  return SMX_OK;
+}
+
+int64_t smx_tiled_min_tokens(void) { return g_tile_min_tokens; }
 
 int smx_set_profile_events(void* const* events, int count) {
   if (events == nullptr || count == 0) {

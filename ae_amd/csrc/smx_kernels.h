@@ -27,6 +27,12 @@ constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 
 static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
               "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");
 
+// Tiled expert kernels (tiles.hip), for experts that see many tokens: output tiles of
+// 128 token rows by 128 intermediate columns (gate/up) or 256 W2 rows (down) per workgroup.
+constexpr int kTileTok = 128;        // sorted positions per work range
+constexpr int kTileGateCols = 128;   // intermediate columns per gate/up workgroup
+constexpr int kTileDownRows = 256;   // W2 rows per down workgroup
+
 // Work ranges of the expert kernels: up to `span` consecutive sorted positions of one active
 // expert. An expert with more tokens than one pass of the kernels holds is split into nr
 // ranges, numbered j0 .. j0 + nr - 1; each of them holds the same record (the expert's), so a
@@ -131,5 +137,7 @@ hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok
 hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
                        hipStream_t s);
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s);
+hipError_t launch_tile_gateup(int dtype, const ExpertArgs& a, int max_ranges, hipStream_t s);
+hipError_t launch_tile_down(int dtype, const ExpertArgs& a, int max_ranges, hipStream_t s);
 
 }  // namespace smx

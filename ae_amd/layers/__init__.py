@@ -1,7 +1,7 @@
 """Drop-in MoE layer operators (the reference's specmoe/layers MoE surface)."""
 from .FusedMoE import FusedMoE, UnquantizedFusedMoEMethod, set_weight_attrs
 from .fused_moe_kernel import (fused_moe_forward, fused_moe_shared_forward, moe_align_block_size,
-                               stack_fused_moe)
+                               set_tiled_min_tokens, stack_fused_moe, tiled_min_tokens)
 from .layernorm import RMSNorm, add_rmsnorm_gate
 from .mixtral_moe import MixtralMoE
 from .moe_layer import PostAttentionMoE, moe_layer_forward
@@ -13,4 +13,5 @@ __all__ = [
     "fused_moe_shared_forward", "moe_align_block_size", "stack_fused_moe", "MixtralMoE",
     "SharedExpertMoE", "Qwen2MoeSparseMoeBlock", "DeepseekV2MoE", "fused_topk", "select_experts",
     "RMSNorm", "add_rmsnorm_gate", "PostAttentionMoE", "moe_layer_forward",
+    "set_tiled_min_tokens", "tiled_min_tokens",
 ]

@@ -11,7 +11,8 @@ on the GPU) names the page of expert ``e``. Only the pages of routed experts are
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple
+import contextlib
+from typing import Iterator, Optional, Tuple
 
 import torch
 
@@ -43,6 +44,25 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_size: int,
     _lib.call("smx_moe_align_block_size", ptr(ids), numel, num_experts, block_size,
               ptr(sorted_ids), ptr(expert_ids), ptr(num_tokens_post_pad), stream_of(ids))
     return sorted_ids, expert_ids, num_tokens_post_pad
+
+
+def set_tiled_min_tokens(tokens_per_expert: Optional[int]) -> int:
+    """Set the expected tokens per active expert at which MoE calls switch from the
+    weight-streaming expert kernels to the tiled MFMA kernels (0: always tiled; None: the
+    library default). Returns the previous setting. Process-wide."""
+    prev = int(_lib.lib().smx_tiled_min_tokens())
+    _lib.call("smx_set_tiled_min_tokens", -1 if tokens_per_expert is None else int(tokens_per_expert))
+    return prev
+
+
+@contextlib.contextmanager
+def tiled_min_tokens(tokens_per_expert: Optional[int]) -> Iterator[None]:
+    """Scope a set_tiled_min_tokens setting (restored on exit)."""
+    prev = set_tiled_min_tokens(tokens_per_expert)
+    try:
+        yield
+    finally:
+        set_tiled_min_tokens(prev)
 
 
 def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:

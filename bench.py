@@ -37,6 +37,7 @@ import torch
 
 METRIC = "MoE layer us/verify-step + achieved HBM GB/s (% peak), Mixtral shape, 8-64 tokens"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak of one MI355X
 
 WORKLOADS = {
     "mixtral": dict(title="Mixtral-8x7B-shape MoE layer verify step", tokens=32, hidden=4096,
@@ -78,6 +79,10 @@ def parse():
                     help="measure host -> device streaming of expert pages through the transfer "
                          "engine (pinned host memory, chunked copies), alone and beside the MoE "
                          "kernels")
+    ap.add_argument("--tiled-min-tokens", type=int, default=None,
+                    help="expected tokens per active expert at which the tiled MFMA expert "
+                         "kernels replace the streaming ones (0 = always, a huge value = never; "
+                         "default: the library's)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy 10 times (HBM counter calibration)")
     return ap.parse_args()
@@ -219,6 +224,12 @@ def run_tokens(args, wl, T, layers, L, dev):
     step_bytes = layer_bytes * len(layers)
     gateup_bytes = ((len(active) * 2 * H * I + 2 * H * Is) * es + T * H * es
                     + (T * k * I + T * Is) * es)
+    gateup_flops = 2.0 * (T * k * 2 * H * I + T * 2 * H * Is)
+    step_flops = 2.0 * (T * k * 3 * H * I + T * 3 * H * Is) * len(layers)
+    # the library's choice of expert kernels: expected tokens per active expert vs its threshold
+    n_assign = T * k
+    exp_active = min(max(E * (1.0 - (1.0 - k / E) ** T), 1.0), min(E, n_assign))
+    tiled = n_assign > 0 and n_assign / exp_active >= L.smx_tiled_min_tokens()
 
     for i in range(args.warmup):
         step(i)
@@ -302,6 +313,7 @@ def run_tokens(args, wl, T, layers, L, dev):
         "tokens": T, "hidden": H, "ffn": I, "experts": E, "top_k": k,
         "routing": routing, "active_experts": len(active), "tokens_per_expert": counts,
         "pool_copies_rotated": copies,
+        "expert_kernels": "tiled" if tiled else "streaming",
     }
     if Is:
         config.update({"shared_ffn": Is, "shared_gate": wl["gated"]})
@@ -331,6 +343,7 @@ def run_tokens(args, wl, T, layers, L, dev):
         "us_per_step": round(us_step, 2),
         "layer_hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "algorithmic_bytes": step_bytes,
+        "tflops": round(step_flops / (us_step * 1e-6) / 1e12, 1),
         "wall_s_timed": round(wall, 4),
         "roofline": None,
         "cpu_baseline": None,
@@ -346,17 +359,32 @@ def run_tokens(args, wl, T, layers, L, dev):
         gateup_gbs = gateup_bytes / (stage_us[1] * 1e-6) / 1e9
         out["stage_us"] = {"route": round(stage_us[0], 2), "gate_up": round(stage_us[1], 2),
                            "down": round(stage_us[2], 2), "combine": round(stage_us[3], 2)}
-        out["roofline"] = {
-            "kernel": "gateup_kernel (W1/W3 stream + SiLU*up epilogue)",
-            "bound": "hbm",
-            "achieved": round(gateup_gbs, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(gateup_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(T, H, I, E, k, args.workload),
-            "algorithmic_bytes": gateup_bytes,
-            "us_per_launch": round(stage_us[1], 2),
-        }
+        if tiled:  # many tokens per expert: the matrix cores bound the tiled kernels
+            tflops = gateup_flops / (stage_us[1] * 1e-6) / 1e12
+            out["roofline"] = {
+                "kernel": "tile_gateup_kernel (W1/W3 x 128-token MFMA tiles + SiLU*up epilogue)",
+                "bound": "mfma",
+                "achieved": round(tflops, 1),
+                "peak": MFMA_BF16_PEAK_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "traffic": None,
+                "algorithmic_flops": gateup_flops,
+                "hbm_gbs": round(gateup_bytes / (stage_us[1] * 1e-6) / 1e9, 1),
+                "us_per_launch": round(stage_us[1], 2),
+            }
+        else:
+            out["roofline"] = {
+                "kernel": "gateup_kernel (W1/W3 stream + SiLU*up epilogue)",
+                "bound": "hbm",
+                "achieved": round(gateup_gbs, 1),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(gateup_gbs / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic(T, H, I, E, k, args.workload),
+                "algorithmic_bytes": gateup_bytes,
+                "us_per_launch": round(stage_us[1], 2),
+            }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args, wl, x, logits, sgate, layers[0], slots,
                                            layer_bytes)
@@ -388,6 +416,8 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     L = _lib.lib()
+    if args.tiled_min_tokens is not None:
+        _lib.check("smx_set_tiled_min_tokens", L.smx_set_tiled_min_tokens(args.tiled_min_tokens))
     g = torch.Generator(device=dev).manual_seed(0)
     copies = args.rotate if args.layers == 1 else 1  # a stack of layers is its own rotation
     layers = [Layer(g, dev, args.hidden, args.ffn, args.experts, wl["shared_ffn"], copies,

@@ -240,6 +240,22 @@ int smx_h2d_set_enabled(smx_h2d_engine* engine, int enabled);
 int smx_h2d_pending(smx_h2d_engine* engine);
 
 /*
+ * Expert-kernel selection. A MoE call whose expected tokens per active expert -- T*top_k
+ * divided by the experts expected to be active under uniform routing,
+ * E*(1 - (1 - top_k/E)^T) -- is at least `tokens_per_expert` runs the tiled expert kernels
+ * (MFMA output tiles of 128 tokens by 128 intermediate columns / 256 hidden rows, for
+ * prefill-sized batches); below it, the weight-streaming kernels. 0 = always tiled,
+ * INT64_MAX = never; a negative value restores the default (64). Both produce the same
+ * routing and rounding points; only the fp32 summation order over K differs. The workspace
+ * size depends on the choice, so query it after setting. Process-wide, not synchronised with
+ * calls in flight on other threads.
+ * Plays the role of the reference's per-call kernel configuration rule (T*top_k vs E picks
+ * the Triton tile sizes, specmoe/layers/fused_moe_kernel.py:293-306).
+ */
+int smx_set_tiled_min_tokens(int64_t tokens_per_expert);
+int64_t smx_tiled_min_tokens(void);
+
+/*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
  * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
  * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and

@@ -18,7 +18,7 @@ A = VP(0x10000)  # an aligned fake address: the calls below return before derefe
 def _declared():
     with open(HEADER) as f:
         text = f.read()
-    return re.findall(r"^\s*(?:int|size_t|const char\*)\s+(smx_\w+)\s*\(", text, re.M)
+    return re.findall(r"^\s*(?:int64_t|int|size_t|const char\*)\s+(smx_\w+)\s*\(", text, re.M)
 
 
 def test_library_built_in_tree():
@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 23, names
+    assert len(names) == 25, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -113,6 +113,24 @@ def test_profile_events_argument_checks():
     holes = (VP * 5)(A, A, VP(0), A, A)
     assert L.smx_set_profile_events(holes, 5) == _lib.SMX_ERR_INVALID_ARG
     assert L.smx_set_profile_events(None, 0) == _lib.SMX_OK
+
+
+def test_tiled_threshold_setting():
+    """The tiled-kernel threshold is process-wide; the workspace query follows it (the tiled
+    plan takes 128-token ranges and its own down-projection split)."""
+    default = L.smx_tiled_min_tokens()
+    assert default == 64
+    try:
+        never = (1 << 63) - 1
+        assert L.smx_set_tiled_min_tokens(never) == _lib.SMX_OK
+        assert L.smx_tiled_min_tokens() == never
+        stream_ws = L.smx_moe_workspace_size(1024, 4096, 14336, 8, 2, 2)
+        assert L.smx_set_tiled_min_tokens(0) == _lib.SMX_OK
+        tiled_ws = L.smx_moe_workspace_size(1024, 4096, 14336, 8, 2, 2)
+        assert tiled_ws > 0 and stream_ws > 0 and tiled_ws != stream_ws
+    finally:
+        assert L.smx_set_tiled_min_tokens(-1) == _lib.SMX_OK
+    assert L.smx_tiled_min_tokens() == default
 
 
 def test_python_error_mapping():

@@ -6,7 +6,7 @@ import torch
 
 from oracle import moe_ref as ref
 from ae_amd.layers import (FusedMoE, MixtralMoE, fused_moe_forward, select_experts,
-                           set_weight_attrs, stack_fused_moe)
+                           set_weight_attrs, stack_fused_moe, tiled_min_tokens)
 from tests.helpers import (TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle,
                            zipf_gate_logits)
 
@@ -59,7 +59,8 @@ def test_fused_forward_matches_oracle(dtype, T, H, I, E, k, P):
     assert err <= TOL[dtype], err
 
 
-# Large batches: experts with several 64-token ranges (run side by side on one XCD).
+# Large batches on the streaming kernels (forced: several of these reach the tiled kernels'
+# threshold): experts with several 64-token ranges (run side by side on one XCD).
 LARGE_CASES = [
     # T, H, I, E, k, slots
     (256, 256, 128, 8, 2, 8),
@@ -74,8 +75,9 @@ LARGE_CASES = [
 def test_large_batch_matches_oracle(dtype, T, H, I, E, k, P):
     x, logits = _inputs(T, H, E, dtype, seed=T + H + I)
     pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E)
-    y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
-                                  return_routing=True)
+    with tiled_min_tokens(1 << 62):
+        y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                      return_routing=True)
     torch.cuda.synchronize()
     y_ref, w_ref, ids_ref = _oracle_forward(x, logits, pool, slots, k, True)
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)

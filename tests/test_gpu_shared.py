@@ -7,7 +7,7 @@ import torch
 
 from oracle import moe_ref as ref
 from ae_amd.layers import (DeepseekV2MoE, Qwen2MoeSparseMoeBlock, fused_moe_forward,
-                           fused_moe_shared_forward, set_weight_attrs)
+                           fused_moe_shared_forward, set_weight_attrs, tiled_min_tokens)
 from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle
 
 pytestmark = pytest.mark.gpu
@@ -59,15 +59,21 @@ CASES = [
 ]
 
 
+# expert kernels: the weight-streaming ones or the tiled ones, forced either way
+PATHS = {"streaming": 1 << 62, "tiled": 0}
+
+
+@pytest.mark.parametrize("path", sorted(PATHS))
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("gated", [True, False])
 @pytest.mark.parametrize("T,H,I,E,k,Is", CASES)
-def test_shared_block_matches_oracle(dtype, gated, T, H, I, E, k, Is):
+def test_shared_block_matches_oracle(dtype, gated, T, H, I, E, k, Is, path):
     x, logits, sgate = _inputs(T, H, E, dtype, seed=T + Is)
     pool, slots = make_pool(E, H, I, dtype, num_slots=E + 2, seed=E + 1)
     page = _shared_page(H, Is, dtype, seed=Is)
-    _check(x, logits, pool, slots, k, gated, page, sgate if gated else None,
-           1.0 if gated else 2.5)
+    with tiled_min_tokens(PATHS[path]):
+        _check(x, logits, pool, slots, k, gated, page, sgate if gated else None,
+               1.0 if gated else 2.5)
 
 
 def test_no_shared_expert_is_scaled_routed():
