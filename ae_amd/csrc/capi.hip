@@ -141,14 +141,16 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     const int64_t ranges = ex * (per_expert < 1 ? 1 : per_expert);
     const int64_t units = ranges * ((H + kTileDownRows - 1) / kTileDownRows);
     const int64_t want = (kTileTargetDownBlocks + units - 1) / units;
-    s = divisor_at_least(nsteps, want);
-    if (s > 4 * want) s = divisor_at_most(nsteps, want);
+    // each split walks an even number of steps (the kernels' loop is unrolled by two), so the
+    // split count divides nsteps / 2 (whole: I * eb is a multiple of 256 bytes)
+    s = divisor_at_least(nsteps / 2, want);
+    if (s > 4 * want) s = divisor_at_most(nsteps / 2, want);
     p.splits = static_cast<int>(s);
     p.split_steps = static_cast<int>(nsteps / s * 2);  // in 64-byte units
     if (Is > 0) {
       const int64_t ssteps = Is * eb / 128;
       const int64_t per = nsteps / s;
-      const int64_t ss = divisor_at_most(ssteps, (ssteps + per - 1) / per);
+      const int64_t ss = divisor_at_most(ssteps / 2, (ssteps + per - 1) / per);
       p.Is = static_cast<int>(Is);
       p.s_splits = static_cast<int>(ss);
       p.s_split_steps = static_cast<int>(ssteps / ss * 2);

@@ -148,16 +148,54 @@ struct TWalk {
   int rb0, rb1;  // per lane: LDS slot of its A and B fragments, k-group 0 / 1, tile 0
 };
 
-// acc += the wave's 64 weight rows . the workgroup's 128 token rows over n K steps. Step c+1's
-// weights and token rows are loaded while step c is multiplied, then written to the wave's
-// weight tile (after this step's fragments were read from it) and to the other token stage
-// (one barrier per step). The loop body has no branches -- the last step reloads itself, in
-// bounds and unused -- so the waits the compiler places cover the current step's loads only,
-// and the sched_barrier fences keep the loads ahead of the MFMAs. Two workgroups per CU cover
-// each other's load waits.
+// acc += the wave's 64 weight rows . the workgroup's 128 token rows over n K steps (n even).
+// Weights are loaded two steps ahead (two register sets, the loop unrolled by two) and token
+// rows one step ahead; at the end of step c the wave writes step c+1's weights to its tile
+// (after reading step c's fragments from it) and the workgroup writes step c+1's token rows to
+// the other stage (one barrier per step). Step indices past the end are clamped to the last
+// step (reloads in bounds, unused), so the body has no branches and the waits the compiler
+// places cover only the loads they need; the sched_barrier fences keep the loads ahead of
+// the MFMAs. Two workgroups per CU cover each other's waits.
 template <int CP, int DT>
 __device__ __forceinline__ void tile_walk(const TWalk& wk, int n, u32x4* s0, u32x4* s1,
                                           u32x4* wtile, f32x4 (&acc)[kTATiles][kTBTiles]) {
+  WRegs r0, r1, frag;
+  TRegs tnext;
+  load_t(tnext, wk.t, 0);
+  load_w<CP>(r0, wk.w, 0);
+  load_w<CP>(r1, wk.w, min(1, n - 1));
+  store_t(tnext, s0, wk.wbase);
+  store_w(r0, wtile, wk.wa);
+  wg_barrier();
+  for (int c = 0; c < n; c += 2) {
+    // step c: tokens in s0, weights in the tile; r1 holds step c+1's weights
+    load_t(tnext, wk.t, min(c + 1, n - 1));
+    load_w<CP>(r0, wk.w, min(c + 2, n - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(frag, wtile, wk.rb0, wk.rb1);
+    mma_step<DT>(frag, s0, wk.rb0, wk.rb1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    store_t(tnext, s1, wk.wbase);
+    store_w(r1, wtile, wk.wa);
+    wg_barrier();
+    // step c+1: tokens in s1; r0 holds step c+2's weights
+    load_t(tnext, wk.t, min(c + 2, n - 1));
+    load_w<CP>(r1, wk.w, min(c + 3, n - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(frag, wtile, wk.rb0, wk.rb1);
+    mma_step<DT>(frag, s1, wk.rb0, wk.rb1, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    store_t(tnext, s0, wk.wbase);
+    store_w(r0, wtile, wk.wa);
+    wg_barrier();
+  }
+}
+
+// The same walk with weights loaded one step ahead (one register set), for fp32 (whose four
+// MFMAs per fragment need more registers than a second weight set leaves).
+template <int CP, int DT>
+__device__ __forceinline__ void tile_walk_1(const TWalk& wk, int n, u32x4* s0, u32x4* s1,
+                                            u32x4* wtile, f32x4 (&acc)[kTATiles][kTBTiles]) {
   WRegs raw, frag;
   TRegs tnext;
   load_t(tnext, wk.t, 0);
@@ -179,6 +217,13 @@ __device__ __forceinline__ void tile_walk(const TWalk& wk, int n, u32x4* s0, u32
     store_w(raw, wtile, wk.wa);
     wg_barrier();
   }
+}
+
+template <int CP, int DT>
+__device__ __forceinline__ void walk(const TWalk& wk, int n, u32x4* s0, u32x4* s1, u32x4* wtile,
+                                     f32x4 (&acc)[kTATiles][kTBTiles]) {
+  if constexpr (DT == kF32) tile_walk_1<CP, DT>(wk, n, s0, s1, wtile, acc);
+  else tile_walk<CP, DT>(wk, n, s0, s1, wtile, acc);
 }
 
 // Per-thread LDS addressing of the token stage (see the layout note at the top).
@@ -258,7 +303,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_gateup_kernel(ExpertAr
   zero_acc(acc);
   const int n = static_cast<int>(row_bytes / kTStep);
   // Weight rows are re-read by the other token ranges of the expert: normal caching.
-  tile_walk<0, DT>(wk, n, stage[0], stage[1], wtiles[wave], acc);
+  walk<0, DT>(wk, n, stage[0], stage[1], wtiles[wave], acc);
 
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   const int g = lane >> 4;
@@ -330,7 +375,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_down_kernel(ExpertArgs
   f32x4 acc[kTATiles][kTBTiles];
   zero_acc(acc);
   const int n = split_steps * kStepBytes / kTStep;
-  tile_walk<0, DT>(wk, n, stage[0], stage[1], wtiles[wave], acc);
+  walk<0, DT>(wk, n, stage[0], stage[1], wtiles[wave], acc);
 
   float* part = it.shared ? a.sh.part : a.part;
   const int g = lane >> 4;
