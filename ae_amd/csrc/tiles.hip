@@ -124,6 +124,30 @@ __device__ __forceinline__ void store_t(const TRegs& r, u32x4* stage, int wbase)
   for (int j = 0; j < kTBLoads; ++j) stage[wbase + j * kTRowsPerLoad * kTSlots] = r.v[j];
 }
 
+// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding.
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+// Token rows of a step straight into an LDS stage (buffer_load ... lds, 16 bytes per lane, no
+// registers): instruction j of wave w fills stage slots [256 j + 64 w, +64) in lane order. Slot
+// 256 j + 64 w + l is row q = 32 j + 8 w + l / 8 at position l % 8, which the swizzled layout
+// assigns the row's slot (l % 8) ^ swz(q); the per-lane offsets `off` (set for this path)
+// select those bytes.
+__device__ __forceinline__ void dma_t(const TRows& t, u32x4* stage, int step) {
+  const uint32_t kb = t.base + static_cast<uint32_t>(step) * kTStep;
+  const int w = wave_id();
+#pragma unroll
+  for (int j = 0; j < kTBLoads; ++j)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        t.rsrc, (__attribute__((address_space(3))) void*)(stage + j * kTRowsPerLoad * kTSlots + w * kWave),
+        16, t.off[j], kb, 0, 0);
+}
+
+// Workgroup barrier without a memory fence: the token stages are filled by LDS DMA, and a
+// fence would wait for every DMA in flight (also those for later steps); the callers wait for
+// the stage they need with an explicit vmcnt. The memory clobber keeps the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 // 64 MFMAs of one step: acc[i][bt] += A_i . B_bt over the step's two k-groups.
 template <int DT>
 __device__ __forceinline__ void mma_step(const WRegs& a, const u32x4* stage, int rb0, int rb1,
@@ -148,46 +172,58 @@ struct TWalk {
   int rb0, rb1;  // per lane: LDS slot of its A and B fragments, k-group 0 / 1, tile 0
 };
 
-// acc += the wave's 64 weight rows . the workgroup's 128 token rows over n K steps (n even).
-// Weights are loaded two steps ahead (two register sets, the loop unrolled by two) and token
-// rows one step ahead; at the end of step c the wave writes step c+1's weights to its tile
-// (after reading step c's fragments from it) and the workgroup writes step c+1's token rows to
-// the other stage (one barrier per step). Step indices past the end are clamped to the last
-// step (reloads in bounds, unused), so the body has no branches and the waits the compiler
-// places cover only the loads they need; the sched_barrier fences keep the loads ahead of
-// the MFMAs. Two workgroups per CU cover each other's waits.
+// One step of the 16-bit walk, for step c: its token rows are in stage `cur` and its weights in
+// the wave's tile. Step c+2's token rows go out by DMA into `dma_dst` (the stage step c-1 read)
+// and its weights into `issue_to`; after the MFMAs, step c+1's weights (`next`, loaded two steps
+// back) are written to the tile, the wave waits until step c+1's DMA has landed -- loads
+// issued after it: step c+1's weights (8), step c+2's DMA (4) and weights (8) -- and the
+// workgroup meets at the barrier.
 template <int CP, int DT>
-__device__ __forceinline__ void tile_walk(const TWalk& wk, int n, u32x4* s0, u32x4* s1,
-                                          u32x4* wtile, f32x4 (&acc)[kTATiles][kTBTiles]) {
+__device__ __forceinline__ void dma_step(WRegs& issue_to, const WRegs& next, WRegs& frag,
+                                         const u32x4* cur, u32x4* dma_dst, u32x4* wtile,
+                                         const TWalk& wk, int issue, f32x4 (&acc)[kTATiles][kTBTiles]) {
+  dma_t(wk.t, dma_dst, issue);
+  load_w<CP>(issue_to, wk.w, issue);
+  __builtin_amdgcn_sched_barrier(0);
+  read_frags(frag, wtile, wk.rb0, wk.rb1);
+  mma_step<DT>(frag, cur, wk.rb0, wk.rb1, acc);
+  __builtin_amdgcn_sched_barrier(0);
+  store_w(next, wtile, wk.wa);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTATiles * 2 + kTBLoads));
+  bare_barrier();
+}
+
+// acc += the wave's 64 weight rows . the workgroup's 128 token rows over n K steps (n even),
+// 16-bit types. Token rows go by DMA into three LDS stages, two steps ahead; weights two steps
+// ahead into two register sets, written to the wave's tile one step ahead (after the step's
+// fragments were read from it). The loop is unrolled by six so that every stage and register
+// set is a fixed object (the compiler then sees that a DMA in flight and the stage being read
+// do not alias). Step indices past the end are clamped to the last step (reloads in bounds,
+// into stages and registers no later step reads), so the body has no branches apart from the
+// exits between step pairs. Two workgroups per CU cover each other's waits.
+template <int CP, int DT>
+__device__ __forceinline__ void tile_walk(const TWalk& wk, int n, u32x4* st0, u32x4* st1,
+                                          u32x4* st2, u32x4* wtile,
+                                          f32x4 (&acc)[kTATiles][kTBTiles]) {
   WRegs r0, r1, frag;
-  TRegs tnext;
-  load_t(tnext, wk.t, 0);
+  dma_t(wk.t, st0, 0);
+  dma_t(wk.t, st1, min(1, n - 1));
   load_w<CP>(r0, wk.w, 0);
   load_w<CP>(r1, wk.w, min(1, n - 1));
-  store_t(tnext, s0, wk.wbase);
   store_w(r0, wtile, wk.wa);
-  wg_barrier();
-  for (int c = 0; c < n; c += 2) {
-    // step c: tokens in s0, weights in the tile; r1 holds step c+1's weights
-    load_t(tnext, wk.t, min(c + 1, n - 1));
-    load_w<CP>(r0, wk.w, min(c + 2, n - 1));
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(frag, wtile, wk.rb0, wk.rb1);
-    mma_step<DT>(frag, s0, wk.rb0, wk.rb1, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    store_t(tnext, s1, wk.wbase);
-    store_w(r1, wtile, wk.wa);
-    wg_barrier();
-    // step c+1: tokens in s1; r0 holds step c+2's weights
-    load_t(tnext, wk.t, min(c + 2, n - 1));
-    load_w<CP>(r1, wk.w, min(c + 3, n - 1));
-    __builtin_amdgcn_sched_barrier(0);
-    read_frags(frag, wtile, wk.rb0, wk.rb1);
-    mma_step<DT>(frag, s1, wk.rb0, wk.rb1, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    store_t(tnext, s0, wk.wbase);
-    store_w(r0, wtile, wk.wa);
-    wg_barrier();
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTATiles * 2 + kTBLoads));  // step 0's DMA
+  bare_barrier();
+  for (int c = 0;; c += 6) {
+    const int l = n - 1;
+    dma_step<CP, DT>(r0, r1, frag, st0, st2, wtile, wk, min(c + 2, l), acc);
+    dma_step<CP, DT>(r1, r0, frag, st1, st0, wtile, wk, min(c + 3, l), acc);
+    if (c + 2 >= n) break;
+    dma_step<CP, DT>(r0, r1, frag, st2, st1, wtile, wk, min(c + 4, l), acc);
+    dma_step<CP, DT>(r1, r0, frag, st0, st2, wtile, wk, min(c + 5, l), acc);
+    if (c + 4 >= n) break;
+    dma_step<CP, DT>(r0, r1, frag, st1, st0, wtile, wk, min(c + 6, l), acc);
+    dma_step<CP, DT>(r1, r0, frag, st2, st1, wtile, wk, min(c + 7, l), acc);
+    if (c + 6 >= n) break;
   }
 }
 
@@ -220,10 +256,20 @@ __device__ __forceinline__ void tile_walk_1(const TWalk& wk, int n, u32x4* s0, u
 }
 
 template <int CP, int DT>
-__device__ __forceinline__ void walk(const TWalk& wk, int n, u32x4* s0, u32x4* s1, u32x4* wtile,
-                                     f32x4 (&acc)[kTATiles][kTBTiles]) {
+__device__ __forceinline__ void walk(const TWalk& wk, int n, u32x4* s0, u32x4* s1, u32x4* s2,
+                                     u32x4* wtile, f32x4 (&acc)[kTATiles][kTBTiles]) {
   if constexpr (DT == kF32) tile_walk_1<CP, DT>(wk, n, s0, s1, wtile, acc);
-  else tile_walk<CP, DT>(wk, n, s0, s1, wtile, acc);
+  else tile_walk<CP, DT>(wk, n, s0, s1, s2, wtile, acc);
+}
+
+// Per-thread byte offset of token row `row`'s slot for this thread: the DMA path (16-bit
+// types) loads the slot its fixed LDS position holds, the register path its own slot.
+template <int DT>
+__device__ __forceinline__ uint32_t token_off(int row, int64_t row_bytes) {
+  const int tid = threadIdx.x;
+  int slot = tid % kTSlots;
+  if constexpr (DT != kF32) slot ^= tswz(tid / kTSlots);
+  return static_cast<uint32_t>(row * row_bytes + slot * 16);
 }
 
 // Per-thread LDS addressing of the token stage (see the layout note at the top).
@@ -267,7 +313,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_gateup_kernel(ExpertAr
   const int groups = (Iw + kTileGateCols - 1) / kTileGateCols;
   WorkItem it;
   if (!work_item<S>(a, a.sh.gateup_blocks, groups, it)) return;
-  __shared__ u32x4 stage[2][kTStage];
+  __shared__ u32x4 st0[kTStage], st1[kTStage], st2[DT == kF32 ? 1 : kTStage];
   __shared__ u32x4 wtiles[kExpertWaves][kTATiles * kRowTile * kTSlots];
   const int H = a.H, I = it.I;
   const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
@@ -296,14 +342,14 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_gateup_kernel(ExpertAr
 #pragma unroll
   for (int j = 0; j < kTBLoads; ++j) {
     const int tok = range_row(a, it, tid / kTSlots + j * kTRowsPerLoad, true);
-    wk.t.off[j] = static_cast<uint32_t>(tok * row_bytes + (tid % kTSlots) * 16);
+    wk.t.off[j] = token_off<DT>(tok, row_bytes);
   }
   stage_addressing(wk);
   f32x4 acc[kTATiles][kTBTiles];
   zero_acc(acc);
   const int n = static_cast<int>(row_bytes / kTStep);
   // Weight rows are re-read by the other token ranges of the expert: normal caching.
-  walk<0, DT>(wk, n, stage[0], stage[1], wtiles[wave], acc);
+  walk<0, DT>(wk, n, st0, st1, st2, wtiles[wave], acc);
 
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   const int g = lane >> 4;
@@ -337,7 +383,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_down_kernel(ExpertArgs
   const int split_steps = in_shared ? a.sh.split_steps : a.split_steps;  // 64-byte units
   WorkItem it;
   if (!work_item<S>(a, a.sh.down_blocks, rgroups * splits, it)) return;
-  __shared__ u32x4 stage[2][kTStage];
+  __shared__ u32x4 st0[kTStage], st1[kTStage], st2[DT == kF32 ? 1 : kTStage];
   __shared__ u32x4 wtiles[kExpertWaves][kTATiles * kRowTile * kTSlots];
   const int sp = it.tg / rgroups;
   const int rg = it.tg - sp * rgroups;
@@ -369,13 +415,13 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_down_kernel(ExpertArgs
 #pragma unroll
   for (int j = 0; j < kTBLoads; ++j) {
     const int row = range_row(a, it, tid / kTSlots + j * kTRowsPerLoad, false);
-    wk.t.off[j] = static_cast<uint32_t>(row * row_bytes + (tid % kTSlots) * 16);
+    wk.t.off[j] = token_off<DT>(row, row_bytes);
   }
   stage_addressing(wk);
   f32x4 acc[kTATiles][kTBTiles];
   zero_acc(acc);
   const int n = split_steps * kStepBytes / kTStep;
-  walk<0, DT>(wk, n, stage[0], stage[1], wtiles[wave], acc);
+  walk<0, DT>(wk, n, st0, st1, st2, wtiles[wave], acc);
 
   float* part = it.shared ? a.sh.part : a.part;
   const int g = lane >> 4;
