@@ -213,6 +213,28 @@ def test_other_model_shapes(T, H, I, E, k, renorm):
     assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("path", ["default", "tiled"])
+def test_cpu_reference_config(path):
+    """The survey's CPU-path configuration: hidden 1024, ffn 2816, 8 experts, top-2, fp32,
+    32 tokens (4 sequences x 8 draft tokens) of N(0,1) hidden states, gate and expert weights
+    N(0, 0.02), seed 0; the router logits are x Wg^T. On the default plan (weight-streaming
+    kernels at 8 tokens per expert) and with the tiled kernels forced."""
+    T, H, I, E, k = 32, 1024, 2816, 8, 2
+    g = torch.Generator(device=DEV).manual_seed(0)
+    x = torch.randn((T, H), generator=g, device=DEV)
+    wg = torch.randn((E, H), generator=g, device=DEV) * 0.02
+    logits = x @ wg.T
+    pool, slots = make_pool(E, H, I, torch.float32, seed=0)
+    with tiled_min_tokens(0 if path == "tiled" else None):
+        y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                      return_routing=True)
+    torch.cuda.synchronize()
+    y_ref, w_ref, ids_ref = _oracle_forward(x, logits, pool, slots, k, True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[torch.float32]
+
+
 @pytest.mark.parametrize("T", [1, 8, 32, 64])
 def test_mixtral_full_size(T):
     """Mixtral-8x7B MoE layer (H=4096, I=14336, E=8, top-2, bf16) with the Zipf-skewed gate."""
