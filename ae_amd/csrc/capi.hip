@@ -24,6 +24,14 @@ constexpr int64_t kTargetDownWaves = 2048;
 // (measured crossover: Mixtral 64 tokens per expert 613 vs 637 us, 32: 590 vs 502 us;
 // Qwen1.5-MoE 68: 378 vs 466 us, 34: 456 vs 293 us).
 constexpr int64_t kTileTargetDownBlocks = 512;
+// From this many expected tokens per active expert the down projection aims for 4x the
+// workgroups: with ~2 rounds of workgroups the last round ran mostly empty (Mixtral 4096 tokens:
+// 1072 workgroups on 512 slots; 2 K splits: down 1164 -> 1035 us, the combine's extra split 33 ->
+// 56 us). Below it the extra splits cost more in the combine than they save.
+constexpr int64_t kTileLargeTokens = 512;
+// Batches from this many tokens combine with one thread per 8 outputs (combine_rows_kernel);
+// smaller ones with one workgroup per (token, 256 outputs), one wave per assignment.
+constexpr int64_t kCombineRowsMinTokens = 256;
 constexpr int64_t kTileMinTokensDefault = 64;
 int64_t g_tile_min_tokens = kTileMinTokensDefault;
 
@@ -140,7 +148,9 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     const int64_t per_expert = (static_cast<int64_t>(p.N / active + 0.5) + kTileTok - 1) / kTileTok;
     const int64_t ranges = ex * (per_expert < 1 ? 1 : per_expert);
     const int64_t units = ranges * ((H + kTileDownRows - 1) / kTileDownRows);
-    const int64_t want = (kTileTargetDownBlocks + units - 1) / units;
+    const int64_t target = static_cast<double>(p.N) / active >= kTileLargeTokens ? 4 * kTileTargetDownBlocks
+                                                                               : kTileTargetDownBlocks;
+    const int64_t want = (target + units - 1) / units;
     // each split walks an even number of steps (the kernels' loop is unrolled by two), so the
     // split count divides nsteps / 2 (whole: I * eb is a multiple of 256 bytes)
     s = divisor_at_least(nsteps / 2, want);
@@ -282,6 +292,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   c.splits_s = p.s_splits;
   c.sgate = bt.sgate;
   c.sgate_dtype = bt.sgate_dtype;
+  c.rows = T >= kCombineRowsMinTokens ? 1 : 0;
   err = launch_combine(dtype, c, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(4, s);

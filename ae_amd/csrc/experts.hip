@@ -468,6 +468,77 @@ __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(Combi
   store4<DT>(c.y, static_cast<int64_t>(t) * c.H + h, y[0], y[1], y[2], y[3]);
 }
 
+// Combine for large batches: one thread per 8 consecutive outputs of a token, every
+// assignment of the token (and the shared expert) summed in the same order as combine_kernel
+// -- splits in order from 0, then round(w * sum) added over j in order, then the block form --
+// so both kernels give identical bits. No LDS or barriers; at thousands of tokens the
+// per-(token, 256 outputs) workgroups of combine_kernel are bound by workgroup dispatch.
+constexpr int kCombineRowThreads = 256;
+constexpr int kCombineRowOuts = 8;
+
+template <int DT>
+__global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(CombineArgs c) {
+  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * kCombineRowThreads + threadIdx.x) * kCombineRowOuts;
+  if (idx >= static_cast<int64_t>(c.T) * c.H) return;
+  const int t = static_cast<int>(idx / c.H);
+  const int h = static_cast<int>(idx - static_cast<int64_t>(t) * c.H);
+  const uint32_t vm = static_cast<uint32_t>(c.tmask[t]);
+  const int64_t split_stride = static_cast<int64_t>(c.T) * c.k * c.H;
+  f32x4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < c.k; ++j) {
+    if (!((vm >> j) & 1u)) continue;
+    const int64_t f = static_cast<int64_t>(t) * c.k + j;
+    const float* src = c.part + f * c.H + h;
+    f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < c.splits; ++sp) {
+      v0 += *reinterpret_cast<const f32x4*>(src + sp * split_stride);
+      v1 += *reinterpret_cast<const f32x4*>(src + sp * split_stride + 4);
+    }
+    const float wf = c.w[f];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y0[e] += Elem<DT>::round(v0[e] * wf);
+      y1[e] += Elem<DT>::round(v1[e] * wf);
+    }
+  }
+  if (c.block) {
+    const bool scaled = c.scale != 1.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      y0[e] = Elem<DT>::round(y0[e]);
+      y1[e] = Elem<DT>::round(y1[e]);
+      if (scaled) {
+        y0[e] = Elem<DT>::round(y0[e] * c.scale);
+        y1[e] = Elem<DT>::round(y1[e] * c.scale);
+      }
+    }
+    if (c.part_s) {
+      const int64_t sstride = static_cast<int64_t>(c.T) * c.H;
+      const float* src = c.part_s + static_cast<int64_t>(t) * c.H + h;
+      f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < c.splits_s; ++sp) {
+        d0 += *reinterpret_cast<const f32x4*>(src + sp * sstride);
+        d1 += *reinterpret_cast<const f32x4*>(src + sp * sstride + 4);
+      }
+      const bool gated = c.sgate != nullptr;
+      float gs = 1.0f;
+      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + __expf(-load_scalar(c.sgate, c.sgate_dtype, t))));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float s0 = Elem<DT>::round(d0[e]), s1 = Elem<DT>::round(d1[e]);
+        if (gated) {
+          s0 = Elem<DT>::round(gs * s0);
+          s1 = Elem<DT>::round(gs * s1);
+        }
+        y0[e] += s0;
+        y1[e] += s1;
+      }
+    }
+  }
+  store4<DT>(c.y, idx, y0[0], y0[1], y0[2], y0[3]);
+  store4<DT>(c.y, idx + 4, y1[0], y1[1], y1[2], y1[3]);
+}
+
 template <bool kMulti, int DT, int MT>
 static void launch_stage_m(int stage, const ExpertArgs& a, int max_ranges, hipStream_t s) {
   if (stage == 0) {
@@ -518,6 +589,16 @@ hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_t
 }
 
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s) {
+  if (c.rows) {
+    const int64_t outs = static_cast<int64_t>(c.T) * c.H / kCombineRowOuts;
+    const unsigned blocks = static_cast<unsigned>((outs + kCombineRowThreads - 1) / kCombineRowThreads);
+    switch (dtype) {
+      case kF32: combine_rows_kernel<kF32><<<blocks, kCombineRowThreads, 0, s>>>(c); break;
+      case kF16: combine_rows_kernel<kF16><<<blocks, kCombineRowThreads, 0, s>>>(c); break;
+      default: combine_rows_kernel<kBF16><<<blocks, kCombineRowThreads, 0, s>>>(c); break;
+    }
+    return hipGetLastError();
+  }
   const int chunks = (c.H + 4 * kWave - 1) / (4 * kWave);
   const unsigned blocks = static_cast<unsigned>(static_cast<int64_t>(c.T) * chunks);
   const int items = c.k + (c.part_s != nullptr ? 1 : 0);

@@ -100,6 +100,7 @@ struct CombineArgs {
   int splits_s;
   const void* sgate;         // [T] shared-expert gate logits (s = sigmoid), null: s = 1
   int sgate_dtype;
+  int rows;                  // thread-per-outputs kernel (large batches) instead of per-token
 };
 
 // Post-attention residual add + RMSNorm + router gate (+ shared-expert gate row, + top-k).
