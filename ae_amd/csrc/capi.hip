@@ -6,6 +6,7 @@
 #include "../../include/specmoe_mi355x.h"
 #include "smx_kernels.h"
 
+#include <algorithm>
 #include <cmath>
 
 namespace {
@@ -75,15 +76,26 @@ int check_shape(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype
   if (T < 0 || H <= 0 || I <= 0 || E <= 0 || k <= 0 || !valid_dtype(dtype)) return SMX_ERR_INVALID_ARG;
   if (k > E) return SMX_ERR_INVALID_ARG;
   if (E > kMaxExperts || k > kMaxTopK) return SMX_ERR_UNSUPPORTED;
-  if (T * k > kMaxAssignments) return SMX_ERR_UNSUPPORTED;
   const int64_t eb = dtype_bytes(dtype);
   const int64_t chunk = static_cast<int64_t>(kStepBytes) * kUnroll;  // bytes per pipelined chunk
   if ((H * eb) % chunk != 0 || (I * eb) % chunk != 0) return SMX_ERR_UNSUPPORTED;
   if (H % (kRowTile * kDownRows) != 0 || I % kRowTile != 0) return SMX_ERR_UNSUPPORTED;
   if (H > (1 << 20) || I > (1 << 20)) return SMX_ERR_UNSUPPORTED;
-  // per-lane token/activation offsets are 32-bit
-  if (T * H * eb >= (int64_t{1} << 31) || T * k * I * eb >= (int64_t{1} << 31)) return SMX_ERR_UNSUPPORTED;
   return SMX_OK;
+}
+
+// Tokens per pass of the kernels: the expert sort holds at most kMaxAssignments assignments in
+// one workgroup's LDS, and per-lane offsets into the hidden states and activations are 32-bit.
+// Calls with more tokens run as consecutive passes over token chunks on the same stream (each
+// token's output depends on its own row only), sharing the workspace.
+int64_t chunk_tokens(int64_t T, int64_t H, int64_t I, int64_t k, int64_t Is, int dtype) {
+  const int64_t eb = dtype_bytes(dtype);
+  const int64_t lim = (int64_t{1} << 31) - 1;
+  int64_t c = kMaxAssignments / k;
+  c = std::min(c, lim / (H * eb));
+  c = std::min(c, lim / (k * I * eb));
+  if (Is > 0) c = std::min(c, lim / (Is * eb));
+  return std::max<int64_t>(1, std::min(T, c));
 }
 
 // Smallest divisor of n that is >= want (n when want > n).
@@ -109,7 +121,8 @@ int check_shared(int64_t T, int64_t H, int64_t Is, int dtype) {
   const int64_t eb = dtype_bytes(dtype);
   const int64_t chunk = static_cast<int64_t>(kStepBytes) * kUnroll;
   if ((Is * eb) % chunk != 0 || Is % kRowTile != 0 || Is > (1 << 20)) return SMX_ERR_UNSUPPORTED;
-  if (3 * H * Is * eb >= (int64_t{1} << 32) || T * Is * eb >= (int64_t{1} << 31)) return SMX_ERR_UNSUPPORTED;
+  if (3 * H * Is * eb >= (int64_t{1} << 32)) return SMX_ERR_UNSUPPORTED;
+  (void)T;
   return SMX_OK;
 }
 
@@ -216,6 +229,17 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
   }
   p.total = o;
   return p;
+}
+
+// Workspace of a call of T tokens: the larger of the plans of its full token chunks and of its
+// last, partial one.
+size_t workspace_for(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype, int64_t Is,
+                     bool layer) {
+  const int64_t tc = chunk_tokens(T, H, I, k, Is, dtype);
+  size_t total = make_plan(tc, H, I, E, k, dtype, Is, layer).total;
+  const int64_t rest = T % tc;
+  if (T > tc && rest > 0) total = std::max(total, make_plan(rest, H, I, E, k, dtype, Is, layer).total);
+  return total;
 }
 
 RouteBuffers carve(const Plan& p, void* ws) {
@@ -354,7 +378,7 @@ int smx_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E, 
 
 size_t smx_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k, int dtype) {
   if (check_shape(T, H, I, E, top_k, dtype) != SMX_OK) return 0;
-  return make_plan(T, H, I, E, top_k, dtype).total;
+  return workspace_for(T, H, I, E, top_k, dtype, 0, false);
 }
 
 int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
@@ -370,6 +394,19 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
   rc = check_shape(T, H, I, E, top_k, dtype);
   if (rc != SMX_OK) return rc;
   if (!topk_weights || !topk_ids || !workspace) return SMX_ERR_INVALID_ARG;
+  const int64_t tc = chunk_tokens(T, H, I, top_k, 0, dtype);
+  if (T > tc) {
+    if (workspace_bytes < workspace_for(T, H, I, E, top_k, dtype, 0, false)) return SMX_ERR_WORKSPACE;
+    const int64_t rb = H * dtype_bytes(dtype);
+    for (int64_t t0 = 0; t0 < T; t0 += tc) {
+      rc = smx_stack_fused_moe(static_cast<const char*>(hidden) + t0 * rb, static_cast<char*>(out) + t0 * rb,
+                               dtype, std::min(tc, T - t0), H, pool, num_slots, page_elems, expert_to_slot,
+                               E, topk_weights + t0 * top_k, topk_ids + t0 * top_k, top_k, workspace,
+                               workspace_bytes, stream);
+      if (rc != SMX_OK) return rc;
+    }
+    return SMX_OK;
+  }
   const Plan p = make_plan(T, H, I, E, top_k, dtype);
   if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
   if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
@@ -406,6 +443,24 @@ int fused_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H
   rc = check_shared(T, H, Is, dtype);
   if (rc != SMX_OK) return rc;
   if (!router_logits || !workspace) return SMX_ERR_INVALID_ARG;
+  const int64_t tc = chunk_tokens(T, H, I, top_k, Is, dtype);
+  if (T > tc) {
+    if (workspace_bytes < workspace_for(T, H, I, E, top_k, dtype, Is, false)) return SMX_ERR_WORKSPACE;
+    const int64_t rb = H * dtype_bytes(dtype);
+    const int64_t lb = E * dtype_bytes(logits_dtype);
+    for (int64_t t0 = 0; t0 < T; t0 += tc) {
+      BlockTerms bc = bt;
+      if (bc.sgate) bc.sgate = static_cast<const char*>(bc.sgate) + t0 * dtype_bytes(bc.sgate_dtype);
+      rc = fused_forward(static_cast<const char*>(hidden) + t0 * rb, static_cast<char*>(out) + t0 * rb, dtype,
+                         std::min(tc, T - t0), H, static_cast<const char*>(router_logits) + t0 * lb,
+                         logits_dtype, E, top_k, renormalize, pool, num_slots, page_elems, expert_to_slot,
+                         Is, bc, topk_weights_out ? topk_weights_out + t0 * top_k : nullptr,
+                         topk_ids_out ? topk_ids_out + t0 * top_k : nullptr, workspace, workspace_bytes,
+                         stream);
+      if (rc != SMX_OK) return rc;
+    }
+    return SMX_OK;
+  }
   const Plan p = make_plan(T, H, I, E, top_k, dtype, Is);
   if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
   if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
@@ -442,7 +497,7 @@ size_t smx_moe_shared_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E,
                                      int64_t shared_I, int dtype) {
   if (check_shape(T, H, I, E, top_k, dtype) != SMX_OK || check_shared(T, H, shared_I, dtype) != SMX_OK)
     return 0;
-  return make_plan(T, H, I, E, top_k, dtype, shared_I).total;
+  return workspace_for(T, H, I, E, top_k, dtype, shared_I, false);
 }
 
 int smx_fused_moe_shared_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
@@ -502,7 +557,7 @@ size_t smx_moe_layer_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, 
   if (check_shape(T, H, I, E, top_k, dtype) != SMX_OK || check_shared(T, H, shared_I, dtype) != SMX_OK ||
       check_norm(H, dtype) != SMX_OK)
     return 0;
-  return make_plan(T, H, I, E, top_k, dtype, shared_I, true).total;
+  return workspace_for(T, H, I, E, top_k, dtype, shared_I, true);
 }
 
 int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, int64_t H,
@@ -535,6 +590,23 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
       (shared_page && !aligned16(shared_page)) ||
       (shared_gate_weight && !aligned16(shared_gate_weight)))
     return SMX_ERR_MISALIGNED;
+  const int64_t tc = chunk_tokens(T, H, I, top_k, shared_I, dtype);
+  if (T > tc) {
+    if (workspace_bytes < workspace_for(T, H, I, E, top_k, dtype, shared_I, true)) return SMX_ERR_WORKSPACE;
+    const int64_t rb = H * dtype_bytes(dtype);
+    const int64_t lb = E * dtype_bytes(dtype);
+    for (int64_t t0 = 0; t0 < T; t0 += tc) {
+      rc = smx_moe_layer_forward(
+          static_cast<char*>(hidden) + t0 * rb, static_cast<char*>(residual) + t0 * rb, dtype,
+          std::min(tc, T - t0), H, norm_weight, eps, gate_weight, E, top_k, renormalize, pool, num_slots,
+          page_elems, expert_to_slot, shared_page, shared_I, shared_gate_weight, routed_scaling_factor,
+          router_logits_out ? static_cast<char*>(router_logits_out) + t0 * lb : nullptr,
+          topk_weights_out ? topk_weights_out + t0 * top_k : nullptr,
+          topk_ids_out ? topk_ids_out + t0 * top_k : nullptr, workspace, workspace_bytes, stream);
+      if (rc != SMX_OK) return rc;
+    }
+    return SMX_OK;
+  }
   const Plan p = make_plan(T, H, I, E, top_k, dtype, shared_I, true);
   if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
   if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;

@@ -40,10 +40,12 @@ enum smx_status {
   SMX_ERR_NOT_FOUND = 1005        /* smx_h2d_wait: no such task id (or it was cleared) */
 };
 
-/* Limits: 1 <= E <= 256; 1 <= top_k <= min(E, 16); T*top_k <= 16384;
- * H and I multiples of 128 for 16-bit types and of 64 for fp32 (a weight row is a whole
- * number of 256-byte chunks); H, I <= 2^20; T*H and T*top_k*I activation bytes < 2^31;
- * page_elems <= 2^30 and page bytes < 2^32.
+/* Limits: 1 <= E <= 256; 1 <= top_k <= min(E, 16); H and I multiples of 128 for 16-bit
+ * types and of 64 for fp32 (a weight row is a whole number of 256-byte chunks); H, I <= 2^20;
+ * page_elems <= 2^30 and page bytes < 2^32. Any T: a MoE call with more than 16384
+ * assignments (T*top_k), or whose activations exceed 2^31 bytes, runs as consecutive passes
+ * over token chunks on its stream (the expert sort holds 16384 assignments), sharing the
+ * workspace, which the *_workspace_size queries size for the largest chunk.
  * T == 0 is a no-op. Shapes outside these limits return SMX_ERR_UNSUPPORTED. */
 
 /* Library version (major*10000 + minor*100 + patch). */

@@ -185,3 +185,9 @@ def test_post_attention_module(kind):
     # the two paths compute router logits with different accumulation orders (gate kernel vs
     # torch GEMM); compare against each other to the output tolerance
     assert max_rel_err(f32_of(y), f32_of(y2)) <= 2 * TOL[dt]
+
+
+def test_layer_forward_token_chunks():
+    """The whole post-attention call with 9000 tokens at top-2 (18000 assignments, two token
+    chunks): residual, logits, routing and outputs on every token."""
+    _layer_case(9000, 128, 128, 8, 2, True, seed=97)

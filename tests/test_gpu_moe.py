@@ -254,3 +254,33 @@ def test_mixtral_full_size(T):
     err = max_rel_err(f32_of(y), y_ref)
     print(f"mixtral T={T}: max rel err {err:.3e}")
     assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("inplace", [False, True])
+def test_more_than_16384_assignments_run_in_token_chunks(inplace):
+    """T*top_k above the expert sort's 16384: the call runs as consecutive token chunks (8192
+    tokens at top-2) sharing one workspace; routing and outputs match the oracle on every token."""
+    T, H, I, E, k = 9000, 128, 128, 8, 2
+    x, logits = _inputs(T, H, E, torch.bfloat16, seed=90)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, num_slots=10, seed=91)
+    x_in = x.clone()
+    y, w, ids = fused_moe_forward(x_in, logits, pool, slots, k, True, inplace=inplace,
+                                  return_routing=True)
+    torch.cuda.synchronize()
+    assert (y.data_ptr() == x_in.data_ptr()) == inplace
+    y_ref, w_ref, ids_ref = _oracle_forward(x, logits, pool, slots, k, True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[torch.bfloat16]
+
+
+def test_stack_fused_moe_token_chunks():
+    T, H, I, E, k = 9000, 128, 256, 8, 2
+    x, logits = _inputs(T, H, E, torch.float16, seed=92)
+    pool, slots = make_pool(E, H, I, torch.float16, seed=93)
+    w, ids = select_experts(x, logits, k, False, True)
+    out = stack_fused_moe(x.clone(), pool, slots, logits, w, ids, True, inplace=False)
+    torch.cuda.synchronize()
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.cpu().numpy(), ids.cpu().numpy(), TORCH_TO_ORACLE[torch.float16])
+    assert max_rel_err(f32_of(out), y_ref) <= TOL[torch.float16]

@@ -202,3 +202,13 @@ def test_hip_graph_replays_match_eager(shared):
         assert torch.equal(out, eager), i
         run()  # eager work between replays
         torch.cuda.synchronize()
+
+
+def test_shared_block_token_chunks():
+    """DeepSeek-V2-style block (top-6, shared expert, routed scaling) with 3000 tokens = 18000
+    assignments: two token chunks (2730 + 270) sharing one workspace."""
+    T, H, I, E, k, Is = 3000, 128, 128, 16, 6, 256
+    x, logits, _ = _inputs(T, H, E, torch.bfloat16, seed=94)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=95)
+    page = _shared_page(H, Is, torch.bfloat16, seed=96)
+    _check(x, logits, pool, slots, k, False, page, None, 2.5)
