@@ -14,8 +14,8 @@ from typing import Callable, List, Optional, Tuple
 
 import torch
 
-from .fused_moe_kernel import fused_moe_forward
-from .topk import check_routing_options
+from .fused_moe_kernel import fused_moe_forward, stack_fused_moe
+from .topk import check_routing_options, select_experts
 
 
 def _tp_rank_world() -> Tuple[int, int]:
@@ -98,6 +98,13 @@ class UnquantizedFusedMoEMethod:
         pool = getattr(layer.ws, "gpu_cache", None)
         if pool is None:
             raise RuntimeError("no expert pool attached: set ws.gpu_cache before forward")
+        if custom_routing_function is not None:
+            # the caller's routing, then the experts on the pool (reference :174-196)
+            topk_weights, topk_ids = select_experts(
+                x, router_logits, top_k, use_grouped_topk, renormalize,
+                custom_routing_function=custom_routing_function)
+            return stack_fused_moe(x, pool, expert_cache_indices, router_logits, topk_weights,
+                                   topk_ids, renormalize, inplace=True)
         return fused_moe_forward(x, router_logits, pool, expert_cache_indices, top_k,
                                  renormalize, inplace=True)
 

@@ -4,7 +4,10 @@ Reference call site: specmoe/layers/FusedMoE.py:174-185, which calls
 ``sglang.srt.layers.moe.topk.select_experts`` (sglang==0.4.5.post3, not vendored): an fp32
 softmax over the experts (sgl_kernel.topk_softmax), top-k selection in descending order
 with ties resolved to the lower expert index, then an optional renormalisation
-``w / w.sum(-1)``. Returns ``(topk_weights fp32 [T,k], topk_ids int32 [T,k])``.
+``w / w.sum(-1)``. Returns ``(topk_weights fp32 [T,k], topk_ids int32 [T,k])``. A
+``custom_routing_function`` replaces that selection: it is called as
+``custom_routing_function(hidden_states=..., gating_output=..., topk=..., renormalize=...)``
+and its ``(weights, ids)`` are returned as fp32 / int32.
 """
 from __future__ import annotations
 
@@ -23,12 +26,13 @@ def check_routing_options(use_grouped_topk: bool, topk_group: Optional[int],
                           routed_scaling_factor: Optional[float]) -> None:
     """Reject the select_experts options this build does not implement.
 
-    Grouped top-k with a single group is plain top-k and is accepted.
+    Grouped top-k with a single group is plain top-k and is accepted; a custom routing
+    function is called as the reference calls it.
     """
     if use_grouped_topk and not (num_expert_group in (None, 1) and topk_group in (None, 1)):
         raise NotImplementedError("grouped top-k with more than one expert group")
-    if custom_routing_function is not None:
-        raise NotImplementedError("custom_routing_function")
+    if custom_routing_function is not None and use_grouped_topk:
+        raise NotImplementedError("custom_routing_function together with grouped top-k")
     if correction_bias is not None:
         raise NotImplementedError("correction_bias (biased grouped top-k)")
     if routed_scaling_factor not in (None, 1.0):
@@ -50,6 +54,10 @@ def select_experts(
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     check_routing_options(use_grouped_topk, topk_group, num_expert_group,
                           custom_routing_function, correction_bias, routed_scaling_factor)
+    if custom_routing_function is not None:
+        w, ids = custom_routing_function(hidden_states=hidden_states, gating_output=router_logits,
+                                         topk=top_k, renormalize=renormalize)
+        return w.to(torch.float32), ids.to(torch.int32)
     if torch_native:
         raise NotImplementedError("torch_native routing (this build routes on the GPU only)")
     assert hidden_states.shape[0] == router_logits.shape[0], "Number of tokens mismatch"

@@ -284,3 +284,27 @@ def test_stack_fused_moe_token_chunks():
     y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
                                 w.cpu().numpy(), ids.cpu().numpy(), TORCH_TO_ORACLE[torch.float16])
     assert max_rel_err(f32_of(out), y_ref) <= TOL[torch.float16]
+
+
+def test_fused_moe_custom_routing_function():
+    """FusedMoE with a caller-supplied routing function: its weights and ids drive the experts
+    (reference FusedMoE.py:174-196), checked against the oracle's expert math on them."""
+    T, H, I, E, k = 40, 256, 256, 8, 2
+    dtype = torch.bfloat16
+
+    def route(hidden_states, gating_output, topk, renormalize):
+        # the k lowest-logit experts, weights 1/k (any rule the caller likes)
+        ids = torch.argsort(gating_output.float(), dim=-1)[:, :topk]
+        return torch.full(ids.shape, 1.0 / topk, device=ids.device), ids
+
+    moe = FusedMoE(num_experts=E, top_k=k, hidden_size=H, intermediate_size=I,
+                   params_dtype=dtype, tp_size=1, custom_routing_function=route)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=2 * E, seed=51)
+    set_weight_attrs(moe.ws, {"gpu_cache": pool})
+    x, logits = _inputs(T, H, E, dtype, seed=52)
+    out = moe(x.clone(), logits, slots)
+    torch.cuda.synchronize()
+    w, ids = route(x, logits, k, True)
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.float().cpu().numpy(), ids.int().cpu().numpy(), TORCH_TO_ORACLE[dtype])
+    assert max_rel_err(f32_of(out), y_ref) <= TOL[dtype]

@@ -56,8 +56,9 @@ def test_unsupported_options_raise():
     with pytest.raises(NotImplementedError):
         check_routing_options(True, 2, 4, None, None, None)
     check_routing_options(True, 1, 1, None, None, None)  # one group == plain top-k
+    check_routing_options(False, None, None, lambda **kw: kw, None, None)  # custom routing
     with pytest.raises(NotImplementedError):
-        check_routing_options(False, None, None, lambda *a: a, None, None)
+        check_routing_options(True, 1, 1, lambda **kw: kw, None, None)
     with pytest.raises(NotImplementedError):
         check_routing_options(False, None, None, None, torch.zeros(4), None)
     with pytest.raises(NotImplementedError):
@@ -81,3 +82,21 @@ def test_mixtral_block_structure():
     blk = MixtralMoE(8, 2, 64, 128, params_dtype=torch.float32, tp_size=1)
     assert blk.gate.weight.shape == (8, 64) and blk.gate.bias is None
     assert blk.experts.renormalize is True and blk.experts.top_k == 2
+
+
+def test_custom_routing_function_is_called_like_the_reference():
+    """select_experts hands a custom routing function the reference's keyword arguments and
+    returns its result as fp32 weights / int32 ids (no kernel involved)."""
+    from ae_amd.layers import select_experts
+    seen = {}
+
+    def route(hidden_states, gating_output, topk, renormalize):
+        seen.update(topk=topk, renormalize=renormalize, shape=tuple(gating_output.shape))
+        ids = torch.argsort(gating_output, dim=-1, descending=True)[:, :topk]
+        return torch.full(ids.shape, 0.5, dtype=torch.float64), ids.to(torch.int64)
+
+    x, logits = torch.randn(5, 8), torch.randn(5, 4)
+    w, ids = select_experts(x, logits, 2, renormalize=False, custom_routing_function=route)
+    assert seen == {"topk": 2, "renormalize": False, "shape": (5, 4)}
+    assert w.dtype == torch.float32 and ids.dtype == torch.int32
+    assert torch.equal(ids, torch.argsort(logits, dim=-1, descending=True)[:, :2].to(torch.int32))
