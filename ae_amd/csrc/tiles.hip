@@ -439,6 +439,15 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_down_kernel(ExpertArgs
 
 template <int DT>
 static hipError_t tile_launch(int stage, const ExpertArgs& a, int max_ranges, hipStream_t s) {
+  // The 16-bit walk consumes K steps in pairs: the plan gives every walk an even step count
+  // (H and I are whole 256-byte chunks, split counts divide half the steps); refuse otherwise.
+  if (DT != kF32) {
+    const int64_t eb = dtype_bytes(DT);
+    const bool odd = stage == 0 ? (a.H * eb / kTStep) % 2 != 0
+                                : (a.split_steps * kStepBytes / kTStep) % 2 != 0 ||
+                                      (a.sh.I > 0 && (a.sh.split_steps * kStepBytes / kTStep) % 2 != 0);
+    if (odd) return hipErrorInvalidValue;
+  }
   if (stage == 0) {
     const int64_t groups = (a.I + kTileGateCols - 1) / kTileGateCols;
     const int64_t blocks = a.sh.gateup_blocks + max_ranges * groups;
