@@ -64,6 +64,8 @@ SIGNATURES = [
     ("smx_h2d_pending", ctypes.c_int, [_c_void_p]),
     ("smx_set_tiled_min_tokens", ctypes.c_int, [_i64]),
     ("smx_tiled_min_tokens", _i64, []),
+    ("smx_set_fused_down_max_tokens", ctypes.c_int, [_i64]),
+    ("smx_fused_down_max_tokens", _i64, []),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

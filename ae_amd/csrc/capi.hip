@@ -35,6 +35,19 @@ constexpr int64_t kTileLargeTokens = 512;
 constexpr int64_t kCombineRowsMinTokens = 256;
 constexpr int64_t kTileMinTokensDefault = 64;
 int64_t g_tile_min_tokens = kTileMinTokensDefault;
+// Batches of at most this many tokens run the down projection and the combine as one kernel
+// (down_rows_kernel) instead of the split down kernel plus the combine; negative: the default
+// rule (batches whose output rows each stream at most kRowsDefaultMaxUnits weight units).
+int64_t g_rows_max_tokens = -1;
+
+bool fused_down(int64_t T, int64_t H, int64_t I, int64_t k, int64_t Is, int dtype) {
+  if (T < 1 || T > kRowsMaxTokens || H % 4 != 0) return false;
+  if (g_rows_max_tokens >= 0) return T <= g_rows_max_tokens;
+  const int64_t eb = dtype_bytes(dtype);
+  const int64_t units = T * (k * ((I * eb + kRowsUnitBytes - 1) / kRowsUnitBytes) +
+                             (Is * eb + kRowsUnitBytes - 1) / kRowsUnitBytes);
+  return units <= kRowsDefaultMaxUnits;
+}
 
 // Optional measurement events (smx_set_profile_events): recorded on the launch stream
 // before routing and after each of the four kernels.
@@ -54,6 +67,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 struct Plan {
   bool tiled = false;  // tiled expert kernels (many tokens per expert) instead of streaming
+  bool rows = false;   // down projection fused with the combine (a few tokens)
   int N = 0;
   int max_active = 0;  // experts that can be active: min(E, T*k)
   int span = 0;        // sorted positions per work range: the tokens of one kernel pass
@@ -62,7 +76,7 @@ struct Plan {
   int splits = 1;
   int split_steps = 0;
   size_t hdr = 0, ranges = 0, sorted_f = 0, w = 0, ids = 0;
-  size_t tmask = 0;
+  size_t tmask = 0, fpos = 0, fslot = 0;
   size_t act = 0, part = 0, total = 0;
   // shared expert (Is > 0)
   int Is = 0, s_splits = 1, s_split_steps = 0, s_tok_groups = 0, s_gateup_blocks = 0, s_down_blocks = 0;
@@ -182,6 +196,7 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
       p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H + kTileDownRows - 1) / kTileDownRows) * ss);
     }
   } else {
+    p.rows = fused_down(T, H, I, k, Is, dtype);
     const int64_t tiles = (T + kTokTile - 1) / kTokTile;
     p.tok_tiles = static_cast<int>(tiles < 1 ? 1 : (tiles > kMaxTokTiles ? kMaxTokTiles : tiles));
     p.span = kTokTile * p.tok_tiles;
@@ -215,13 +230,18 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
   p.ranges = o;     o = align_up(o + sizeof(RangeRec) * static_cast<size_t>(p.max_ranges > 0 ? p.max_ranges : 1));
   p.sorted_f = o;   o = align_up(o + sizeof(int32_t) * p.N);
   p.tmask = o;      o = align_up(o + sizeof(int32_t) * T);
+  if (p.rows) {
+    p.fpos = o;     o = align_up(o + sizeof(int32_t) * p.N);
+    p.fslot = o;    o = align_up(o + sizeof(int64_t) * p.N);
+  }
   p.w = o;          o = align_up(o + sizeof(float) * p.N);
   p.ids = o;        o = align_up(o + sizeof(int32_t) * p.N);
   p.act = o;        o = align_up(o + static_cast<size_t>(eb) * p.N * I);
-  p.part = o;       o = align_up(o + sizeof(float) * static_cast<size_t>(s) * p.N * H);
+  // the fused down kernel writes y directly: no fp32 partials
+  p.part = o;       if (!p.rows) o = align_up(o + sizeof(float) * static_cast<size_t>(s) * p.N * H);
   if (Is > 0) {
     p.act_s = o;    o = align_up(o + static_cast<size_t>(eb) * T * Is);
-    p.part_s = o;   o = align_up(o + sizeof(float) * static_cast<size_t>(p.s_splits) * T * H);
+    p.part_s = o;   if (!p.rows) o = align_up(o + sizeof(float) * static_cast<size_t>(p.s_splits) * T * H);
   }
   if (layer) {
     p.logits = o;   o = align_up(o + static_cast<size_t>(eb) * T * E);
@@ -249,6 +269,8 @@ RouteBuffers carve(const Plan& p, void* ws) {
   rb.ranges = reinterpret_cast<RangeRec*>(b + p.ranges);
   rb.sorted_f = reinterpret_cast<int32_t*>(b + p.sorted_f);
   rb.tmask = reinterpret_cast<int32_t*>(b + p.tmask);
+  rb.fpos = p.rows ? reinterpret_cast<int32_t*>(b + p.fpos) : nullptr;
+  rb.fslot = p.rows ? reinterpret_cast<int64_t*>(b + p.fslot) : nullptr;
   rb.span = p.span;
   return rb;
 }
@@ -297,6 +319,33 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
                            : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(2, s);
+  if (p.rows) {
+    RowsArgs r{};
+    r.pool = pool;
+    r.page_bytes = page_elems * dtype_bytes(dtype);
+    r.act = a.act;
+    r.tmask = a.rb.tmask;
+    r.fpos = a.rb.fpos;
+    r.fslot = a.rb.fslot;
+    r.w = w;
+    r.page_s = p.Is > 0 ? bt.shared_page : nullptr;
+    r.act_s = p.Is > 0 ? a.sh.act : nullptr;
+    r.Is = p.Is;
+    r.y = out;
+    r.T = static_cast<int>(T);
+    r.H = static_cast<int>(H);
+    r.I = static_cast<int>(I);
+    r.k = static_cast<int>(k);
+    r.block = bt.block ? 1 : 0;
+    r.scale = bt.scale;
+    r.sgate = bt.sgate;
+    r.sgate_dtype = bt.sgate_dtype;
+    err = launch_down_rows(dtype, r, s);
+    if (err != hipSuccess) return static_cast<int>(err);
+    mark(3, s);
+    mark(4, s);  // no combine launch
+    return SMX_OK;
+  }
   err = p.tiled ? launch_tile_down(dtype, a, p.max_ranges, s)
                 : launch_down(dtype, a, p.max_ranges, p.tok_tiles, s);
   if (err != hipSuccess) return static_cast<int>(err);
@@ -655,6 +704,13 @@ int smx_set_tiled_min_tokens(int64_t tokens_per_expert) {
 }
 
 int64_t smx_tiled_min_tokens(void) { return g_tile_min_tokens; }
+
+int smx_set_fused_down_max_tokens(int64_t tokens) {
+  g_rows_max_tokens = tokens < 0 ? -1 : std::min<int64_t>(tokens, kRowsMaxTokens);
+  return SMX_OK;
+}
+
+int64_t smx_fused_down_max_tokens(void) { return g_rows_max_tokens; }
 
 int smx_set_profile_events(void* const* events, int count) {
   if (events == nullptr || count == 0) {

@@ -539,6 +539,223 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
   store4<DT>(c.y, idx + 4, y1[0], y1[1], y1[2], y1[3]);
 }
 
+// ---------------------------------------------------------------------------------------
+// Down projection fused with the combine, for batches of a few tokens. One wave per output
+// row h computes every term of y[:, h] -- the dot of W2 row h of each routed assignment's
+// expert with that assignment's activation row (and, in the block form, of the shared
+// expert's W2 row h with the token's shared activation row) -- and lanes 0..T-1 then apply
+// the combine's arithmetic and store y[t, h]. No fp32 partials are written and no combine
+// kernel runs. A wave's terms form one stream of 1 KB units (16 bytes per lane of the weight
+// row and of the activation row), kRowsDepth units in flight across term boundaries; each row
+// of an active expert's W2 is read by one wave.
+// Terms run in sorted-position order (an expert's tokens back to back: a row that several
+// tokens need is read from HBM once and then from L2), then the shared expert's T rows.
+// Arithmetic: term = round(w * dot) per routed assignment, summed in j order; block form as
+// combine_kernel. The dot runs in fp32 over the lane's elements in K order, then a fixed
+// butterfly across lanes.
+// Measured alternatives (DeepSeek-V2-Lite block, 1 token): 2 or 4 waves per row taking
+// interleaved units, 16 units in flight, and a cursor that steps over several units at once
+// were all 4-6 us slower than this form (33 us per layer against 37 us for the split down
+// kernel + combine).
+// ---------------------------------------------------------------------------------------
+constexpr int kRowsWaves = 4;                                   // rows (waves) per workgroup
+constexpr int kRowsDepth = 8;                                   // units in flight per wave
+constexpr int kRowsUnit = kWave * 16;                           // bytes per unit
+constexpr int kRowsMaxAssign = kRowsMaxTokens * kMaxTopK;
+constexpr int kRowsMaxTerms = kRowsMaxAssign + kRowsMaxTokens;
+static_assert(kRowsUnit == kRowsUnitBytes, "unit size of the host-side rule");
+
+struct RowTerm {
+  uint64_t w;   // byte address of row 0 of the term's W2
+  uint64_t a;   // byte address of the term's activation row
+  int rowb;     // bytes per row
+  int units;    // kRowsUnit units per row
+};
+
+// Wave-uniform position in the term stream: term, unit within it, and the term's row.
+struct RowCursor {
+  int tau, u, rowb, units;
+  uint64_t w, a;
+};
+
+__device__ __forceinline__ void row_cursor_at(RowCursor& c, const RowTerm* terms, int tau, int h) {
+  const RowTerm& r = terms[tau];
+  c.tau = tau;
+  c.u = 0;
+  c.rowb = uniform(r.rowb);
+  c.units = uniform(r.units);
+  c.w = static_cast<uint64_t>(uniform64(static_cast<int64_t>(r.w))) +
+        static_cast<uint64_t>(h) * static_cast<uint64_t>(c.rowb);
+  c.a = static_cast<uint64_t>(uniform64(static_cast<int64_t>(r.a)));
+}
+
+// acc + the 16-byte lane slices' element products, in element order.
+template <int DT>
+__device__ __forceinline__ float dot16(const u32x4& wv, const u32x4& xv, float acc) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    if constexpr (DT == kF32) {
+      acc = fmaf(__uint_as_float(wv[e]), __uint_as_float(xv[e]), acc);
+    } else {
+      using S = typename Elem<DT>::S;
+      acc = fmaf(Elem<DT>::to_f32(static_cast<S>(wv[e] & 0xffffu)),
+                 Elem<DT>::to_f32(static_cast<S>(xv[e] & 0xffffu)), acc);
+      acc = fmaf(Elem<DT>::to_f32(static_cast<S>(wv[e] >> 16)),
+                 Elem<DT>::to_f32(static_cast<S>(xv[e] >> 16)), acc);
+    }
+  }
+  return acc;
+}
+
+// 16-byte load from a global-memory byte address (global, not flat, instructions: their
+// completion is tracked by the vector-memory counter alone).
+typedef const __attribute__((address_space(1))) u32x4* GlobalU32x4;
+
+template <int CP>
+__device__ __forceinline__ u32x4 load16(uint64_t addr) {
+  if constexpr (CP == kNonTemporal)
+    return __builtin_nontemporal_load(reinterpret_cast<GlobalU32x4>(addr));
+  else
+    return *reinterpret_cast<GlobalU32x4>(addr);
+}
+
+template <int DT, int CP>
+__global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs a) {
+  using S = typename Elem<DT>::S;
+  __shared__ RowTerm terms[kRowsMaxTerms];
+  __shared__ int fpos_l[kRowsMaxAssign];
+  __shared__ float w_l[kRowsMaxAssign];
+  __shared__ float z_l[kRowsMaxTokens];
+  __shared__ float vals[kRowsWaves][kRowsMaxTerms];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int wave = wave_id();
+  const int h = blockIdx.x * kRowsWaves + wave;
+  const int N = a.T * a.k;
+  const int rowb = a.I * static_cast<int>(sizeof(S));
+  const int units = (rowb + kRowsUnit - 1) / kRowsUnit;
+  const bool shared = a.page_s != nullptr;
+  const bool gated = a.block && shared && a.sgate != nullptr;
+  // Term table: routed assignment f becomes term fpos[f]. The loads are independent of one
+  // another (one latency).
+  int routed = 0;
+  if (tid < N) {
+    const int t = tid / a.k;
+    const int j = tid - t * a.k;
+    const uint32_t m = static_cast<uint32_t>(a.tmask[t]);
+    const int pos = a.fpos[tid];
+    const int64_t slot = a.fslot[tid];
+    w_l[tid] = a.w[tid];
+    routed = (m >> j) & 1u;
+    fpos_l[tid] = routed ? pos : -1;
+    if (routed) {
+      RowTerm r;
+      r.w = reinterpret_cast<uint64_t>(a.pool) + static_cast<uint64_t>(slot * a.page_bytes) +
+            2ull * static_cast<uint64_t>(a.H) * static_cast<uint64_t>(rowb);
+      r.a = reinterpret_cast<uint64_t>(a.act) + static_cast<uint64_t>(pos) * static_cast<uint64_t>(rowb);
+      r.rowb = rowb;
+      r.units = units;
+      terms[pos] = r;
+    }
+  }
+  if (tid < a.T) z_l[tid] = gated ? load_scalar(a.sgate, a.sgate_dtype, tid) : 0.0f;
+  const int nr = __syncthreads_count(routed);
+  const int rowb_s = a.Is * static_cast<int>(sizeof(S));
+  const int units_s = (rowb_s + kRowsUnit - 1) / kRowsUnit;
+  if (shared && tid < a.T) {
+    RowTerm r;
+    r.w = reinterpret_cast<uint64_t>(a.page_s) + 2ull * static_cast<uint64_t>(a.H) * static_cast<uint64_t>(rowb_s);
+    r.a = reinterpret_cast<uint64_t>(a.act_s) + static_cast<uint64_t>(tid) * static_cast<uint64_t>(rowb_s);
+    r.rowb = rowb_s;
+    r.units = units_s;
+    terms[nr + tid] = r;
+  }
+  __syncthreads();
+  const int nterms = nr + (shared ? a.T : 0);
+  const int total = nr * units + (shared ? a.T * units_s : 0);
+  if (total > 0) {
+    RowCursor ic, cc;
+    row_cursor_at(ic, terms, 0, h);
+    cc = ic;
+    u32x4 wr[kRowsDepth], ar[kRowsDepth];
+    float part = 0.0f;
+    // Issue the cursor's unit into ring slot d and advance; past the last unit the cursor
+    // stays on it (reloads in bounds, never consumed).
+    auto issue = [&](int d) {
+      const int o = ic.u * kRowsUnit + lane * 16;
+      const int oc = o < ic.rowb ? o : ic.rowb - 16;
+      wr[d] = load16<CP>(ic.w + static_cast<uint64_t>(oc));
+      ar[d] = load16<0>(ic.a + static_cast<uint64_t>(oc));
+      if (++ic.u == ic.units) {
+        if (ic.tau + 1 < nterms) row_cursor_at(ic, terms, ic.tau + 1, h);
+        else ic.u = ic.units - 1;
+      }
+    };
+#pragma unroll
+    for (int d = 0; d < kRowsDepth; ++d) issue(d);
+    for (int i = 0; i < total; i += kRowsDepth) {
+#pragma unroll
+      for (int d = 0; d < kRowsDepth; ++d) {
+        if (i + d < total) {
+          const int o = cc.u * kRowsUnit + lane * 16;
+          if (o < cc.rowb) part = dot16<DT>(wr[d], ar[d], part);
+          if (++cc.u == cc.units) {  // the term's last unit: its dot goes to LDS
+            const float v = wave_sum_butterfly(part);
+            if (lane == 0) vals[wave][cc.tau] = v;
+            part = 0.0f;
+            if (cc.tau + 1 < nterms) row_cursor_at(cc, terms, cc.tau + 1, h);
+          }
+        }
+        issue(d);
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  if (lane >= a.T) return;
+  // lane t: y[t, h] in the combine's arithmetic
+  const int t = lane;
+  float y = 0.0f;
+  for (int j = 0; j < a.k; ++j) {
+    const int f = t * a.k + j;
+    const int p = fpos_l[f];
+    if (p >= 0) y += Elem<DT>::round(vals[wave][p] * w_l[f]);
+  }
+  if (a.block) {
+    y = Elem<DT>::round(y);
+    if (a.scale != 1.0f) y = Elem<DT>::round(y * a.scale);
+    if (shared) {
+      float sh = Elem<DT>::round(vals[wave][nr + t]);
+      if (gated) sh = Elem<DT>::round(Elem<DT>::round(1.0f / (1.0f + __expf(-z_l[t]))) * sh);
+      y += sh;
+    }
+  }
+  static_cast<S*>(a.y)[static_cast<int64_t>(t) * a.H + h] = Elem<DT>::from_f32(y);
+}
+
+hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s) {
+  if (a.T < 1 || a.T > kRowsMaxTokens || a.k > kMaxTopK || a.H % kRowsWaves != 0)
+    return hipErrorInvalidValue;
+  const unsigned blocks = static_cast<unsigned>(a.H / kRowsWaves);
+  // a token's expert rows are read once at T = 1 (streaming hint); larger batches may read a
+  // row twice in a row (two tokens of one expert) and keep it in L2
+  const bool once = a.T == 1;
+  switch (dtype) {
+    case kF32:
+      if (once) down_rows_kernel<kF32, kNonTemporal><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
+      else down_rows_kernel<kF32, 0><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
+      break;
+    case kF16:
+      if (once) down_rows_kernel<kF16, kNonTemporal><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
+      else down_rows_kernel<kF16, 0><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
+      break;
+    default:
+      if (once) down_rows_kernel<kBF16, kNonTemporal><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
+      else down_rows_kernel<kBF16, 0><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
+      break;
+  }
+  return hipGetLastError();
+}
+
 template <bool kMulti, int DT, int MT>
 static void launch_stage_m(int stage, const ExpertArgs& a, int max_ranges, hipStream_t s) {
   if (stage == 0) {

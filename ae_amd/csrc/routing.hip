@@ -325,6 +325,8 @@ struct AlignOutputs {
   int span;             // sorted positions per range
   int32_t* sorted_f;    // [N]
   int32_t* tmask;       // [T] per token: bit j set if assignment t*k+j is routable
+  int32_t* fpos;        // [N] sorted position of each routable assignment
+  int64_t* fslot;       // [N] pool slot of each routable assignment (route only)
   // reference-format outputs (may be null)
   int32_t* sorted_ids;  // [N + E*(BM-1)]
   int32_t* expert_ids;  // [ceil((N + E*(BM-1)) / BM)]
@@ -455,6 +457,10 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
     const int base = sh.cntw[wave][e];
     const int pos = base + rank;
     if (out.sorted_f) out.sorted_f[pos] = f;
+    if (out.fpos) {
+      out.fpos[f] = pos;
+      out.fslot[f] = kCheckSlots ? sh.slot[e] : -1;
+    }
     if (out.sorted_ids) out.sorted_ids[sh.seg[e] + (pos - sh.off[e])] = f;
     if (rank == 0) sh.cntw[wave][e] = base + count;
   });
@@ -623,6 +629,10 @@ __global__ __launch_bounds__(kWave) void route_small_kernel(
   const uint64_t first = ballot(ok && rank == 0);
   if (ok) {
     if (out.sorted_f) out.sorted_f[nless + rank] = lane;
+    if (out.fpos) {
+      out.fpos[lane] = nless + rank;
+      out.fslot[lane] = sl;
+    }
     if (rank == 0 && out.ranges) {  // the host runs this kernel only when T <= span
       const int ai = __popcll(less & first);
       RangeRec rec{};
@@ -895,6 +905,8 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
   out.span = rb.span;
   out.sorted_f = rb.sorted_f;
   out.tmask = rb.tmask;
+  out.fpos = rb.fpos;
+  out.fslot = rb.fpos ? rb.fslot : nullptr;
   out.bm = 1;
   const bool small = static_cast<int64_t>(T) * k <= kWave && E <= kWave && T <= rb.span;
   // the ids-given form needs no top-k: one instantiation serves every E

@@ -54,6 +54,8 @@ struct RouteBuffers {
   RangeRec* ranges;     // [max_ranges] in expert order, then range order
   int32_t* sorted_f;    // [T*k] flat assignment index f = t*k + j at each sorted position
   int32_t* tmask;       // [T] bit j set: assignment t*k+j contributes (routable expert and slot)
+  int32_t* fpos;        // [T*k] sorted position of each contributing assignment (may be null)
+  int64_t* fslot;       // [T*k] pool slot of each contributing assignment (with fpos)
   int span;             // sorted positions per range (the tokens of one kernel pass)
 };
 
@@ -102,6 +104,38 @@ struct CombineArgs {
   int sgate_dtype;
   int rows;                  // thread-per-outputs kernel (large batches) instead of per-token
 };
+
+// Down projection fused with the combine for batches of a few tokens (experts.hip,
+// down_rows_kernel): one wave per output row, every term of y[:, row] in one launch.
+constexpr int kRowsMaxTokens = 8;                       // largest batch the kernel takes
+constexpr int kRowsUnitBytes = 1024;                    // one 16-byte load per lane of a wave
+// By default the fused kernel runs when each wave's terms stream at most this many units
+// (weight bytes per output row, in 1 KB units): DeepSeek-V2-Lite and Qwen1.5-MoE blocks at
+// one token (23 units) run 4-5 us faster per layer than the split down kernel + combine;
+// Mixtral at one token (56 units) and DeepSeek-V2-Lite at two (46) run as fast or slower.
+constexpr int kRowsDefaultMaxUnits = 32;
+
+struct RowsArgs {
+  const void* pool;          // [num_slots, page] expert pages
+  int64_t page_bytes;
+  const void* act;           // [T*k, I] silu(gate)*up, row = sorted position
+  const int32_t* tmask;      // [T] contributing assignments (RouteBuffers::tmask)
+  const int32_t* fpos;       // [T*k] sorted position of each contributing assignment
+  const int64_t* fslot;      // [T*k] pool slot of each contributing assignment
+  const float* w;            // [T*k] routing weights
+  const void* page_s;        // shared-expert page (null: none)
+  const void* act_s;         // [T, Is]
+  int Is;
+  void* y;                   // [T, H]
+  int T, H, I, k;
+  // block form, as CombineArgs
+  int block;
+  float scale;
+  const void* sgate;
+  int sgate_dtype;
+};
+
+hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s);
 
 // Post-attention residual add + RMSNorm + router gate (+ shared-expert gate row, + top-k).
 constexpr int kNormThreads = 256;

@@ -1,6 +1,7 @@
 """Drop-in MoE layer operators (the reference's specmoe/layers MoE surface)."""
 from .FusedMoE import FusedMoE, UnquantizedFusedMoEMethod, set_weight_attrs
-from .fused_moe_kernel import (fused_moe_forward, fused_moe_shared_forward, moe_align_block_size,
+from .fused_moe_kernel import (fused_down_max_tokens, fused_moe_forward, fused_moe_shared_forward,
+                               moe_align_block_size, set_fused_down_max_tokens,
                                set_tiled_min_tokens, stack_fused_moe, tiled_min_tokens)
 from .layernorm import RMSNorm, add_rmsnorm_gate
 from .mixtral_moe import MixtralMoE
@@ -13,5 +14,6 @@ __all__ = [
     "fused_moe_shared_forward", "moe_align_block_size", "stack_fused_moe", "MixtralMoE",
     "SharedExpertMoE", "Qwen2MoeSparseMoeBlock", "DeepseekV2MoE", "fused_topk", "select_experts",
     "RMSNorm", "add_rmsnorm_gate", "PostAttentionMoE", "moe_layer_forward",
-    "set_tiled_min_tokens", "tiled_min_tokens",
+    "set_tiled_min_tokens", "tiled_min_tokens", "set_fused_down_max_tokens",
+    "fused_down_max_tokens",
 ]

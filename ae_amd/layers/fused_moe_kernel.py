@@ -65,6 +65,26 @@ def tiled_min_tokens(tokens_per_expert: Optional[int]) -> Iterator[None]:
         set_tiled_min_tokens(prev)
 
 
+def set_fused_down_max_tokens(tokens: Optional[int]) -> int:
+    """Set the largest batch (tokens) whose down projection and top-k combine run as one
+    kernel (0: never; at most 8; None: the library's default rule, which fuses batches whose
+    output rows each stream at most 32 KB of weight rows). Returns the previous setting (None
+    for the default rule). Process-wide."""
+    prev = int(_lib.lib().smx_fused_down_max_tokens())
+    _lib.call("smx_set_fused_down_max_tokens", -1 if tokens is None else int(tokens))
+    return None if prev < 0 else prev
+
+
+@contextlib.contextmanager
+def fused_down_max_tokens(tokens: Optional[int]) -> Iterator[None]:
+    """Scope a set_fused_down_max_tokens setting (restored on exit)."""
+    prev = set_fused_down_max_tokens(tokens)
+    try:
+        yield
+    finally:
+        set_fused_down_max_tokens(prev)
+
+
 def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:
     H = hidden_states.shape[1]
     _, page_size = w1.shape

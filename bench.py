@@ -83,6 +83,9 @@ def parse():
                     help="expected tokens per active expert at which the tiled MFMA expert "
                          "kernels replace the streaming ones (0 = always, a huge value = never; "
                          "default: the library's)")
+    ap.add_argument("--fused-down-max-tokens", type=int, default=None,
+                    help="largest batch whose down projection and combine run as one kernel "
+                         "(0 = never; default: the library's)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy 10 times (HBM counter calibration)")
     return ap.parse_args()
@@ -230,6 +233,10 @@ def run_tokens(args, wl, T, layers, L, dev):
     n_assign = T * k
     exp_active = min(max(E * (1.0 - (1.0 - k / E) ** T), 1.0), min(E, n_assign))
     tiled = n_assign > 0 and n_assign / exp_active >= L.smx_tiled_min_tokens()
+    # and of the fused down projection + combine (a few tokens, short weight rows per output)
+    fd = L.smx_fused_down_max_tokens()
+    units = T * (k * -(-I * es // 1024) + -(-Is * es // 1024))
+    fused_down = not tiled and 1 <= T <= 8 and (T <= fd if fd >= 0 else units <= 32)
 
     for i in range(args.warmup):
         step(i)
@@ -314,6 +321,7 @@ def run_tokens(args, wl, T, layers, L, dev):
         "routing": routing, "active_experts": len(active), "tokens_per_expert": counts,
         "pool_copies_rotated": copies,
         "expert_kernels": "tiled" if tiled else "streaming",
+        "down_combine": "fused" if fused_down else "split",
     }
     if Is:
         config.update({"shared_ffn": Is, "shared_gate": wl["gated"]})
@@ -418,6 +426,9 @@ def main():
     L = _lib.lib()
     if args.tiled_min_tokens is not None:
         _lib.check("smx_set_tiled_min_tokens", L.smx_set_tiled_min_tokens(args.tiled_min_tokens))
+    if args.fused_down_max_tokens is not None:
+        _lib.check("smx_set_fused_down_max_tokens",
+                   L.smx_set_fused_down_max_tokens(args.fused_down_max_tokens))
     g = torch.Generator(device=dev).manual_seed(0)
     copies = args.rotate if args.layers == 1 else 1  # a stack of layers is its own rotation
     layers = [Layer(g, dev, args.hidden, args.ffn, args.experts, wl["shared_ffn"], copies,

@@ -258,6 +258,25 @@ int smx_set_tiled_min_tokens(int64_t tokens_per_expert);
 int64_t smx_tiled_min_tokens(void);
 
 /*
+ * Down projection fused with the top-k combine, for batches of a few tokens on the
+ * weight-streaming path: one wave per hidden row streams that row of every active expert's W2
+ * (and of the shared expert's) and writes the layer output directly, instead of the K-split
+ * down kernel writing fp32 partials and a combine kernel summing them. Same rounding points
+ * (each routed term rounded after its weight is applied, the fp32 sum over j in order, the
+ * block form); only the fp32 summation order over K differs.
+ * `tokens` = 0: never; 1..8: every batch of at most that many tokens (larger values are taken
+ * as 8); negative (the default): batches of at most 8 tokens whose output rows each stream at
+ * most 32 KB of weight rows, T * (top_k * ceil(I*eb / 1 KB) + ceil(Is*eb / 1 KB)) <= 32 (the
+ * DeepSeek-V2-Lite and Qwen1.5-MoE blocks at one token). The workspace size depends on the
+ * choice, so query it after setting. Process-wide, like smx_set_tiled_min_tokens.
+ * Replaces the third and fourth steps of stack_fused_moe
+ * (specmoe/layers/fused_moe_kernel.py:339-347: the W2 GEMM with MUL_ROUTED_WEIGHT, then
+ * torch.sum over top_k into hidden_states) for such batches.
+ */
+int smx_set_fused_down_max_tokens(int64_t tokens);
+int64_t smx_fused_down_max_tokens(void);
+
+/*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
  * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
  * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and

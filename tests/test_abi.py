@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 25, names
+    assert len(names) == 27, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -133,6 +133,33 @@ def test_tiled_threshold_setting():
     finally:
         assert L.smx_set_tiled_min_tokens(-1) == _lib.SMX_OK
     assert L.smx_tiled_min_tokens() == default
+
+
+def test_fused_down_setting():
+    """The fused down + combine setting is process-wide: negative = the default rule (at most
+    32 KB of weight rows per output row), 0 = never, n = batches up to n tokens (capped at 8).
+    Its plan needs no fp32 partials, so the workspace shrinks for batches it takes."""
+    assert L.smx_fused_down_max_tokens() == -1
+    ws = L.smx_moe_workspace_size
+    sws = L.smx_moe_shared_workspace_size
+    try:
+        # default rule: DeepSeek-V2-Lite block at one token (23 units) fused, Mixtral (56) not
+        ds_default = sws(1, 2048, 1408, 64, 6, 2816, 2)
+        mx_default = ws(1, 4096, 14336, 8, 2, 2)
+        assert L.smx_set_fused_down_max_tokens(0) == _lib.SMX_OK
+        assert L.smx_fused_down_max_tokens() == 0
+        assert sws(1, 2048, 1408, 64, 6, 2816, 2) > ds_default
+        assert ws(1, 4096, 14336, 8, 2, 2) == mx_default
+        split4 = ws(4, 4096, 14336, 8, 2, 2)
+        assert L.smx_set_fused_down_max_tokens(100) == _lib.SMX_OK
+        assert L.smx_fused_down_max_tokens() == 8
+        assert 0 < ws(4, 4096, 14336, 8, 2, 2) < split4
+        assert ws(1, 4096, 14336, 8, 2, 2) < mx_default
+        # beyond 8 tokens the plan is the split one
+        assert ws(9, 4096, 14336, 8, 2, 2) > ws(8, 4096, 14336, 8, 2, 2)
+    finally:
+        assert L.smx_set_fused_down_max_tokens(-1) == _lib.SMX_OK
+    assert L.smx_fused_down_max_tokens() == -1
 
 
 def test_python_error_mapping():
