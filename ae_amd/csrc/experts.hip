@@ -553,13 +553,13 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
 // Arithmetic: term = round(w * dot) per routed assignment, summed in j order; block form as
 // combine_kernel. The dot runs in fp32 over the lane's elements in K order, then a fixed
 // butterfly across lanes.
-// Measured alternatives (DeepSeek-V2-Lite block, 1 token): 2 or 4 waves per row taking
-// interleaved units, 16 units in flight, and a cursor that steps over several units at once
-// were all 4-6 us slower than this form (33 us per layer against 37 us for the split down
-// kernel + combine).
+// Units in flight per wave, measured on the DeepSeek-V2-Lite block at one token (us per
+// layer): 2: 34.5, 3: 32.9, 4: 32.4, 6: 33.0, 8: 33.3, 12: 34.3, 16: 36.4, 24: 37.3 (the split
+// down kernel + combine: 37.1). 2 or 4 waves per row taking interleaved units, and a cursor
+// stepping over several units at once, were 4-6 us slower.
 // ---------------------------------------------------------------------------------------
 constexpr int kRowsWaves = 4;                                   // rows (waves) per workgroup
-constexpr int kRowsDepth = 8;                                   // units in flight per wave
+constexpr int kRowsDepth = 4;                                   // units in flight per wave
 constexpr int kRowsUnit = kWave * 16;                           // bytes per unit
 constexpr int kRowsMaxAssign = kRowsMaxTokens * kMaxTopK;
 constexpr int kRowsMaxTerms = kRowsMaxAssign + kRowsMaxTokens;

@@ -111,9 +111,10 @@ constexpr int kRowsMaxTokens = 8;                       // largest batch the ker
 constexpr int kRowsUnitBytes = 1024;                    // one 16-byte load per lane of a wave
 // By default the fused kernel runs when each wave's terms stream at most this many units
 // (weight bytes per output row, in 1 KB units): DeepSeek-V2-Lite and Qwen1.5-MoE blocks at
-// one token (23 units) run 4-5 us faster per layer than the split down kernel + combine;
-// Mixtral at one token (56 units) and DeepSeek-V2-Lite at two (46) run as fast or slower.
-constexpr int kRowsDefaultMaxUnits = 32;
+// one token (23 units) run ~5 us faster per layer than the split down kernel + combine and
+// DeepSeek-V2-Lite at two tokens (46) 1.5 us faster; Mixtral at one token (56 units, 114 vs
+// 113 us) and DeepSeek-V2-Lite at four (92 units, 82 vs 76 us) run slower.
+constexpr int kRowsDefaultMaxUnits = 48;
 
 struct RowsArgs {
   const void* pool;          // [num_slots, page] expert pages

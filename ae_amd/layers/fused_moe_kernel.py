@@ -68,7 +68,7 @@ def tiled_min_tokens(tokens_per_expert: Optional[int]) -> Iterator[None]:
 def set_fused_down_max_tokens(tokens: Optional[int]) -> int:
     """Set the largest batch (tokens) whose down projection and top-k combine run as one
     kernel (0: never; at most 8; None: the library's default rule, which fuses batches whose
-    output rows each stream at most 32 KB of weight rows). Returns the previous setting (None
+    output rows each stream at most 48 KB of weight rows). Returns the previous setting (None
     for the default rule). Process-wide."""
     prev = int(_lib.lib().smx_fused_down_max_tokens())
     _lib.call("smx_set_fused_down_max_tokens", -1 if tokens is None else int(tokens))

@@ -236,7 +236,7 @@ def run_tokens(args, wl, T, layers, L, dev):
     # and of the fused down projection + combine (a few tokens, short weight rows per output)
     fd = L.smx_fused_down_max_tokens()
     units = T * (k * -(-I * es // 1024) + -(-Is * es // 1024))
-    fused_down = not tiled and 1 <= T <= 8 and (T <= fd if fd >= 0 else units <= 32)
+    fused_down = not tiled and 1 <= T <= 8 and (T <= fd if fd >= 0 else units <= 48)
 
     for i in range(args.warmup):
         step(i)

@@ -266,8 +266,8 @@ int64_t smx_tiled_min_tokens(void);
  * block form); only the fp32 summation order over K differs.
  * `tokens` = 0: never; 1..8: every batch of at most that many tokens (larger values are taken
  * as 8); negative (the default): batches of at most 8 tokens whose output rows each stream at
- * most 32 KB of weight rows, T * (top_k * ceil(I*eb / 1 KB) + ceil(Is*eb / 1 KB)) <= 32 (the
- * DeepSeek-V2-Lite and Qwen1.5-MoE blocks at one token). The workspace size depends on the
+ * most 48 KB of weight rows, T * (top_k * ceil(I*eb / 1 KB) + ceil(Is*eb / 1 KB)) <= 48 (the
+ * DeepSeek-V2-Lite and Qwen1.5-MoE blocks at one and two tokens). The workspace size depends on the
  * choice, so query it after setting. Process-wide, like smx_set_tiled_min_tokens.
  * Replaces the third and fourth steps of stack_fused_moe
  * (specmoe/layers/fused_moe_kernel.py:339-347: the W2 GEMM with MUL_ROUTED_WEIGHT, then

@@ -137,7 +137,7 @@ def test_tiled_threshold_setting():
 
 def test_fused_down_setting():
     """The fused down + combine setting is process-wide: negative = the default rule (at most
-    32 KB of weight rows per output row), 0 = never, n = batches up to n tokens (capped at 8).
+    48 KB of weight rows per output row), 0 = never, n = batches up to n tokens (capped at 8).
     Its plan needs no fp32 partials, so the workspace shrinks for batches it takes."""
     assert L.smx_fused_down_max_tokens() == -1
     ws = L.smx_moe_workspace_size
