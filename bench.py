@@ -86,6 +86,9 @@ def parse():
     ap.add_argument("--fused-down-max-tokens", type=int, default=None,
                     help="largest batch whose down projection and combine run as one kernel "
                          "(0 = never; default: the library's)")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="only time torch.matmul (the ROCm library GEMM) on one expert's dense "
+                         "gate/up and down shapes, the practical reference for the tiled kernels")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy 10 times (HBM counter calibration)")
     return ap.parse_args()
@@ -106,6 +109,32 @@ def copy_calibration():
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n,
                       "launches": 10}), flush=True)
+
+
+def library_gemm():
+    """torch.matmul in bf16 (hipBLASLt on ROCm) on one Mixtral expert's dense shapes: gate/up
+    [M, 4096] x [4096, 2 * 14336] and down [M, 14336] x [14336, 4096], weights row-major
+    [N, K] as nn.Linear stores them, for M tokens per expert."""
+    dev = "cuda"
+    out = {}
+    for M, K, N in [(512, 4096, 28672), (1024, 4096, 28672), (2048, 4096, 28672),
+                    (1024, 14336, 4096)]:
+        a = torch.randn((M, K), device=dev, dtype=torch.bfloat16)
+        b = torch.randn((N, K), device=dev, dtype=torch.bfloat16)
+        for _ in range(5):
+            torch.matmul(a, b.t())
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 20
+        e0.record()
+        for _ in range(n):
+            torch.matmul(a, b.t())
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / n
+        out[f"{M}x{K}x{N}"] = {"us": round(us, 1),
+                               "tflops": round(2.0 * M * K * N / (us * 1e-6) / 1e12, 1)}
+    print(json.dumps({"library_gemm_bf16": out, "peak_tflops": MFMA_BF16_PEAK_TFLOPS}), flush=True)
 
 
 def measured_traffic(T, H, I, E, k, workload):
@@ -408,6 +437,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.library_gemm:
+        library_gemm()
         return
     if args.h2d:
         h2d_bench(args)
