@@ -39,6 +39,8 @@ int64_t g_tile_min_tokens = kTileMinTokensDefault;
 // (down_rows_kernel) instead of the split down kernel plus the combine; negative: the default
 // rule (batches whose output rows each stream at most kRowsDefaultMaxUnits weight units).
 int64_t g_rows_max_tokens = -1;
+// fp32 runs round the routed GEMM outputs to fp16 as the reference stores them (opt-in).
+bool g_fp32_f16out = false;
 
 bool fused_down(int64_t T, int64_t H, int64_t I, int64_t k, int64_t Is, int dtype) {
   if (T < 1 || T > kRowsMaxTokens || H % 4 != 0) return false;
@@ -304,6 +306,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   a.part = reinterpret_cast<float*>(b + p.part);
   a.splits = p.splits;
   a.split_steps = p.split_steps;
+  a.f16out = dtype == kF32 && g_fp32_f16out ? 1 : 0;
   if (p.Is > 0) {
     a.sh.page = bt.shared_page;
     a.sh.I = p.Is;
@@ -340,6 +343,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
     r.scale = bt.scale;
     r.sgate = bt.sgate;
     r.sgate_dtype = bt.sgate_dtype;
+    r.f16out = a.f16out;
     err = launch_down_rows(dtype, r, s);
     if (err != hipSuccess) return static_cast<int>(err);
     mark(3, s);
@@ -366,6 +370,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   c.sgate = bt.sgate;
   c.sgate_dtype = bt.sgate_dtype;
   c.rows = T >= kCombineRowsMinTokens ? 1 : 0;
+  c.f16out = a.f16out;
   err = launch_combine(dtype, c, s);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(4, s);
@@ -711,6 +716,13 @@ int smx_set_fused_down_max_tokens(int64_t tokens) {
 }
 
 int64_t smx_fused_down_max_tokens(void) { return g_rows_max_tokens; }
+
+int smx_set_fp32_gemm_outputs_fp16(int on) {
+  g_fp32_f16out = on != 0;
+  return SMX_OK;
+}
+
+int smx_fp32_gemm_outputs_fp16(void) { return g_fp32_f16out ? 1 : 0; }
 
 int smx_set_profile_events(void* const* events, int count) {
   if (events == nullptr || count == 0) {

@@ -45,6 +45,15 @@ __device__ __forceinline__ ChunkOrder rotated_order(int n, int index) {
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
 
+// Rounding of a routed GEMM output (gate/up, and the weighted down output): to the activation
+// dtype; for fp32 runs with f16out set, to fp16 -- the reference's Triton kernel stores fp32
+// runs' GEMM outputs with compute_type fp16 (specmoe/layers/fused_moe_kernel.py:203,248).
+template <int DT>
+__device__ __forceinline__ float round_out(float v, int f16out) {
+  if constexpr (DT == kF32) return f16out ? Elem<kF16>::round(v) : v;
+  else return Elem<DT>::round(v);
+}
+
 // Store 4 consecutive elements (one accumulator register group) of an output row.
 template <int DT>
 __device__ __forceinline__ void store4(void* base, int64_t idx, float v0, float v1, float v2, float v3) {

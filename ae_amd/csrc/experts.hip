@@ -212,6 +212,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
   const ChunkOrder ord = rotated_order(static_cast<int>(row_bytes / (kStepBytes * kUnroll)), it.rot);
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
+  const int f16out = it.shared ? 0 : a.f16out;
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<2> wa, wb;
     issue_weights<CP>(wa, wb, ws, ord);
@@ -237,8 +238,8 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
         float o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float gate = Elem<DT>::round(acc[0][mt][i]);
-          const float up = Elem<DT>::round(acc[1][mt][i]);
+          const float gate = round_out<DT>(acc[0][mt][i], f16out);
+          const float up = round_out<DT>(acc[1][mt][i], f16out);
           o[i] = silu_f32(gate) * up;
         }
         store4<DT>(act, static_cast<int64_t>(off + q) * I + kRowTile * p + 4 * g, o[0], o[1], o[2], o[3]);
@@ -434,7 +435,7 @@ __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(Combi
         const float wf = c.w[f];
         const bool routed = (vm >> i) & 1u;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) term[e] = routed ? Elem<DT>::round(v[e] * wf) : 0.0f;
+        for (int e = 0; e < 4; ++e) term[e] = routed ? round_out<DT>(v[e] * wf, c.f16out) : 0.0f;
       }
     } else if (live) {
       term = split_sum(c.part_s + static_cast<int64_t>(t) * c.H + h, static_cast<int64_t>(c.T) * c.H, c.splits_s);
@@ -497,8 +498,8 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
     const float wf = c.w[f];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      y0[e] += Elem<DT>::round(v0[e] * wf);
-      y1[e] += Elem<DT>::round(v1[e] * wf);
+      y0[e] += round_out<DT>(v0[e] * wf, c.f16out);
+      y1[e] += round_out<DT>(v1[e] * wf, c.f16out);
     }
   }
   if (c.block) {
@@ -718,7 +719,7 @@ __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs 
   for (int j = 0; j < a.k; ++j) {
     const int f = t * a.k + j;
     const int p = fpos_l[f];
-    if (p >= 0) y += Elem<DT>::round(vals[wave][p] * w_l[f]);
+    if (p >= 0) y += round_out<DT>(vals[wave][p] * w_l[f], a.f16out);
   }
   if (a.block) {
     y = Elem<DT>::round(y);

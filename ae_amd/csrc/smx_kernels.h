@@ -86,6 +86,7 @@ struct ExpertArgs {
   float* part;          // [splits, T*k, H] fp32 partial down projections, row = f
   int splits;           // K splits of the down projection
   int split_steps;      // load steps per split
+  int f16out;           // fp32 runs: routed gate/up outputs rounded to fp16 (reference stores)
   SharedArgs sh;
 };
 
@@ -103,6 +104,7 @@ struct CombineArgs {
   const void* sgate;         // [T] shared-expert gate logits (s = sigmoid), null: s = 1
   int sgate_dtype;
   int rows;                  // thread-per-outputs kernel (large batches) instead of per-token
+  int f16out;                // fp32 runs: each routed term rounded to fp16 (reference stores)
 };
 
 // Down projection fused with the combine for batches of a few tokens (experts.hip,
@@ -134,6 +136,7 @@ struct RowsArgs {
   float scale;
   const void* sgate;
   int sgate_dtype;
+  int f16out;                // as CombineArgs::f16out
 };
 
 hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s);

@@ -352,6 +352,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_gateup_kernel(ExpertAr
   walk<0, DT>(wk, n, st0, st1, st2, wtiles[wave], acc);
 
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
+  const int f16out = it.shared ? 0 : a.f16out;
   const int g = lane >> 4;
 #pragma unroll
   for (int bt = 0; bt < kTBTiles; ++bt) {
@@ -363,8 +364,8 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_gateup_kernel(ExpertAr
       float o[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float gate = Elem<DT>::round(acc[i][bt][e]);
-        const float up = Elem<DT>::round(acc[i + 2][bt][e]);
+        const float gate = round_out<DT>(acc[i][bt][e], f16out);
+        const float up = round_out<DT>(acc[i + 2][bt][e], f16out);
         o[e] = silu_f32(gate) * up;
       }
       store4<DT>(act, static_cast<int64_t>(it.off + q) * I + ct[i] * kRowTile + 4 * g, o[0], o[1], o[2], o[3]);

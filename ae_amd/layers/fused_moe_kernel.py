@@ -85,6 +85,25 @@ def fused_down_max_tokens(tokens: Optional[int]) -> Iterator[None]:
         set_fused_down_max_tokens(prev)
 
 
+def set_fp32_gemm_outputs_fp16(on: bool) -> bool:
+    """fp32 runs: round the routed GEMM outputs (gate/up and the weighted down projection) to
+    fp16 as the reference stores them for fp32 inputs (specmoe/layers/fused_moe_kernel.py:
+    203,248), instead of keeping true fp32. Returns the previous setting. Process-wide."""
+    prev = bool(_lib.lib().smx_fp32_gemm_outputs_fp16())
+    _lib.call("smx_set_fp32_gemm_outputs_fp16", 1 if on else 0)
+    return prev
+
+
+@contextlib.contextmanager
+def fp32_gemm_outputs_fp16(on: bool = True) -> Iterator[None]:
+    """Scope a set_fp32_gemm_outputs_fp16 setting (restored on exit)."""
+    prev = set_fp32_gemm_outputs_fp16(on)
+    try:
+        yield
+    finally:
+        set_fp32_gemm_outputs_fp16(prev)
+
+
 def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:
     H = hidden_states.shape[1]
     _, page_size = w1.shape

@@ -277,6 +277,18 @@ int smx_set_fused_down_max_tokens(int64_t tokens);
 int64_t smx_fused_down_max_tokens(void);
 
 /*
+ * fp32 runs only: with `on` set, the routed experts' GEMM outputs are rounded to fp16 where
+ * the reference's Triton kernel stores them for fp32 inputs -- the gate and up projections
+ * (C1) and each assignment's weighted down projection (C3); the SiLU*up activation and the
+ * top-k sum stay fp32 (specmoe/layers/fused_moe_kernel.py:203,248: compute_type is fp16 unless
+ * the input is bf16; :319-327 and :337 keep the intermediates in the input dtype). Off by
+ * default (true fp32 throughout). Shared-expert blocks are not affected (the reference has
+ * none). bf16/fp16 runs already round to their own dtype at these points. Process-wide.
+ */
+int smx_set_fp32_gemm_outputs_fp16(int on);
+int smx_fp32_gemm_outputs_fp16(void);
+
+/*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
  * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
  * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and

@@ -15,8 +15,10 @@ A plain numpy restatement of the reference's arithmetic:
             assignment, C1 = round(x W13^T) (:332-335, rounded at :203), C2 =
             round(silu(C1_gate) * C1_up) (:337), C3 = round((C2 W2^T) * w) (:339-342, weight
             applied at :197-201), y = round(sum_j C3) (:344-347). round() is to the activation
-            dtype; fp32 runs round nowhere (the reference's fp16 store of fp32 GEMM outputs,
-            :248, is not reproduced).
+            dtype; fp32 runs round nowhere by default. With fp16_outputs (fp32 only) the two
+            GEMM outputs C1 and C3 are rounded to fp16 as the reference's Triton kernel
+            stores them for fp32 inputs (compute_type fp16, :248; cast at :203), C2 stays fp32
+            (silu_and_mul into the fp32 intermediate, :337) and so does the sum.
   page      FusedMoE.weight_loader, specmoe/layers/FusedMoE.py:485-505: one page per expert,
             [W1 (I x H) | W3 (I x H) | W2 (H x I)].
   norm      RMSNorm.forward_native, specmoe/layers/layernorm.py:36-52 (residual add in fp32,
@@ -239,10 +241,13 @@ def silu(g: np.ndarray) -> np.ndarray:
 
 
 def stack_fused_moe(x: np.ndarray, pool: np.ndarray, slots: np.ndarray, topk_weights: np.ndarray,
-                    topk_ids: np.ndarray, dtype: str, num_experts: int | None = None) -> np.ndarray:
+                    topk_ids: np.ndarray, dtype: str, num_experts: int | None = None,
+                    fp16_outputs: bool = False) -> np.ndarray:
     """y [T,H] float32 (values representable in dtype). x and pool may be float arrays or
     uint16 bit arrays (bf16/f16). Assignments with an id outside [0,E) or a slot outside the
-    pool contribute nothing."""
+    pool contribute nothing. fp16_outputs (dtype f32 only): C1 and C3 rounded to fp16, as the
+    reference stores fp32 runs' GEMM outputs (specmoe/layers/fused_moe_kernel.py:203,248)."""
+    c_dt = F16 if (fp16_outputs and dtype == F32) else dtype
     xf = to_f32(x, dtype)
     T, H = xf.shape
     ids = np.asarray(topk_ids).reshape(T, -1)
@@ -266,22 +271,24 @@ def stack_fused_moe(x: np.ndarray, pool: np.ndarray, slots: np.ndarray, topk_wei
         W1, W3, W2 = unpack_page(pool[slot], H, dtype)
         t, j = f // k, f % k
         xe = xf[t]
-        g = round_to(xe @ W1.T, dtype)
-        u = round_to(xe @ W3.T, dtype)
+        g = round_to(xe @ W1.T, c_dt)
+        u = round_to(xe @ W3.T, c_dt)
         a = round_to(silu(g) * u, dtype)
         d = (a @ W2.T) * w[t, j][:, None]
-        c3[t, j] = round_to(d, dtype)
+        c3[t, j] = round_to(d, c_dt)
     y = c3[:, 0, :].copy()
     for j in range(1, k):
         y = y + c3[:, j, :]
     return round_to(y, dtype)
 
 
-def fused_moe_forward(x, router_logits, pool, slots, top_k: int, renormalize: bool, dtype: str):
+def fused_moe_forward(x, router_logits, pool, slots, top_k: int, renormalize: bool, dtype: str,
+                      fp16_outputs: bool = False):
     """FusedMoE.forward: routing then stack_fused_moe -> (y, topk_weights, topk_ids)."""
     logits = np.asarray(router_logits, dtype=np.float32)
     w, ids = topk_softmax(logits, top_k, renormalize)
-    y = stack_fused_moe(x, pool, slots, w, ids, dtype, num_experts=logits.shape[1])
+    y = stack_fused_moe(x, pool, slots, w, ids, dtype, num_experts=logits.shape[1],
+                        fp16_outputs=fp16_outputs)
     return y, w, ids
 
 

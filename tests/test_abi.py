@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 27, names
+    assert len(names) == 29, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -160,6 +160,18 @@ def test_fused_down_setting():
     finally:
         assert L.smx_set_fused_down_max_tokens(-1) == _lib.SMX_OK
     assert L.smx_fused_down_max_tokens() == -1
+
+
+def test_fp32_gemm_outputs_fp16_setting():
+    assert L.smx_fp32_gemm_outputs_fp16() == 0
+    try:
+        assert L.smx_set_fp32_gemm_outputs_fp16(1) == _lib.SMX_OK
+        assert L.smx_fp32_gemm_outputs_fp16() == 1
+        # it changes rounding only: the plans and workspace sizes stay the same
+        assert L.smx_moe_workspace_size(32, 1024, 2816, 8, 2, 0) > 0
+    finally:
+        assert L.smx_set_fp32_gemm_outputs_fp16(0) == _lib.SMX_OK
+    assert L.smx_fp32_gemm_outputs_fp16() == 0
 
 
 def test_python_error_mapping():

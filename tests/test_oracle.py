@@ -254,6 +254,47 @@ def test_expert_math_against_textbook(dtype, rtol):
     assert err < rtol, err
 
 
+def _textbook_fp16_outputs(x, w1s, w3s, w2s, w, ids, round_act=False):
+    """float64 block with the reference's fp32-input stores: gate/up outputs and the weighted
+    down output cast to fp16 (np.float16, nearest even), activation and sum unrounded."""
+    x = x.astype(np.float64)
+    y = np.zeros_like(x)
+    h16 = lambda v: v.astype(np.float16).astype(np.float64)
+    for t in range(x.shape[0]):
+        for j in range(ids.shape[1]):
+            e = ids[t, j]
+            g = h16(w1s[e].astype(np.float64) @ x[t])
+            u = h16(w3s[e].astype(np.float64) @ x[t])
+            a = g / (1 + np.exp(-g)) * u
+            if round_act:
+                a = h16(a)
+            y[t] += h16(w[t, j] * (w2s[e].astype(np.float64) @ a))
+    return y
+
+
+def test_fp32_fp16_outputs_mode_against_textbook():
+    """The opt-in fp16 stores of fp32 runs: close to the float64 block with fp16 casts at C1
+    and C3 only, clearly farther from true fp32 and from a block that also rounds C2."""
+    rng = np.random.default_rng(15)
+    T, H, I, E, k = 8, 64, 96, 4, 2
+    x, w1s, w3s, w2s, slots, pool, logits = _make_layer(rng, T, H, I, E, k, 6, ref.F32)
+    y, w, ids = ref.fused_moe_forward(x, logits, pool, slots, k, True, ref.F32, fp16_outputs=True)
+    y_plain, _, _ = ref.fused_moe_forward(x, logits, pool, slots, k, True, ref.F32)
+    want = _textbook_fp16_outputs(x, w1s, w3s, w2s, w, ids)
+    also_act = _textbook_fp16_outputs(x, w1s, w3s, w2s, w, ids, round_act=True)
+    scale = np.abs(want).max()
+    err = np.abs(y - want).max() / scale
+    assert err < 2e-5, err
+    assert np.abs(y_plain - want).max() / scale > 10 * err
+    assert np.abs(y - also_act).max() / scale > 5 * err
+    # a no-op for 16-bit activations
+    xb = ref.round_to(x, ref.BF16)
+    pb = ref.round_to(pool, ref.BF16)
+    a1 = ref.stack_fused_moe(xb, pb, slots, w, ids, ref.BF16)
+    a2 = ref.stack_fused_moe(xb, pb, slots, w, ids, ref.BF16, fp16_outputs=True)
+    np.testing.assert_array_equal(a1, a2)
+
+
 def test_expert_math_detects_swapped_gate_up():
     rng = np.random.default_rng(12)
     T, H, I, E, k = 6, 32, 64, 3, 2
