@@ -74,7 +74,9 @@ def parse():
                     help="Mixtral gate bias exponent (0 = unbiased)")
     ap.add_argument("--rotate", type=int, default=2, help="copies of the weights rotated per step")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-calls", type=int, default=2, help="CPU baseline sample: layer calls")
+    ap.add_argument("--cpu-calls", type=int, default=12,
+                    help="CPU baseline sample: layer calls (the default is ~10 s of host work "
+                         "for the Mixtral layer at 32 tokens)")
     ap.add_argument("--h2d", action="store_true",
                     help="measure host -> device streaming of expert pages through the transfer "
                          "engine (pinned host memory, chunked copies), alone and beside the MoE "
