@@ -687,11 +687,22 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
   g.k = static_cast<int>(top_k);
   g.renorm = renormalize;
   g.dtype = dtype;
+  // one token over at most 64 experts: the norm kernel's top-k wave also writes the expert
+  // sort, and no routing kernel is launched
+  const bool sort_in_norm = T == 1 && E <= kWave;
+  if (sort_in_norm) {
+    g.route = 1;
+    g.rb = carve(p, workspace);
+    g.e2s = expert_to_slot;
+    g.num_slots = num_slots;
+  }
   hipError_t err = launch_norm_gate(g, s);
   if (err != hipSuccess) return static_cast<int>(err);
-  err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k), 0,
-                     nullptr, nullptr, ids, expert_to_slot, num_slots, carve(p, workspace), s);
-  if (err != hipSuccess) return static_cast<int>(err);
+  if (!sort_in_norm) {
+    err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k), 0,
+                       nullptr, nullptr, ids, expert_to_slot, num_slots, carve(p, workspace), s);
+    if (err != hipSuccess) return static_cast<int>(err);
+  }
   mark(1, s);
   BlockTerms bt;
   bt.block = shared_I > 0 || routed_scaling_factor != 1.0f;

@@ -794,6 +794,44 @@ __global__ __launch_bounds__(kNormThreads) void norm_gate_kernel(NormGateArgs a)
     a.topk_w[static_cast<int64_t>(t) * a.k + slot[0]] = w[0];
     a.topk_ids[static_cast<int64_t>(t) * a.k + slot[0]] = id[0];
   }
+  if constexpr (PL == 1) {
+    if (a.route) {
+      // One token (the host checks T = 1): its picks are its assignments f = slot, one per
+      // expert, so the expert sort is the picks in expert order (lane j holds expert j) --
+      // the records route_small_kernel writes for the same ids: sorted position = routable
+      // picks of smaller experts, one range per routable pick.
+      const bool pick = lane < G && slot[0] >= 0;
+      const int64_t sl = pick ? a.e2s[id[0]] : -1;
+      const bool ok = pick && sl >= 0 && sl < a.num_slots;
+      const uint64_t okm = ballot(ok);
+      const bool bad = ballot(pick && !ok) != 0;
+      const uint64_t below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+      const int pos = __popcll(okm & below);
+      uint32_t tm = 0;
+      for (int s = 0; s < a.k; ++s)
+        if (ballot(ok && slot[0] == s) != 0) tm |= 1u << s;
+      if (ok) {
+        a.rb.sorted_f[pos] = slot[0];
+        if (a.rb.fpos) {
+          a.rb.fpos[slot[0]] = pos;
+          a.rb.fslot[slot[0]] = sl;
+        }
+        RangeRec rec{};
+        rec.slot = sl;
+        rec.off = pos;
+        rec.cnt = 1;
+        rec.key = pos;
+        rec.j0 = pos;
+        rec.nr = 1;
+        a.rb.ranges[pos] = rec;
+      }
+      if (lane == 0) {
+        a.rb.hdr[0] = __popcll(okm);
+        a.rb.hdr[1] = bad ? 1 : 0;
+        a.rb.tmask[0] = static_cast<int32_t>(tm);
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------------------

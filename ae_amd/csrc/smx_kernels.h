@@ -159,6 +159,12 @@ struct NormGateArgs {
   float* topk_w;          // [T, k] top-k weights out (null: no top-k)
   int32_t* topk_ids;      // [T, k]
   int T, H, E, k, renorm, dtype;
+  // One token and E <= 64: the expert sort of the token's picks written here (the records the
+  // routing kernels write), in place of a routing launch. route = 0: not written.
+  int route;
+  RouteBuffers rb;
+  const int64_t* e2s;     // [E] expert -> pool slot
+  int64_t num_slots;
 };
 
 hipError_t launch_norm_gate(const NormGateArgs& a, hipStream_t s);

@@ -100,13 +100,15 @@ def test_norm_inplace_and_module():
     assert y.shape == x0.shape and y.data_ptr() != x0.data_ptr()
 
 
-def _layer_case(T, H, I, E, k, renorm, Is=0, gated=False, scale=1.0, seed=0):
+def _layer_case(T, H, I, E, k, renorm, Is=0, gated=False, scale=1.0, seed=0, drop=False):
     dt = torch.bfloat16
     x = _rand((T, H), dt, seed=seed + 1)
     r = _rand((T, H), dt, seed=seed + 2)
     nw = _rand((H,), dt, seed=seed + 3, scale=0.1) + 1
     gw = _rand((E, H), dt, seed=seed + 4, scale=0.05)
     pool, slots = make_pool(E, H, I, dt, num_slots=E + 3, seed=seed + 5)
+    if drop:  # every other expert maps outside the pool: its assignments contribute nothing
+        slots[::2] = E + 10
     page = _rand((3 * Is * H,), dt, seed=seed + 6, scale=0.02) if Is else None
     sgw = _rand((H,), dt, seed=seed + 7, scale=0.05) if gated else None
     x0, r0 = x.clone(), r.clone()
@@ -140,6 +142,15 @@ def test_layer_forward_mixtral_like(T):
 @pytest.mark.parametrize("T", [3, 64])
 def test_layer_forward_qwen_like(T):
     _layer_case(T, 256, 128, 60, 4, False, Is=512, gated=True, seed=100 + T)
+
+
+@pytest.mark.parametrize("E,k,Is,drop", [(8, 2, 0, False), (8, 2, 0, True), (64, 6, 256, False),
+                                         (64, 6, 256, True), (60, 4, 512, True), (4, 4, 0, True)])
+def test_layer_forward_one_token(E, k, Is, drop):
+    """One token over at most 64 experts: the norm kernel writes the expert sort itself (no
+    routing launch), with unroutable picks dropped; the fused down + combine follows."""
+    _layer_case(1, 256, 256, E, k, E <= 8, Is=Is, gated=Is == 512, seed=400 + E + k + int(drop),
+                drop=drop)
 
 
 def test_layer_forward_deepseek_like():
