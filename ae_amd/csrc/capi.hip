@@ -31,8 +31,10 @@ constexpr int64_t kTileTargetDownBlocks = 512;
 // 56 us). Below it the extra splits cost more in the combine than they save.
 constexpr int64_t kTileLargeTokens = 512;
 // Batches from this many tokens combine with one thread per 8 outputs (combine_rows_kernel);
-// smaller ones with one workgroup per (token, 256 outputs), one wave per assignment.
-constexpr int64_t kCombineRowsMinTokens = 256;
+// smaller ones with one workgroup per (token, 256 outputs), one wave per assignment. Measured
+// per layer, rows vs per-token: Mixtral 128 tokens 492.4 vs 493.3 us, DeepSeek-V2-Lite 128
+// tokens 213.2 vs 213.6; at 64 tokens rows is 1.5-2 us slower (201.4 vs 199.6).
+constexpr int64_t kCombineRowsMinTokens = 128;
 constexpr int64_t kTileMinTokensDefault = 64;
 int64_t g_tile_min_tokens = kTileMinTokensDefault;
 // Batches of at most this many tokens run the down projection and the combine as one kernel
