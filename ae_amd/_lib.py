@@ -68,6 +68,8 @@ SIGNATURES = [
     ("smx_fused_down_max_tokens", _i64, []),
     ("smx_set_fp32_gemm_outputs_fp16", ctypes.c_int, [_i32]),
     ("smx_fp32_gemm_outputs_fp16", _i32, []),
+    ("smx_set_routing_in_gateup", ctypes.c_int, [_i32]),
+    ("smx_routing_in_gateup", _i32, []),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

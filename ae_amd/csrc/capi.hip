@@ -43,6 +43,8 @@ int64_t g_tile_min_tokens = kTileMinTokensDefault;
 int64_t g_rows_max_tokens = -1;
 // fp32 runs round the routed GEMM outputs to fp16 as the reference stores them (opt-in).
 bool g_fp32_f16out = false;
+// Small batches route inside the gate/up launch (smx_set_routing_in_gateup).
+bool g_route_in_gateup = true;
 
 bool fused_down(int64_t T, int64_t H, int64_t I, int64_t k, int64_t Is, int dtype) {
   if (T < 1 || T > kRowsMaxTokens || H % 4 != 0) return false;
@@ -288,11 +290,28 @@ struct BlockTerms {
   int sgate_dtype = kF32;
 };
 
-// Shared tail of the MoE entry points: expert kernels then combine.
+// Lanes per token of the one-wave top-k: the power of two >= E, at least 8.
+int route_group(int64_t E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64; }
+
+// The routing runs inside the gate/up launch (no routing launch) for batches one wave routes:
+// T*k <= 64 assignments over E <= 64 experts, every expert one token range of at most two
+// token tiles, the top-k (when logits are given, in the activation dtype) in at most 4 passes
+// of 64/G tokens. Returns G, or 0 when the routing kernels run instead.
+int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logits, bool logits_dt_ok) {
+  if (!g_route_in_gateup) return 0;
+  if (p.tiled || T < 1 || T * k > kWave || E > kWave || T > p.span || p.tok_tiles > 2) return 0;
+  const int g = route_group(E);
+  if (logits && (!logits_dt_ok || T * g > kWave * kSmallRoutePasses)) return 0;
+  return g;
+}
+
+// Shared tail of the MoE entry points: expert kernels then combine. route_g > 0: the gate/up
+// launch routes the batch itself (rt).
 int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t T, int64_t H,
                 int64_t I, int64_t E, int64_t k, const void* pool, int64_t num_slots,
                 int64_t page_elems, const int64_t* e2s, const float* w, const int32_t* ids,
-                void* ws, hipStream_t s, const BlockTerms& bt = BlockTerms{}) {
+                void* ws, hipStream_t s, const BlockTerms& bt = BlockTerms{}, int route_g = 0,
+                const InRoute& rt = InRoute{}) {
   char* b = static_cast<char*>(ws);
   ExpertArgs a{};
   a.x = hidden;
@@ -320,8 +339,9 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
     a.sh.gateup_blocks = p.s_gateup_blocks;
     a.sh.down_blocks = p.s_down_blocks;
   }
+  a.rt = rt;
   hipError_t err = p.tiled ? launch_tile_gateup(dtype, a, p.max_ranges, s)
-                           : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s);
+                           : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s, route_g);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(2, s);
   if (p.rows) {
@@ -468,12 +488,20 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
   if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   mark(0, s);
-  hipError_t err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k),
-                                0, nullptr, nullptr, topk_ids, expert_to_slot, num_slots, carve(p, workspace), s);
-  if (err != hipSuccess) return static_cast<int>(err);
+  const int rg = in_launch_route_g(p, T, E, top_k, false, true);
+  InRoute rt{};
+  if (rg > 0) {
+    rt.ids_in = topk_ids;
+    rt.num_slots = num_slots;
+    rt.E = static_cast<int>(E);
+  } else {
+    hipError_t err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k),
+                                  0, nullptr, nullptr, topk_ids, expert_to_slot, num_slots, carve(p, workspace), s);
+    if (err != hipSuccess) return static_cast<int>(err);
+  }
   mark(1, s);
   return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, topk_weights, topk_ids, workspace, s);
+                     expert_to_slot, topk_weights, topk_ids, workspace, s, BlockTerms{}, rg, rt);
 }
 
 }  // extern "C"
@@ -525,13 +553,24 @@ int fused_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H
   int32_t* ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t*>(b + p.ids);
   hipStream_t s = static_cast<hipStream_t>(stream);
   mark(0, s);
-  hipError_t err = launch_route(router_logits, logits_dtype, static_cast<int>(T), static_cast<int>(E),
-                                static_cast<int>(top_k), renormalize, w, ids, nullptr, expert_to_slot,
-                                num_slots, carve(p, workspace), s);
-  if (err != hipSuccess) return static_cast<int>(err);
+  const int rg = in_launch_route_g(p, T, E, top_k, true, logits_dtype == dtype);
+  InRoute rt{};
+  if (rg > 0) {
+    rt.logits = router_logits;
+    rt.w_out = w;
+    rt.ids_out = ids;
+    rt.num_slots = num_slots;
+    rt.E = static_cast<int>(E);
+    rt.renorm = renormalize;
+  } else {
+    hipError_t err = launch_route(router_logits, logits_dtype, static_cast<int>(T), static_cast<int>(E),
+                                  static_cast<int>(top_k), renormalize, w, ids, nullptr, expert_to_slot,
+                                  num_slots, carve(p, workspace), s);
+    if (err != hipSuccess) return static_cast<int>(err);
+  }
   mark(1, s);
   return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, w, ids, workspace, s, bt);
+                     expert_to_slot, w, ids, workspace, s, bt, rg, rt);
 }
 
 }  // namespace
@@ -700,7 +739,14 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
   }
   hipError_t err = launch_norm_gate(g, s);
   if (err != hipSuccess) return static_cast<int>(err);
-  if (!sort_in_norm) {
+  // larger small batches: the sort of the norm kernel's picks inside the gate/up launch
+  const int rg = sort_in_norm ? 0 : in_launch_route_g(p, T, E, top_k, false, true);
+  InRoute rt{};
+  if (rg > 0) {
+    rt.ids_in = ids;
+    rt.num_slots = num_slots;
+    rt.E = static_cast<int>(E);
+  } else if (!sort_in_norm) {
     err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k), 0,
                        nullptr, nullptr, ids, expert_to_slot, num_slots, carve(p, workspace), s);
     if (err != hipSuccess) return static_cast<int>(err);
@@ -713,7 +759,7 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
   bt.sgate = shared_gate_weight ? b + p.sgl : nullptr;
   bt.sgate_dtype = dtype;
   return run_experts(p, dtype, hidden, hidden, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, w, ids, workspace, s, bt);
+                     expert_to_slot, w, ids, workspace, s, bt, rg, rt);
 }
 
 int smx_set_tiled_min_tokens(int64_t tokens_per_expert) {
@@ -736,6 +782,13 @@ int smx_set_fp32_gemm_outputs_fp16(int on) {
 }
 
 int smx_fp32_gemm_outputs_fp16(void) { return g_fp32_f16out ? 1 : 0; }
+
+int smx_set_routing_in_gateup(int on) {
+  g_route_in_gateup = on != 0;
+  return SMX_OK;
+}
+
+int smx_routing_in_gateup(void) { return g_route_in_gateup ? 1 : 0; }
 
 int smx_set_profile_events(void* const* events, int count) {
   if (events == nullptr || count == 0) {

@@ -95,9 +95,10 @@ struct WorkItem {
 // Leading `sh.*_blocks` workgroups run the shared expert (v = token range, then tg); the rest
 // run the routing's work ranges (j = range, then tg). Returns false for a workgroup past the
 // ranges of this batch.
+// hdr and ranges: the routing's records (global memory, or a workgroup's own copy in LDS).
 template <typename S>
 __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
-                                          WorkItem& w) {
+                                          WorkItem& w, const int32_t* hdr, const RangeRec* ranges) {
   const int64_t elem = static_cast<int64_t>(sizeof(S));
   const int b = blockIdx.x;
   if (b < shared_blocks) {
@@ -118,8 +119,8 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
   const int j = rb / per_item;  // one of the expert's ranges; uniform across the workgroup
   // j is below the launch's range bound, so the record may be read before the range count is
   // known (the loads then share one latency); records past the count are unused.
-  const int nranges = uniform(a.rb.hdr[0]);
-  const RangeRec& rr = a.rb.ranges[j];
+  const int nranges = uniform(hdr[0]);
+  const RangeRec& rr = ranges[j];
   const int off = uniform(rr.off);
   const int cnt = uniform(rr.cnt);
   const int key = uniform(rr.key);

@@ -20,6 +20,7 @@
 // silu_and_mul (:337), the down GEMM scaled by the routing weight before rounding (:197-203),
 // and the fp32 top-k sum rounded once (:344-347).
 #include "expert_items.h"
+#include "topk_device.h"
 
 namespace smx {
 
@@ -195,9 +196,11 @@ __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTok
 // The token passes of one gate/up workgroup with MT token tiles per pass: wave `wave` owns
 // weight-row tile p (gate rows [16p, 16p+16) and the matching up rows); `owner` is false for
 // a wave past the expert's last tile (it streams tile p again and stores nothing).
+// `sorted`: the routing's sorted flat assignments (global memory, or the workgroup's LDS copy).
 template <int CP, int DT, int MT>
 __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkItem& it, int p,
-                                              bool owner, u32x4* lds, u32x4* bsh) {
+                                              bool owner, u32x4* lds, u32x4* bsh,
+                                              const int32_t* sorted) {
   using S = typename Elem<DT>::S;
   const int lane = lane_id();
   const int wave = wave_id();
@@ -222,7 +225,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       const int q = min(q0 + j * kTokTile + 4 * wave + (lane >> 4), m - 1);
-      const int tok = it.shared ? off + q : a.rb.sorted_f[off + q] / a.k;
+      const int tok = it.shared ? off + q : sorted[off + q] / a.k;
       tb.off[j] = static_cast<uint32_t>(tok * row_bytes + (lane & 15) * 16);
     }
     f32x4 acc[2][MT];
@@ -255,33 +258,72 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
 // one tile of 16 tokens.
 template <int CP, int DT, int MT>
 __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem& it, int p,
-                                            bool owner, u32x4* lds, u32x4* bsh) {
-  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1>(a, it, p, owner, lds, bsh);
-  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1)>(a, it, p, owner, lds, bsh);
-  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1)>(a, it, p, owner, lds, bsh);
-  else gateup_passes<CP, DT, MT>(a, it, p, owner, lds, bsh);
+                                            bool owner, u32x4* lds, u32x4* bsh,
+                                            const int32_t* sorted) {
+  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1>(a, it, p, owner, lds, bsh, sorted);
+  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1)>(a, it, p, owner, lds, bsh, sorted);
+  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1)>(a, it, p, owner, lds, bsh, sorted);
+  else gateup_passes<CP, DT, MT>(a, it, p, owner, lds, bsh, sorted);
 }
 
 // kMulti: the launch may hold experts split into several token ranges (T > span). Their
 // items load weights with normal caching (the ranges of a weight group read the same rows
 // side by side); every other item streams with the non-temporal hint.
-template <bool kMulti, int DT, int MT>
+// RG > 0: the routing runs inside the launch (a.rt; RG lanes per token in the top-k): wave 0
+// of every routed workgroup routes the batch into the workgroup's LDS (route_small_wave), the
+// workgroup meets at a barrier and takes its work item and token rows from there; the first
+// routed workgroup also writes the records (and the top-k results) the later kernels read.
+// The shared-expert workgroups need no routing and start at once.
+template <bool kMulti, int DT, int MT, int RG>
 __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a) {
   const int wave = wave_id();
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
   const int Iw = in_shared ? a.sh.I : a.I;
   const int tiles = Iw / kRowTile;
   const int groups = (tiles + kExpertWaves - 1) / kExpertWaves;
+  const int32_t* hdr = a.rb.hdr;
+  const RangeRec* ranges = a.rb.ranges;
+  const int32_t* sorted = a.rb.sorted_f;
+  if constexpr (RG > 0) {
+    __shared__ SmallRouteLds sc;
+    __shared__ RangeRec rr_l[kWave];
+    __shared__ int32_t sf_l[kWave];
+    __shared__ int32_t hdr_l[2];
+    if (!in_shared) {
+      if (wave == 0) {
+        SmallRouteOut g, l;
+        l.hdr = hdr_l;
+        l.ranges = rr_l;
+        l.sorted_f = sf_l;
+        if (static_cast<int>(blockIdx.x) == a.sh.gateup_blocks) {
+          g.w = a.rt.w_out;
+          g.ids = a.rt.ids_out;
+          g.hdr = a.rb.hdr;
+          g.ranges = a.rb.ranges;
+          g.sorted_f = a.rb.sorted_f;
+          g.tmask = a.rb.tmask;
+          g.fpos = a.rb.fpos;
+          g.fslot = a.rb.fpos ? a.rb.fslot : nullptr;
+        }
+        route_small_wave<DT, RG>(a.rt.logits, a.T, a.rt.E, a.k, a.rt.renorm, a.rt.ids_in, a.e2s,
+                                 a.rt.num_slots, sc, g, l);
+      }
+      __syncthreads();
+      hdr = hdr_l;
+      ranges = rr_l;
+      sorted = sf_l;
+    }
+  }
   WorkItem it;
-  if (!work_item<typename Elem<DT>::S>(a, a.sh.gateup_blocks, groups, it)) return;
+  if (!work_item<typename Elem<DT>::S>(a, a.sh.gateup_blocks, groups, it, hdr, ranges)) return;
   const int praw = it.tg * kExpertWaves + wave;
   const bool owner = praw < tiles;
   const int p = owner ? praw : tiles - 1;
   __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
   __shared__ u32x4 bsh[2 * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
-  if (kMulti && it.nr > 1) gateup_item<0, DT, MT>(a, it, p, owner, lds, bsh);
-  else gateup_item<kNonTemporal, DT, MT>(a, it, p, owner, lds, bsh);
+  if (kMulti && it.nr > 1) gateup_item<0, DT, MT>(a, it, p, owner, lds, bsh, sorted);
+  else gateup_item<kNonTemporal, DT, MT>(a, it, p, owner, lds, bsh, sorted);
 }
 
 // The token passes of one down workgroup with MT token tiles per pass: wave `wave` owns W2
@@ -361,7 +403,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void down_kernel(ExpertArgs a) {
   const int splits = in_shared ? a.sh.splits : a.splits;
   const int split_steps = in_shared ? a.sh.split_steps : a.split_steps;
   WorkItem it;
-  if (!work_item<typename Elem<DT>::S>(a, a.sh.down_blocks, groups * splits, it)) return;
+  if (!work_item<typename Elem<DT>::S>(a, a.sh.down_blocks, groups * splits, it, a.rb.hdr, a.rb.ranges)) return;
   const int sp = it.tg / groups;
   const int tg = it.tg - sp * groups;
   const int rtraw = tg * kExpertWaves + wave;
@@ -762,7 +804,7 @@ static void launch_stage_m(int stage, const ExpertArgs& a, int max_ranges, hipSt
   if (stage == 0) {
     const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
     const int64_t blocks = a.sh.gateup_blocks + max_ranges * groups;
-    gateup_kernel<kMulti, DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
+    gateup_kernel<kMulti, DT, MT, 0><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   } else {
     const int64_t groups = (a.H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves;
     const int64_t blocks = a.sh.down_blocks + max_ranges * groups * a.splits;
@@ -798,8 +840,40 @@ static hipError_t launch_stage(int stage, int dtype, const ExpertArgs& a, int ma
   }
 }
 
-hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles, hipStream_t s) {
-  return launch_stage(0, dtype, a, max_ranges, tok_tiles, s);
+template <int DT, int MT>
+static void launch_gateup_routed(const ExpertArgs& a, int max_ranges, int route_g, hipStream_t s) {
+  const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
+  const unsigned blocks = static_cast<unsigned>(a.sh.gateup_blocks + max_ranges * groups);
+  switch (route_g) {
+    case 8: gateup_kernel<false, DT, MT, 8><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    case 16: gateup_kernel<false, DT, MT, 16><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    case 32: gateup_kernel<false, DT, MT, 32><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    default: gateup_kernel<false, DT, MT, 64><<<blocks, kExpertThreads, 0, s>>>(a); break;
+  }
+}
+
+template <int DT>
+static void launch_gateup_routed_dt(const ExpertArgs& a, int max_ranges, int tok_tiles, int route_g,
+                                    hipStream_t s) {
+  if (tok_tiles <= 1) launch_gateup_routed<DT, 1>(a, max_ranges, route_g, s);
+  else launch_gateup_routed<DT, 2>(a, max_ranges, route_g, s);
+}
+
+hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles, hipStream_t s,
+                         int route_g) {
+  if (route_g == 0) return launch_stage(0, dtype, a, max_ranges, tok_tiles, s);
+  // routing inside the launch: one wave routes T*k <= 64 assignments over E <= 64 experts, and
+  // every expert is one token range (T <= span, at most two token tiles)
+  if (a.T * a.k > kWave || a.rt.E > kWave || a.T > a.rb.span || tok_tiles > 2 ||
+      (route_g != 8 && route_g != 16 && route_g != 32 && route_g != 64) ||
+      (a.rt.logits != nullptr && a.T * route_g > kWave * kSmallRoutePasses))
+    return hipErrorInvalidValue;
+  switch (dtype) {
+    case kF32: launch_gateup_routed_dt<kF32>(a, max_ranges, tok_tiles, route_g, s); break;
+    case kF16: launch_gateup_routed_dt<kF16>(a, max_ranges, tok_tiles, route_g, s); break;
+    default: launch_gateup_routed_dt<kBF16>(a, max_ranges, tok_tiles, route_g, s); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles, hipStream_t s) {

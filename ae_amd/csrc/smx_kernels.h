@@ -13,6 +13,9 @@ constexpr int kMaxExpertsPerLane = kMaxExperts / kWave;
 constexpr int kMaxAssignments = 16384;  // T * top_k
 constexpr int kMaxTopK = 16;
 constexpr int kTokBatch = 1;            // wave-passes of tokens a wave computes together
+// Token passes of 64/G tokens (T * G <= 256) of the one-wave routing: each pass is a dependent
+// chain of group reductions, so beyond a few passes the multi-wave kernel is faster.
+constexpr int kSmallRoutePasses = 4;
 
 // Expert-kernel geometry.
 constexpr int kExpertThreads = 256;                 // 4 independent waves per workgroup
@@ -75,6 +78,19 @@ struct SharedArgs {
   int down_blocks;      // leading workgroups of the down launch that run it
 };
 
+// Routing done inside the gate/up launch for small batches (T*k <= 64 assignments over E <= 64
+// experts, at most 64/G tokens per pass in 4 passes): no routing launch. Every routed workgroup
+// routes the batch itself (one wave, into LDS) and takes its work item from that; the first
+// routed workgroup also writes the routing records and top-k results for the later kernels.
+struct InRoute {
+  const void* logits;      // [T, E] router logits in the activation dtype (null: ids given)
+  const int32_t* ids_in;   // [T, k] caller ids when logits is null
+  float* w_out;            // [T, k] top-k weights out (logits given)
+  int32_t* ids_out;        // [T, k] top-k ids out (logits given)
+  int64_t num_slots;
+  int E, renorm;
+};
+
 struct ExpertArgs {
   const void* x;        // [T, H] hidden states
   const void* pool;     // [num_slots, page_elems] expert pages
@@ -87,6 +103,7 @@ struct ExpertArgs {
   int splits;           // K splits of the down projection
   int split_steps;      // load steps per split
   int f16out;           // fp32 runs: routed gate/up outputs rounded to fp16 (reference stores)
+  InRoute rt;           // used by the gate/up launch with routing inside (route_g > 0)
   SharedArgs sh;
 };
 
@@ -177,8 +194,9 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
                         float* w_out, int32_t* ids_out, const int32_t* ids_in,
                         const int64_t* e2s, int64_t num_slots, const RouteBuffers& rb,
                         hipStream_t s);
+// route_g > 0: the routing runs inside the launch (a.rt), with route_g lanes per token.
 hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
-                         hipStream_t s);
+                         hipStream_t s, int route_g = 0);
 hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
                        hipStream_t s);
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s);

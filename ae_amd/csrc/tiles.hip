@@ -312,7 +312,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_gateup_kernel(ExpertAr
   const int Iw = in_shared ? a.sh.I : a.I;
   const int groups = (Iw + kTileGateCols - 1) / kTileGateCols;
   WorkItem it;
-  if (!work_item<S>(a, a.sh.gateup_blocks, groups, it)) return;
+  if (!work_item<S>(a, a.sh.gateup_blocks, groups, it, a.rb.hdr, a.rb.ranges)) return;
   __shared__ u32x4 st0[kTStage], st1[kTStage], st2[DT == kF32 ? 1 : kTStage];
   __shared__ u32x4 wtiles[kExpertWaves][kTATiles * kRowTile * kTSlots];
   const int H = a.H, I = it.I;
@@ -383,7 +383,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_down_kernel(ExpertArgs
   const int splits = in_shared ? a.sh.splits : a.splits;
   const int split_steps = in_shared ? a.sh.split_steps : a.split_steps;  // 64-byte units
   WorkItem it;
-  if (!work_item<S>(a, a.sh.down_blocks, rgroups * splits, it)) return;
+  if (!work_item<S>(a, a.sh.down_blocks, rgroups * splits, it, a.rb.hdr, a.rb.ranges)) return;
   __shared__ u32x4 st0[kTStage], st1[kTStage], st2[DT == kF32 ? 1 : kTStage];
   __shared__ u32x4 wtiles[kExpertWaves][kTATiles * kRowTile * kTSlots];
   const int sp = it.tg / rgroups;

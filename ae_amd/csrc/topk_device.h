@@ -1,0 +1,366 @@
+// Device building blocks of the top-k softmax gating and of the one-wave routing, shared by the
+// routing kernels (routing.hip) and the expert kernels that route small batches themselves
+// (experts.hip).
+#pragma once
+
+#include "smx_kernels.h"
+
+namespace smx {
+
+// ---------------------------------------------------------------------------------------
+// Top-k softmax, G lanes per token (G = 8, 16, 32 or 64; a wave holds 64/G tokens). Lane j of
+// a group holds experts j + G*i, i < PL (PL = 4 only for G = 64: up to 256 experts). On
+// return lane j < k of each group holds the j-th pick (descending probability, ties to the
+// lower expert index). The arithmetic (max, exp_nonpos, per-lane sequential sum, butterfly
+// over the group with offsets 1, 2, ..., G/2, p = ex * (1/sum), renormalisation by division
+// with the sum taken in j order) equals the oracle's 64-lane butterfly bit for bit: with
+// E <= G every lane at or past G holds an exact zero, so the oracle's steps at offsets >= G
+// only add zeros.
+// Semantics follow select_experts as called at specmoe/layers/FusedMoE.py:174-185.
+//
+// NB wave-passes (NB groups of tokens) are computed in lockstep: every butterfly step is
+// issued for all NB before the next, so the NB independent shuffle chains hide each
+// other's latency.
+// ---------------------------------------------------------------------------------------
+template <int G, int PL>
+struct TopkGroup {
+  static_assert(PL == 1 || G == kWave, "several experts per lane only with whole-wave groups");
+  static constexpr int kTokens = kWave / G;  // tokens per wave-pass
+};
+
+// Lane j of a group reads experts j + G*i of token t. Experts past E read -inf (never
+// selected); a token past T reads zeros so that its arithmetic stays finite (its results
+// are discarded).
+template <int LDT, int G, int PL>
+__device__ __forceinline__ void load_logits(const void* logits, int t, int T, int E, float (&v)[PL]) {
+  const int j = lane_id() % G;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int e = j + G * i;
+    v[i] = e >= E ? -__builtin_inff()
+                  : (t < T ? load_as_f32<LDT>(logits, static_cast<int64_t>(t) * E + e) : 0.0f);
+  }
+}
+
+// Cross-lane exchange within rows of 16 lanes by DPP (a VALU operand modifier, no LDS
+// round trip). Controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1] (lane ^ 2),
+// row_half_mirror (lane i <-> 7 - i within 8), row_mirror (lane i <-> 15 - i within 16).
+constexpr int kDppXor1 = 0xB1;
+constexpr int kDppXor2 = 0x4E;
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ float readlane(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// op-reduction over the G lanes of each group; every lane of the group gets the result.
+// The steps pair lane i with i^1, i^2, then (on values already equal across each quad,
+// resp. half-row) with the mirrored lane, which holds the same value as lane i^4 (resp.
+// i^8); rows are combined as op(op(r0, r1), op(r2, r3)) from lanes 0, 16, 32, 48. For a
+// commutative op every intermediate value equals that of the xor butterfly over offsets
+// 1, 2, 4, ..., G/2 (for fp32 addition bit for bit: a + b == b + a exactly).
+template <int G, typename Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+  v = op(v, dpp<kDppXor1>(v));
+  v = op(v, dpp<kDppXor2>(v));
+  v = op(v, dpp<kDppHalfMirror>(v));
+  if constexpr (G >= 16) v = op(v, dpp<kDppMirror>(v));
+  if constexpr (G >= 32) {
+    const float r0 = readlane(v, 0), r1 = readlane(v, 16), r2 = readlane(v, 32), r3 = readlane(v, 48);
+    if constexpr (G == 32) v = lane_id() < 32 ? op(r0, r1) : op(r2, r3);
+    else v = op(op(r0, r1), op(r2, r3));
+  }
+  return v;
+}
+
+// (p, e) pair order: larger p first, ties to the lower expert index.
+__device__ __forceinline__ bool better(float op, int oe, float bp, int be) {
+  return op > bp || (op == bp && oe < be);
+}
+
+template <int CTRL>
+__device__ __forceinline__ void argmax_step(float& bp, int& be) {
+  const float op = dpp<CTRL>(bp);
+  const int oe = dpp<CTRL>(be);
+  if (better(op, oe, bp, be)) { bp = op; be = oe; }
+}
+
+// Arg-max over the G lanes of each group, the same reduction shape as group_reduce.
+template <int G>
+__device__ __forceinline__ void group_argmax(float& bp, int& be) {
+  argmax_step<kDppXor1>(bp, be);
+  argmax_step<kDppXor2>(bp, be);
+  argmax_step<kDppHalfMirror>(bp, be);
+  if constexpr (G >= 16) argmax_step<kDppMirror>(bp, be);
+  if constexpr (G >= 32) {
+    float p[4];
+    int e[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p[r] = readlane(bp, 16 * r);
+      e[r] = __builtin_amdgcn_readlane(be, 16 * r);
+    }
+    if (better(p[1], e[1], p[0], e[0])) { p[0] = p[1]; e[0] = e[1]; }
+    if (better(p[3], e[3], p[2], e[2])) { p[2] = p[3]; e[2] = e[3]; }
+    if constexpr (G == 32) {
+      const bool hi = lane_id() >= 32;
+      bp = hi ? p[2] : p[0];
+      be = hi ? e[2] : e[0];
+    } else {
+      if (better(p[2], e[2], p[0], e[0])) { p[0] = p[2]; e[0] = e[2]; }
+      bp = p[0];
+      be = e[0];
+    }
+  }
+}
+
+template <int G, int PL, int NB>
+__device__ __forceinline__ void group_topk_softmax(float (&p)[NB][PL], int E, int k, bool renorm,
+                                                   float (&w_out)[NB], int (&id_out)[NB]) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  const int j = lane % G;
+  const int base = lane - j;
+  float m[NB], s[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    m[b] = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < PL; ++i) m[b] = fmaxf(m[b], p[b][i]);
+    m[b] = group_reduce<G>(m[b], [](float a, float c) { return fmaxf(a, c); });
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int e = j + G * i;
+      p[b][i] = (e < E) ? exp_nonpos(p[b][i] - m[b]) : 0.0f;
+      s[b] = (i == 0) ? p[b][i] : s[b] + p[b][i];
+    }
+    s[b] = group_reduce<G>(s[b], [](float a, float c) { return a + c; });
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float inv = 1.0f / s[b];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int e = j + G * i;
+      p[b][i] = (e < E) ? p[b][i] * inv : -1.0f;  // -1 marks "not selectable"
+    }
+    w_out[b] = 0.0f;
+    id_out[b] = -1;
+  }
+  for (int jj = 0; jj < k; ++jj) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float bp = -2.0f;
+      int be = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        if (p[b][i] > bp) { bp = p[b][i]; be = j + G * i; }  // ascending e: strict > keeps lowest
+      group_argmax<G>(bp, be);
+      if (j == be % G) {
+#pragma unroll
+        for (int i = 0; i < PL; ++i)
+          if (i == be / G) p[b][i] = -1.0f;
+      }
+      if (j == jj) { w_out[b] = bp; id_out[b] = be; }
+    }
+  }
+  if (renorm) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float sum = 0.0f;
+      for (int jj = 0; jj < k; ++jj) {
+        const float v = (G == kWave) ? readlane(w_out[b], jj) : __shfl(w_out[b], base + jj, kWave);
+        sum = (jj == 0) ? v : sum + v;
+      }
+      if (j < k) w_out[b] = w_out[b] / sum;
+    }
+  }
+}
+
+// Top-k by ranking, for one expert per lane (E <= 64). The softmax is as above; then lane j
+// of a group forms the exact 64-bit key (bits(p) << 8) | (255 - j) -- p >= 0, so larger keys
+// mean larger p, ties to the lower expert index -- and its rank is the number of larger keys
+// in its group, read back from the wave's LDS slice (independent compares instead of k
+// dependent arg-max rounds). Lane j with rank r < k is the r-th pick: slot_out = r (else -1).
+// Renormalisation divides by the picks' sum taken in rank order.
+struct RankScratch {
+  uint64_t key[kTokBatch][kWave];
+  float pick[kTokBatch][kWave];
+};
+
+template <int G, int NB>
+__device__ __forceinline__ void group_topk_rank(float (&p)[NB][1], int E, int k, bool renorm,
+                                                RankScratch& rs, float (&w_out)[NB],
+                                                int (&id_out)[NB], int (&slot_out)[NB]) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  const int j = lane % G;
+  const int base = lane - j;
+  const bool valid = j < E;
+  uint64_t key[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const float m = group_reduce<G>(p[b][0], [](float a, float c) { return fmaxf(a, c); });
+    const float ex = valid ? exp_nonpos(p[b][0] - m) : 0.0f;
+    const float s = group_reduce<G>(ex, [](float a, float c) { return a + c; });
+    p[b][0] = ex * (1.0f / s);
+    key[b] = valid ? ((static_cast<uint64_t>(__float_as_uint(p[b][0])) << 8) | static_cast<uint64_t>(255 - j)) : 0ull;
+    rs.key[b][lane] = key[b];
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    int rank = 0;
+#pragma unroll
+    for (int g = 0; g < G; ++g) rank += rs.key[b][base + g] > key[b] ? 1 : 0;
+    slot_out[b] = (valid && rank < k) ? rank : -1;
+    w_out[b] = p[b][0];
+    id_out[b] = j;
+  }
+  if (renorm) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      if (slot_out[b] >= 0) rs.pick[b][base + slot_out[b]] = w_out[b];
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float sum = rs.pick[b][base];
+      for (int r = 1; r < k; ++r) sum = sum + rs.pick[b][base + r];
+      w_out[b] = w_out[b] / sum;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();  // the slice is reused by the next batch
+}
+
+// ---------------------------------------------------------------------------------------
+// Routing of a small batch (T*k <= 64 assignments, E <= 64) by one wave, without workgroup
+// barriers: the top-k of every token (all logits loaded up front, one latency), then lane f
+// takes assignment f and the sort is done with ballots. For each lane the lanes with the same
+// expert and the lanes with a smaller expert are found bit by bit from the top id bit down
+// (eq: lanes agreeing on the bits so far; a lane whose id has a 1 where an eq lane has a 0
+// ranks that lane below it); the sorted position is (#smaller) + (#same below this lane), so
+// within an expert assignments stay in ascending f, and the active-expert index is the number
+// of smaller experts present. The records are those of the multi-wave routing kernel (same
+// order, same values). With logits null the ids come from ids_in (out-of-range ids dropped).
+// ---------------------------------------------------------------------------------------
+
+// Outputs of the one-wave routing; null members are not written.
+struct SmallRouteOut {
+  float* w = nullptr;           // [T*k] top-k weights
+  int32_t* ids = nullptr;       // [T*k] top-k expert ids
+  int32_t* hdr = nullptr;       // [0] work ranges (= active experts), [1] dropped flag
+  RangeRec* ranges = nullptr;   // one per active expert (every expert is one range: T <= span)
+  int32_t* sorted_f = nullptr;  // [T*k]
+  int32_t* tmask = nullptr;     // [T]
+  int32_t* fpos = nullptr;      // [T*k]
+  int64_t* fslot = nullptr;     // [T*k]
+};
+
+struct SmallRouteLds {
+  RankScratch rs;
+  int ids[kWave];
+  int64_t slot[kWave];
+};
+
+// Called by one whole wave; writes every non-null member of `a` and of `b`.
+template <int LDT, int G>
+__device__ __forceinline__ void route_small_wave(const void* logits, int T, int E, int k, int renorm,
+                                                 const int32_t* ids_in, const int64_t* e2s,
+                                                 int64_t num_slots, SmallRouteLds& sc,
+                                                 const SmallRouteOut& a, const SmallRouteOut& b) {
+  constexpr int TPW = kWave / G;  // tokens per pass
+  const int lane = lane_id();
+  const int N = T * k;
+  const int64_t my_slot = lane < E ? e2s[lane] : -1;
+  int e = -2;
+  if (logits != nullptr) {
+    const int passes = (T + TPW - 1) / TPW;
+    float v[kSmallRoutePasses][1];
+#pragma unroll
+    for (int ps = 0; ps < kSmallRoutePasses; ++ps)
+      if (ps < passes) load_logits<LDT, G, 1>(logits, ps * TPW + lane / G, T, E, v[ps]);
+#pragma unroll
+    for (int ps = 0; ps < kSmallRoutePasses; ++ps) {
+      if (ps >= passes) break;
+      float pv[1][1] = {{v[ps][0]}};
+      float w[1];
+      int id[1], slot[1];
+      group_topk_rank<G, 1>(pv, E, k, renorm != 0, sc.rs, w, id, slot);
+      const int t = ps * TPW + lane / G;
+      if (t < T && slot[0] >= 0) {
+        const int f = t * k + slot[0];
+        if (a.w) a.w[f] = w[0];
+        if (a.ids) a.ids[f] = id[0];
+        if (b.w) b.w[f] = w[0];
+        if (b.ids) b.ids[f] = id[0];
+        sc.ids[f] = id[0];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    if (lane < N) e = sc.ids[lane];
+  } else if (lane < N) {
+    const int x = ids_in[lane];
+    e = (x >= 0 && x < E) ? x : -2;
+  }
+  sc.slot[lane] = (my_slot >= 0 && my_slot < num_slots) ? my_slot : -1;
+  __builtin_amdgcn_wave_barrier();
+  const int64_t sl = e >= 0 ? sc.slot[e] : -1;
+  const bool ok = e >= 0 && sl >= 0;
+  const uint64_t okm = ballot(ok);
+  const bool bad = ballot(lane < N && !ok) != 0;
+  if (lane < T) {
+    const int32_t tm = static_cast<int32_t>((okm >> (lane * k)) & ((1ull << k) - 1));
+    if (a.tmask) a.tmask[lane] = tm;
+    if (b.tmask) b.tmask[lane] = tm;
+  }
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  uint64_t eq = okm, less = 0;
+  for (int bb = nbits - 1; bb >= 0; --bb) {
+    const bool bit = ok && ((e >> bb) & 1);
+    const uint64_t m1 = ballot(bit);
+    if (bit) less |= eq & ~m1;
+    eq &= bit ? m1 : (okm & ~m1);
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  const int rank = __popcll(eq & below);
+  const int nless = __popcll(less);
+  const uint64_t first = ballot(ok && rank == 0);
+  if (ok) {
+    const int pos = nless + rank;
+    if (a.sorted_f) a.sorted_f[pos] = lane;
+    if (b.sorted_f) b.sorted_f[pos] = lane;
+    if (a.fpos) { a.fpos[lane] = pos; a.fslot[lane] = sl; }
+    if (b.fpos) { b.fpos[lane] = pos; b.fslot[lane] = sl; }
+    if (rank == 0) {
+      const int ai = __popcll(less & first);
+      RangeRec rec{};
+      rec.slot = sl;
+      rec.off = nless;
+      rec.cnt = __popcll(eq);
+      rec.key = ai;
+      rec.j0 = ai;
+      rec.nr = 1;
+      if (a.ranges) a.ranges[ai] = rec;
+      if (b.ranges) b.ranges[ai] = rec;
+    }
+  }
+  if (lane == 0) {
+    const int na = __popcll(first);
+    if (a.hdr) { a.hdr[0] = na; a.hdr[1] = bad ? 1 : 0; }
+    if (b.hdr) { b.hdr[0] = na; b.hdr[1] = bad ? 1 : 0; }
+  }
+}
+
+}  // namespace smx

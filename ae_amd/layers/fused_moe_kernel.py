@@ -104,6 +104,24 @@ def fp32_gemm_outputs_fp16(on: bool = True) -> Iterator[None]:
         set_fp32_gemm_outputs_fp16(prev)
 
 
+def set_routing_in_gateup(on: bool) -> bool:
+    """Route small batches inside the gate/up launch (default) or with the routing kernels.
+    Returns the previous setting. Process-wide."""
+    prev = bool(_lib.lib().smx_routing_in_gateup())
+    _lib.call("smx_set_routing_in_gateup", 1 if on else 0)
+    return prev
+
+
+@contextlib.contextmanager
+def routing_in_gateup(on: bool) -> Iterator[None]:
+    """Scope a set_routing_in_gateup setting (restored on exit)."""
+    prev = set_routing_in_gateup(on)
+    try:
+        yield
+    finally:
+        set_routing_in_gateup(prev)
+
+
 def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:
     H = hidden_states.shape[1]
     _, page_size = w1.shape

@@ -268,6 +268,13 @@ def run_tokens(args, wl, T, layers, L, dev):
     fd = L.smx_fused_down_max_tokens()
     units = T * (k * -(-I * es // 1024) + -(-Is * es // 1024))
     fused_down = not tiled and 1 <= T <= 8 and (T <= fd if fd >= 0 else units <= 48)
+    # and whether the routing runs inside the gate/up launch (small batches, logits in bf16)
+    group = 8 if E <= 8 else 16 if E <= 16 else 32 if E <= 32 else 64
+    in_launch = (bool(L.smx_routing_in_gateup()) and not tiled and T * k <= 64 and E <= 64
+                 and T <= 32 and T * group <= 256)
+    if args.layer:  # the layer call routes from the norm kernel's picks (one token: in the norm)
+        in_launch = not tiled and T * k <= 64 and E <= 64 and T <= 32 and \
+            (T == 1 or bool(L.smx_routing_in_gateup()))
 
     for i in range(args.warmup):
         step(i)
@@ -353,6 +360,7 @@ def run_tokens(args, wl, T, layers, L, dev):
         "pool_copies_rotated": copies,
         "expert_kernels": "tiled" if tiled else "streaming",
         "down_combine": "fused" if fused_down else "split",
+        "routing_launch": "inside the gate/up launch" if in_launch else "routing kernels",
     }
     if Is:
         config.update({"shared_ffn": Is, "shared_gate": wl["gated"]})
@@ -398,7 +406,9 @@ def run_tokens(args, wl, T, layers, L, dev):
         gateup_gbs = gateup_bytes / (stage_us[1] * 1e-6) / 1e9
         # with the fused down projection + combine no combine kernel runs: the last interval is
         # only the cost of recording an event, and is reported as 0
-        out["stage_us"] = {"route": round(stage_us[0], 2), "gate_up": round(stage_us[1], 2),
+        # routing inside the gate/up launch: the first interval is only an event's cost
+        out["stage_us"] = {"route": 0.0 if in_launch else round(stage_us[0], 2),
+                           "gate_up": round(stage_us[1], 2),
                            "down": round(stage_us[2], 2),
                            "combine": 0.0 if fused_down else round(stage_us[3], 2)}
         if tiled:  # many tokens per expert: the matrix cores bound the tiled kernels

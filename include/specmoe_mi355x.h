@@ -289,6 +289,20 @@ int smx_set_fp32_gemm_outputs_fp16(int on);
 int smx_fp32_gemm_outputs_fp16(void);
 
 /*
+ * Small batches -- T*top_k <= 64 assignments over E <= 64 experts, T <= 32, router logits (when
+ * given) in the activation dtype and at most four top-k passes of 64/G tokens -- route inside
+ * the gate/up launch on the weight-streaming path: each routed workgroup computes the top-k
+ * and the expert sort of the whole batch in one wave into its LDS, and one of them writes the
+ * routing records and top-k results for the later kernels; no routing kernel is launched. The
+ * records are the routing kernel's, bit for bit. 0 launches the routing kernels instead;
+ * default 1. Process-wide. Plays the role of the reference's separate select_experts and
+ * moe_align_block_size launches (specmoe/layers/FusedMoE.py:174-185,
+ * specmoe/layers/fused_moe_kernel.py:329-330) for such batches.
+ */
+int smx_set_routing_in_gateup(int on);
+int smx_routing_in_gateup(void);
+
+/*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
  * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
  * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and

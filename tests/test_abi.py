@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 29, names
+    assert len(names) == 31, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -172,6 +172,16 @@ def test_fp32_gemm_outputs_fp16_setting():
     finally:
         assert L.smx_set_fp32_gemm_outputs_fp16(0) == _lib.SMX_OK
     assert L.smx_fp32_gemm_outputs_fp16() == 0
+
+
+def test_routing_in_gateup_setting():
+    assert L.smx_routing_in_gateup() == 1
+    try:
+        assert L.smx_set_routing_in_gateup(0) == _lib.SMX_OK
+        assert L.smx_routing_in_gateup() == 0
+    finally:
+        assert L.smx_set_routing_in_gateup(1) == _lib.SMX_OK
+    assert L.smx_routing_in_gateup() == 1
 
 
 def test_python_error_mapping():

@@ -1,0 +1,113 @@
+"""Routing inside the gate/up launch for small batches (no routing kernel): every entry point
+it covers gives the same bits as with the routing kernels, and matches the oracle, through
+the C ABI -- routing from logits (fused forward, shared-expert blocks), from caller ids
+(stack_fused_moe, dropped and repeated ids included) and from the norm kernel's picks (the
+layer call)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as ref
+from ae_amd.layers import (fused_moe_forward, fused_moe_shared_forward, moe_layer_forward,
+                           routing_in_gateup, stack_fused_moe)
+from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _inputs(T, H, E, dtype, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dtype)
+    logits = (torch.randn((T, E), generator=g, device=DEV) * 2.0).to(dtype)
+    return x, logits
+
+
+def _both(fn):
+    outs = {}
+    for on in (True, False):
+        with routing_in_gateup(on):
+            outs[on] = fn()
+        torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,H,I,E,k,P", [
+    (1, 256, 128, 8, 2, 8),
+    (3, 128, 256, 64, 6, 70),      # 18 assignments over 64 experts, some slots unmapped
+    (4, 256, 128, 60, 4, 60),
+    (16, 256, 128, 8, 2, 8),       # one token tile
+    (32, 256, 128, 8, 2, 12),      # 64 assignments, two token tiles
+    (8, 128, 128, 16, 8, 16),      # 64 assignments over 16 experts
+])
+def test_fused_forward_in_launch_routing(dtype, T, H, I, E, k, P):
+    x, logits = _inputs(T, H, E, dtype, seed=T * 3 + E)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E + k)
+    if P > E:
+        slots[1] = P + 5  # an expert outside the pool: its assignments are dropped
+    outs = _both(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                           return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y, w, ids = outs[True]
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, TORCH_TO_ORACLE[dtype])
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("T", [1, 2, 4])
+def test_shared_block_in_launch_routing(T):
+    """DeepSeek-V2-Lite block: the shared expert's workgroups start without routing."""
+    H, I, E, k, Is = 2048, 1408, 64, 6, 2816
+    x, logits = _inputs(T, H, E, torch.bfloat16, seed=50 + T)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=51)
+    g = torch.Generator(device=DEV).manual_seed(52)
+    page = (torch.randn((3 * Is * H,), generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    outs = _both(lambda: fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page,
+                                                  None, 1.0, inplace=False))
+    assert torch.equal(outs[True], outs[False])
+    y_ref, _, _ = ref.fused_moe_shared_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                               slots.cpu().numpy(), k, False, "bf16",
+                                               shared_page=to_oracle(page))
+    assert max_rel_err(f32_of(outs[True]), y_ref) <= TOL[torch.bfloat16]
+
+
+def test_stack_fused_moe_in_launch_routing_caller_ids():
+    T, H, I, E, k = 6, 256, 128, 8, 3
+    x, _ = _inputs(T, H, E, torch.bfloat16, seed=61)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=62)
+    slots[5] = 1000
+    ids = torch.tensor([[0, 9, 5], [2, 2, 7], [-1, 5, 8], [3, 1, 0], [7, 6, 4], [1, 1, 1]],
+                       dtype=torch.int32, device=DEV)
+    w = torch.rand((T, k), generator=torch.Generator(device=DEV).manual_seed(63), device=DEV)
+    logits = torch.zeros((T, E), dtype=torch.bfloat16, device=DEV)
+    outs = _both(lambda: stack_fused_moe(x.clone(), pool, slots, logits, w, ids, False))
+    assert torch.equal(outs[True], outs[False])
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
+    assert max_rel_err(f32_of(outs[True]), y_ref) <= TOL[torch.bfloat16]
+
+
+@pytest.mark.parametrize("T,E,k", [(2, 8, 2), (8, 64, 6), (32, 8, 2)])
+def test_layer_call_in_launch_routing(T, E, k):
+    """The layer call from two tokens up: the norm kernel's picks sorted inside gate/up."""
+    H, I, dt = 256, 256, torch.bfloat16
+    g = torch.Generator(device=DEV).manual_seed(70 + T)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    r = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    nw = (torch.randn((H,), generator=g, device=DEV) * 0.1 + 1).to(dt)
+    gw = (torch.randn((E, H), generator=g, device=DEV) * 0.05).to(dt)
+    pool, slots = make_pool(E, H, I, dt, num_slots=E + 3, seed=71)
+
+    def run():
+        xx, rr = x.clone(), r.clone()
+        y, (lg, w, ids) = moe_layer_forward(xx, rr, nw, 1e-6, gw, pool, slots, k, E <= 8,
+                                            return_routing=True)
+        return y, rr, lg, w, ids
+
+    outs = _both(run)
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
