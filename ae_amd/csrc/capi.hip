@@ -290,6 +290,17 @@ struct BlockTerms {
   int sgate_dtype = kF32;
 };
 
+// Largest batch (assignments) routed inside the gate/up launch by the multi-wave form, and with
+// logits its largest top-k (T * G elements: 8 wave-passes, 2 per wave). Every routed workgroup
+// repeats the top-k, and its latency passes into the kernel time: measured (us per layer,
+// routing kernels vs inside) DeepSeek-V2-Lite 8 tokens (T*G 512) 122.1 vs 120.6, Mixtral 64
+// tokens (512) 437.1 vs 435.3, but DeepSeek-V2-Lite 16 tokens (1024) 154.4 vs 154.3, Qwen1.5-MoE
+// 16 tokens (1024) 123.7 vs 125.0, DeepSeek-V2-Lite 32 tokens (2048) 181.7 vs 198.3. With ids
+// given (the sort alone) the layer call gains at every size: DeepSeek-V2-Lite 32 tokens 191.7
+// vs 188.8.
+constexpr int64_t kRouteInLaunchMax = 256;
+constexpr int64_t kRouteInLaunchTopkMax = 512;
+
 // Lanes per token of the one-wave top-k: the power of two >= E, at least 8.
 int route_group(int64_t E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64; }
 
@@ -297,12 +308,19 @@ int route_group(int64_t E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 6
 // T*k <= 64 assignments over E <= 64 experts, every expert one token range of at most two
 // token tiles, the top-k (when logits are given, in the activation dtype) in at most 4 passes
 // of 64/G tokens. Returns G, or 0 when the routing kernels run instead.
-int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logits, bool logits_dt_ok) {
+int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logits, bool logits_dt_ok,
+                      bool* multi) {
+  *multi = false;
   if (!g_route_in_gateup) return 0;
-  if (p.tiled || T < 1 || T * k > kWave || E > kWave || T > p.span || p.tok_tiles > 2) return 0;
+  if (p.tiled || T < 1 || E > kWave || T > p.span || (logits && !logits_dt_ok)) return 0;
   const int g = route_group(E);
-  if (logits && (!logits_dt_ok || T * g > kWave * kSmallRoutePasses)) return 0;
-  return g;
+  if (T * k <= kWave && p.tok_tiles <= 2 && (!logits || T * g <= kWave * kSmallRoutePasses)) return g;
+  // the multi-wave form: the workgroup's 4 waves run the top-k, one wave sorts
+  if (T * k <= kRouteInLaunchMax && T <= kWave && (!logits || T * g <= kRouteInLaunchTopkMax)) {
+    *multi = true;
+    return g;
+  }
+  return 0;
 }
 
 // Shared tail of the MoE entry points: expert kernels then combine. route_g > 0: the gate/up
@@ -311,7 +329,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
                 int64_t I, int64_t E, int64_t k, const void* pool, int64_t num_slots,
                 int64_t page_elems, const int64_t* e2s, const float* w, const int32_t* ids,
                 void* ws, hipStream_t s, const BlockTerms& bt = BlockTerms{}, int route_g = 0,
-                const InRoute& rt = InRoute{}) {
+                const InRoute& rt = InRoute{}, bool route_multi = false) {
   char* b = static_cast<char*>(ws);
   ExpertArgs a{};
   a.x = hidden;
@@ -341,7 +359,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   }
   a.rt = rt;
   hipError_t err = p.tiled ? launch_tile_gateup(dtype, a, p.max_ranges, s)
-                           : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s, route_g);
+                           : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s, route_g, route_multi);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(2, s);
   if (p.rows) {
@@ -488,7 +506,8 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
   if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
   hipStream_t s = static_cast<hipStream_t>(stream);
   mark(0, s);
-  const int rg = in_launch_route_g(p, T, E, top_k, false, true);
+  bool rmulti = false;
+  const int rg = in_launch_route_g(p, T, E, top_k, false, true, &rmulti);
   InRoute rt{};
   if (rg > 0) {
     rt.ids_in = topk_ids;
@@ -501,7 +520,7 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
   }
   mark(1, s);
   return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, topk_weights, topk_ids, workspace, s, BlockTerms{}, rg, rt);
+                     expert_to_slot, topk_weights, topk_ids, workspace, s, BlockTerms{}, rg, rt, rmulti);
 }
 
 }  // extern "C"
@@ -553,7 +572,8 @@ int fused_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H
   int32_t* ids = topk_ids_out ? topk_ids_out : reinterpret_cast<int32_t*>(b + p.ids);
   hipStream_t s = static_cast<hipStream_t>(stream);
   mark(0, s);
-  const int rg = in_launch_route_g(p, T, E, top_k, true, logits_dtype == dtype);
+  bool rmulti = false;
+  const int rg = in_launch_route_g(p, T, E, top_k, true, logits_dtype == dtype, &rmulti);
   InRoute rt{};
   if (rg > 0) {
     rt.logits = router_logits;
@@ -570,7 +590,7 @@ int fused_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H
   }
   mark(1, s);
   return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, w, ids, workspace, s, bt, rg, rt);
+                     expert_to_slot, w, ids, workspace, s, bt, rg, rt, rmulti);
 }
 
 }  // namespace
@@ -740,7 +760,8 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
   hipError_t err = launch_norm_gate(g, s);
   if (err != hipSuccess) return static_cast<int>(err);
   // larger small batches: the sort of the norm kernel's picks inside the gate/up launch
-  const int rg = sort_in_norm ? 0 : in_launch_route_g(p, T, E, top_k, false, true);
+  bool rmulti = false;
+  const int rg = sort_in_norm ? 0 : in_launch_route_g(p, T, E, top_k, false, true, &rmulti);
   InRoute rt{};
   if (rg > 0) {
     rt.ids_in = ids;
@@ -759,7 +780,7 @@ int smx_moe_layer_forward(void* hidden, void* residual, int dtype, int64_t T, in
   bt.sgate = shared_gate_weight ? b + p.sgl : nullptr;
   bt.sgate_dtype = dtype;
   return run_experts(p, dtype, hidden, hidden, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, w, ids, workspace, s, bt, rg, rt);
+                     expert_to_slot, w, ids, workspace, s, bt, rg, rt, rmulti);
 }
 
 int smx_set_tiled_min_tokens(int64_t tokens_per_expert) {

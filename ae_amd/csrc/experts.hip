@@ -274,7 +274,11 @@ __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem&
 // workgroup meets at a barrier and takes its work item and token rows from there; the first
 // routed workgroup also writes the records (and the top-k results) the later kernels read.
 // The shared-expert workgroups need no routing and start at once.
-template <bool kMulti, int DT, int MT, int RG>
+// RM: the larger in-launch form (up to kSortWaveMax assignments over E <= 64, T <= 64): the
+// workgroup's 4 waves run the top-k (RG lanes per token; or load caller ids), then wave 0 sorts
+// the assignments (sort_wave) into the workgroup's LDS; the first routed workgroup also
+// writes the records and top-k results, and its threads the token mask.
+template <bool kMulti, int DT, int MT, int RG, bool RM = false>
 __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a) {
   const int wave = wave_id();
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
@@ -284,7 +288,74 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
   const int32_t* hdr = a.rb.hdr;
   const RangeRec* ranges = a.rb.ranges;
   const int32_t* sorted = a.rb.sorted_f;
-  if constexpr (RG > 0) {
+  if constexpr (RG > 0 && RM) {
+    __shared__ int16_t ids_l[kSortWaveMax];
+    __shared__ int64_t slot_l[kWave];
+    __shared__ SortWaveLds sw;
+    __shared__ RangeRec rr_l[kWave];
+    __shared__ int32_t sf_l[kSortWaveMax];
+    __shared__ int32_t hdr_l[2];
+    __shared__ RankScratch rs_all[kExpertWaves];
+    if (!in_shared) {
+      const int lane = lane_id();
+      const int tid = threadIdx.x;
+      const int N = a.T * a.k;
+      const int E = a.rt.E;
+      const bool writer = static_cast<int>(blockIdx.x) == a.sh.gateup_blocks;
+      const int64_t my_slot = tid < E ? a.e2s[tid] : -1;
+      if (a.rt.logits != nullptr) {
+        constexpr int TPW = TopkGroup<RG, 1>::kTokens;
+        const int stride = kExpertWaves * TPW;
+        for (int t0 = wave * TPW + lane / RG; t0 - lane / RG < a.T; t0 += stride * kTokBatch) {
+          topk_batch<DT, RG, 1>(a.rt.logits, a.T, E, a.k, a.rt.renorm != 0, t0, stride, rs_all[wave],
+                                [&](int t, int slot, float wv, int id) {
+            const int f = t * a.k + slot;
+            if (writer) {
+              a.rt.w_out[f] = wv;
+              a.rt.ids_out[f] = id;
+            }
+            ids_l[f] = static_cast<int16_t>(id);
+          });
+        }
+      } else {
+        for (int f = tid; f < N; f += kExpertThreads) {
+          const int x = a.rt.ids_in[f];
+          ids_l[f] = static_cast<int16_t>((x >= 0 && x < E) ? x : -2);
+        }
+      }
+      if (tid < kWave) slot_l[tid] = (my_slot >= 0 && my_slot < a.rt.num_slots) ? my_slot : -1;
+      __syncthreads();
+      if (writer) {
+        for (int t = tid; t < a.T; t += kExpertThreads) {
+          uint32_t m = 0;
+          for (int j = 0; j < a.k; ++j) {
+            const int e = ids_l[t * a.k + j];
+            if (e >= 0 && slot_l[e] >= 0) m |= 1u << j;
+          }
+          a.rb.tmask[t] = static_cast<int32_t>(m);
+        }
+      }
+      if (wave == 0) {
+        AlignOutputs g{}, l{};
+        g.span = a.rb.span;
+        l.hdr = hdr_l;
+        l.ranges = rr_l;
+        l.sorted_f = sf_l;
+        if (writer) {
+          g.hdr = a.rb.hdr;
+          g.ranges = a.rb.ranges;
+          g.sorted_f = a.rb.sorted_f;
+          g.fpos = a.rb.fpos;
+          g.fslot = a.rb.fpos ? a.rb.fslot : nullptr;
+        }
+        sort_wave<true>(ids_l, slot_l, N, E, sw, g, l);
+      }
+      __syncthreads();
+      hdr = hdr_l;
+      ranges = rr_l;
+      sorted = sf_l;
+    }
+  } else if constexpr (RG > 0) {
     __shared__ SmallRouteLds sc;
     __shared__ RangeRec rr_l[kWave];
     __shared__ int32_t sf_l[kWave];
@@ -840,38 +911,52 @@ static hipError_t launch_stage(int stage, int dtype, const ExpertArgs& a, int ma
   }
 }
 
-template <int DT, int MT>
+template <int DT, int MT, bool RM>
 static void launch_gateup_routed(const ExpertArgs& a, int max_ranges, int route_g, hipStream_t s) {
   const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
   const unsigned blocks = static_cast<unsigned>(a.sh.gateup_blocks + max_ranges * groups);
   switch (route_g) {
-    case 8: gateup_kernel<false, DT, MT, 8><<<blocks, kExpertThreads, 0, s>>>(a); break;
-    case 16: gateup_kernel<false, DT, MT, 16><<<blocks, kExpertThreads, 0, s>>>(a); break;
-    case 32: gateup_kernel<false, DT, MT, 32><<<blocks, kExpertThreads, 0, s>>>(a); break;
-    default: gateup_kernel<false, DT, MT, 64><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    case 8: gateup_kernel<false, DT, MT, 8, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    case 16: gateup_kernel<false, DT, MT, 16, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    case 32: gateup_kernel<false, DT, MT, 32, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    default: gateup_kernel<false, DT, MT, 64, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
   }
 }
 
 template <int DT>
 static void launch_gateup_routed_dt(const ExpertArgs& a, int max_ranges, int tok_tiles, int route_g,
-                                    hipStream_t s) {
-  if (tok_tiles <= 1) launch_gateup_routed<DT, 1>(a, max_ranges, route_g, s);
-  else launch_gateup_routed<DT, 2>(a, max_ranges, route_g, s);
+                                    bool multi, hipStream_t s) {
+  if (!multi) {
+    if (tok_tiles <= 1) launch_gateup_routed<DT, 1, false>(a, max_ranges, route_g, s);
+    else launch_gateup_routed<DT, 2, false>(a, max_ranges, route_g, s);
+    return;
+  }
+  switch (tok_tiles) {
+    case 1: launch_gateup_routed<DT, 1, true>(a, max_ranges, route_g, s); break;
+    case 2: launch_gateup_routed<DT, 2, true>(a, max_ranges, route_g, s); break;
+    case 3: launch_gateup_routed<DT, 3, true>(a, max_ranges, route_g, s); break;
+    default: launch_gateup_routed<DT, 4, true>(a, max_ranges, route_g, s); break;
+  }
 }
 
 hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles, hipStream_t s,
-                         int route_g) {
+                         int route_g, bool route_multi) {
   if (route_g == 0) return launch_stage(0, dtype, a, max_ranges, tok_tiles, s);
-  // routing inside the launch: one wave routes T*k <= 64 assignments over E <= 64 experts, and
-  // every expert is one token range (T <= span, at most two token tiles)
-  if (a.T * a.k > kWave || a.rt.E > kWave || a.T > a.rb.span || tok_tiles > 2 ||
-      (route_g != 8 && route_g != 16 && route_g != 32 && route_g != 64) ||
-      (a.rt.logits != nullptr && a.T * route_g > kWave * kSmallRoutePasses))
+  // routing inside the launch, every expert one token range (T <= span): one wave routes
+  // T*k <= 64 assignments over E <= 64 experts in at most 4 top-k passes; the multi-wave form
+  // takes up to kSortWaveMax assignments and up to four token tiles
+  if (route_g != 8 && route_g != 16 && route_g != 32 && route_g != 64) return hipErrorInvalidValue;
+  if (a.rt.E > kWave || a.T > a.rb.span || tok_tiles > kMaxTokTiles) return hipErrorInvalidValue;
+  if (route_multi) {
+    if (a.T * a.k > kSortWaveMax) return hipErrorInvalidValue;
+  } else if (a.T * a.k > kWave || tok_tiles > 2 ||
+             (a.rt.logits != nullptr && a.T * route_g > kWave * kSmallRoutePasses)) {
     return hipErrorInvalidValue;
+  }
   switch (dtype) {
-    case kF32: launch_gateup_routed_dt<kF32>(a, max_ranges, tok_tiles, route_g, s); break;
-    case kF16: launch_gateup_routed_dt<kF16>(a, max_ranges, tok_tiles, route_g, s); break;
-    default: launch_gateup_routed_dt<kBF16>(a, max_ranges, tok_tiles, route_g, s); break;
+    case kF32: launch_gateup_routed_dt<kF32>(a, max_ranges, tok_tiles, route_g, route_multi, s); break;
+    case kF16: launch_gateup_routed_dt<kF16>(a, max_ranges, tok_tiles, route_g, route_multi, s); break;
+    default: launch_gateup_routed_dt<kBF16>(a, max_ranges, tok_tiles, route_g, route_multi, s); break;
   }
   return hipGetLastError();
 }

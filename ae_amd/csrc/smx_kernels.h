@@ -194,9 +194,10 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
                         float* w_out, int32_t* ids_out, const int32_t* ids_in,
                         const int64_t* e2s, int64_t num_slots, const RouteBuffers& rb,
                         hipStream_t s);
-// route_g > 0: the routing runs inside the launch (a.rt), with route_g lanes per token.
+// route_g > 0: the routing runs inside the launch (a.rt), with route_g lanes per token in the
+// top-k; route_multi: the multi-wave form (up to 256 assignments).
 hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
-                         hipStream_t s, int route_g = 0);
+                         hipStream_t s, int route_g = 0, bool route_multi = false);
 hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
                        hipStream_t s);
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s);

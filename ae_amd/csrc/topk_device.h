@@ -244,6 +244,186 @@ __device__ __forceinline__ void group_topk_rank(float (&p)[NB][1], int E, int k,
   __builtin_amdgcn_wave_barrier();  // the slice is reused by the next batch
 }
 
+// The tokens of kTokBatch consecutive wave-passes: token t = first + b * stride for this
+// lane's group. All logit loads are issued before any token is computed, so a wave pays one
+// load latency per batch. fn(t, w, id) is called on every lane (t may be >= T).
+// fn(t, slot, w, id) is called for every pick of token t (t < T): slot in [0, k).
+template <int LDT, int G, int PL, typename Fn>
+__device__ __forceinline__ void topk_batch(const void* logits, int T, int E, int k, bool renorm,
+                                           int first, int stride, RankScratch& rs, Fn&& fn) {
+  float v[kTokBatch][PL];
+#pragma unroll
+  for (int b = 0; b < kTokBatch; ++b) load_logits<LDT, G, PL>(logits, first + b * stride, T, E, v[b]);
+  float w[kTokBatch];
+  int id[kTokBatch];
+  int slot[kTokBatch];
+  if constexpr (PL == 1) {
+    group_topk_rank<G, kTokBatch>(v, E, k, renorm, rs, w, id, slot);
+  } else {
+    group_topk_softmax<G, PL, kTokBatch>(v, E, k, renorm, w, id);
+    const int j = lane_id() % G;
+#pragma unroll
+    for (int b = 0; b < kTokBatch; ++b) slot[b] = j < k ? j : -1;
+  }
+#pragma unroll
+  for (int b = 0; b < kTokBatch; ++b) {
+    const int t = first + b * stride;
+    if (t < T && slot[b] >= 0) fn(t, slot[b], w[b], id[b]);
+  }
+}
+
+struct AlignOutputs {
+  // compact lists for the expert kernels (may be null)
+  int32_t* hdr;         // [0] = number of work ranges, [1] = dropped-assignment flag
+  RangeRec* ranges;     // [active experts + N / span]
+  int span;             // sorted positions per range
+  int32_t* sorted_f;    // [N]
+  int32_t* tmask;       // [T] per token: bit j set if assignment t*k+j is routable
+  int32_t* fpos;        // [N] sorted position of each routable assignment
+  int64_t* fslot;       // [N] pool slot of each routable assignment (route only)
+  // reference-format outputs (may be null)
+  int32_t* sorted_ids;  // [N + E*(BM-1)]
+  int32_t* expert_ids;  // [ceil((N + E*(BM-1)) / BM)]
+  int32_t* ntp;         // [1]
+  int bm;
+};
+
+// Lanes of the wave whose (valid) expert id equals this lane's: one ballot per id bit.
+__device__ __forceinline__ uint64_t same_expert_lanes(int e, bool valid, int nbits) {
+  uint64_t same = ballot(valid);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t m = ballot(bit);
+    same &= bit ? m : ~m;
+  }
+  return same;
+}
+
+// ---------------------------------------------------------------------------------------
+// The expert sort by one wave, for at most kSortWaveMax assignments over at most 64 experts
+// (lane e owns expert e): chunks of 64 assignments in order, the lanes of a chunk with the
+// same expert found with one ballot per id bit, counts per expert in LDS, one wave scan over
+// the experts, then the scatter. No workgroup barriers (a wave's LDS accesses execute in
+// program order). Stable: within an expert, assignments appear in ascending f. Inputs:
+// ids[f] (-1 dropped, -2 out of range: dropped and flagged), slot[e] (kCheckSlots: < 0 drops
+// the expert's assignments and flags them). Every non-null member of `out` and of `out2` is
+// written (out2: a second copy of the records, e.g. in a workgroup's LDS). The records are
+// those of the multi-wave sort (align_block in routing.hip), element for element.
+// Measured against the multi-wave sort (us per layer): DeepSeek-V2-Lite 8 tokens (48
+// assignments, fused top-k) 124.1 -> 122.2, 32 tokens (192) 181.1 -> 180.2; Mixtral 64
+// tokens (128) 438.1 -> 436.5; Qwen1.5-MoE 64 tokens (256) 190.3 -> 189.7; DeepSeek-V2-Lite
+// 64 tokens (384) 198.4 -> 199.3, so the limit is 256.
+// ---------------------------------------------------------------------------------------
+constexpr int kSortWaveMax = 256;
+
+struct SortWaveLds {
+  int cnt[kWave + 1];
+  int off[kWave + 1];
+  int seg[kWave + 1];
+  int run[kWave];
+};
+
+template <bool kCheckSlots>
+__device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E, SortWaveLds& sc,
+                          const AlignOutputs& out, const AlignOutputs& out2) {
+  const int lane = lane_id();
+  const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  const int nch = (N + kWave - 1) / kWave;
+  int* run = sc.run;  // per expert: count, then running sorted position
+  run[lane] = 0;
+  bool bad = false;
+  __builtin_amdgcn_wave_barrier();
+  for (int c = 0; c < nch; ++c) {
+    const int f = c * kWave + lane;
+    int e = f < N ? static_cast<int>(ids[f]) : -1;
+    if (e == -2 || (kCheckSlots && e >= 0 && slot[e] < 0)) {
+      bad = true;
+      e = -1;
+    }
+    const uint64_t same = same_expert_lanes(e, e >= 0, nbits);
+    if (e >= 0 && (same & below) == 0) run[e] += __popcll(same);
+    __builtin_amdgcn_wave_barrier();
+  }
+  // exclusive scans over the experts: compact offset, block-padded segment, active index, range
+  const int ce = lane < E ? run[lane] : 0;
+  const int bm = out.bm > 0 ? out.bm : 1;
+  const int span = out.span > 0 ? out.span : 1;
+  const int pad = (ce + bm - 1) / bm * bm;
+  const int act = ce > 0 ? 1 : 0;
+  const int nr = (ce + span - 1) / span;
+  int ic = ce, ip = pad, ia = act, ir = nr;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int tc = __shfl_up(ic, o, kWave);
+    const int tp = __shfl_up(ip, o, kWave);
+    const int ta = __shfl_up(ia, o, kWave);
+    const int tr = __shfl_up(ir, o, kWave);
+    if (lane >= o) { ic += tc; ip += tp; ia += ta; ir += tr; }
+  }
+  const int off = ic - ce, seg = ip - pad, ai = ia - act, br = ir - nr;
+  const int seg_total = __shfl(ip, kWave - 1, kWave);
+  const int ranges_total = __shfl(ir, kWave - 1, kWave);
+  const bool any_bad = ballot(bad) != 0;
+  if (lane < E) {
+    sc.cnt[lane] = ce;
+    sc.off[lane] = off;
+    sc.seg[lane] = seg;
+    run[lane] = off;
+    if (ce > 0 && (out.ranges || out2.ranges)) {
+      RangeRec rec{};
+      rec.slot = kCheckSlots ? slot[lane] : -1;
+      rec.off = off;
+      rec.cnt = ce;
+      rec.key = ai;
+      rec.j0 = br;
+      rec.nr = nr;
+      for (int r = 0; r < nr; ++r) {
+        if (out.ranges) out.ranges[br + r] = rec;
+        if (out2.ranges) out2.ranges[br + r] = rec;
+      }
+    }
+  }
+  if (lane == 0) {
+    sc.seg[E] = seg_total;
+    if (out.hdr) { out.hdr[0] = ranges_total; out.hdr[1] = any_bad ? 1 : 0; }
+    if (out2.hdr) { out2.hdr[0] = ranges_total; out2.hdr[1] = any_bad ? 1 : 0; }
+    if (out.ntp) out.ntp[0] = seg_total;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // scatter: every lane reads its expert's running position before the rank-0 lane advances it
+  for (int c = 0; c < nch; ++c) {
+    const int f = c * kWave + lane;
+    int e = f < N ? static_cast<int>(ids[f]) : -1;
+    if (e == -2 || (kCheckSlots && e >= 0 && slot[e] < 0)) e = -1;
+    const uint64_t same = same_expert_lanes(e, e >= 0, nbits);
+    if (e >= 0) {
+      const int rank = __popcll(same & below);
+      const int pos = run[e] + rank;
+      if (out.sorted_f) out.sorted_f[pos] = f;
+      if (out2.sorted_f) out2.sorted_f[pos] = f;
+      if (out.fpos) {
+        out.fpos[f] = pos;
+        out.fslot[f] = kCheckSlots ? slot[e] : -1;
+      }
+      if (out.sorted_ids) out.sorted_ids[sc.seg[e] + (pos - sc.off[e])] = f;
+      if (rank == 0) run[e] = pos + __popcll(same);
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // reference format: sentinel padding and per-block expert ids
+  if (out.sorted_ids) {
+    const int len = N + E * (bm - 1);
+    const int nblocks = (len + bm - 1) / bm;
+    for (int e = 0; e < E; ++e) {
+      for (int p = sc.seg[e] + sc.cnt[e] + lane; p < sc.seg[e + 1]; p += kWave) out.sorted_ids[p] = N;
+      for (int b = sc.seg[e] / bm + lane; b < sc.seg[e + 1] / bm; b += kWave) out.expert_ids[b] = e;
+    }
+    for (int p = seg_total + lane; p < len; p += kWave) out.sorted_ids[p] = N;
+    for (int b = seg_total / bm + lane; b < nblocks; b += kWave) out.expert_ids[b] = -1;
+  }
+}
+
 // ---------------------------------------------------------------------------------------
 // Routing of a small batch (T*k <= 64 assignments, E <= 64) by one wave, without workgroup
 // barriers: the top-k of every token (all logits loaded up front, one latency), then lane f

@@ -270,11 +270,12 @@ def run_tokens(args, wl, T, layers, L, dev):
     fused_down = not tiled and 1 <= T <= 8 and (T <= fd if fd >= 0 else units <= 48)
     # and whether the routing runs inside the gate/up launch (small batches, logits in bf16)
     group = 8 if E <= 8 else 16 if E <= 16 else 32 if E <= 32 else 64
-    in_launch = (bool(L.smx_routing_in_gateup()) and not tiled and T * k <= 64 and E <= 64
-                 and T <= 32 and T * group <= 256)
+    on = bool(L.smx_routing_in_gateup())
+    in_launch = on and not tiled and E <= 64 and (
+        (T * k <= 64 and T <= 32 and T * group <= 256) or
+        (T * k <= 256 and T <= 64 and T * group <= 512))
     if args.layer:  # the layer call routes from the norm kernel's picks (one token: in the norm)
-        in_launch = not tiled and T * k <= 64 and E <= 64 and T <= 32 and \
-            (T == 1 or bool(L.smx_routing_in_gateup()))
+        in_launch = not tiled and E <= 64 and (T == 1 or (on and T * k <= 256 and T <= 64))
 
     for i in range(args.warmup):
         step(i)

@@ -111,3 +111,61 @@ def test_layer_call_in_launch_routing(T, E, k):
     outs = _both(run)
     for a, b in zip(outs[True], outs[False]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,H,I,E,k,P", [
+    (8, 256, 128, 64, 6, 70),      # 48 assignments in 8 top-k passes: the multi-wave form
+    (20, 128, 128, 64, 6, 64),     # 120 assignments, two token tiles
+    (40, 256, 128, 60, 4, 60),     # 160 assignments, three token tiles
+    (64, 128, 128, 8, 4, 10),      # 256 assignments, four token tiles
+    (50, 256, 256, 16, 5, 20),
+])
+def test_fused_forward_in_launch_routing_multi_wave(dtype, T, H, I, E, k, P):
+    x, logits = _inputs(T, H, E, dtype, seed=T * 5 + E)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E + k + 1)
+    if P > E:
+        slots[2] = P + 9
+    outs = _both(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                           return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y, w, ids = outs[True]
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, TORCH_TO_ORACLE[dtype])
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("T", [16, 32, 42])
+def test_deepseek_block_in_launch_routing_multi_wave(T):
+    H, I, E, k, Is = 2048, 1408, 64, 6, 2816
+    x, logits = _inputs(T, H, E, torch.bfloat16, seed=90 + T)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=91)
+    g = torch.Generator(device=DEV).manual_seed(92)
+    page = (torch.randn((3 * Is * H,), generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    outs = _both(lambda: fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page,
+                                                  None, 1.0, inplace=False))
+    assert torch.equal(outs[True], outs[False])
+
+
+@pytest.mark.parametrize("T,E,k", [(16, 64, 6), (40, 60, 4)])
+def test_layer_call_in_launch_routing_multi_wave(T, E, k):
+    H, I, dt = 256, 128, torch.bfloat16
+    g = torch.Generator(device=DEV).manual_seed(95 + T)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    r = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    nw = (torch.randn((H,), generator=g, device=DEV) * 0.1 + 1).to(dt)
+    gw = (torch.randn((E, H), generator=g, device=DEV) * 0.05).to(dt)
+    pool, slots = make_pool(E, H, I, dt, num_slots=E + 3, seed=96)
+
+    def run():
+        xx, rr = x.clone(), r.clone()
+        y, (lg, w, ids) = moe_layer_forward(xx, rr, nw, 1e-6, gw, pool, slots, k, False,
+                                            return_routing=True)
+        return y, rr, lg, w, ids
+
+    outs = _both(run)
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
