@@ -307,7 +307,8 @@ int route_group(int64_t E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 6
 // The routing runs inside the gate/up launch (no routing launch) for batches one wave routes:
 // T*k <= 64 assignments over E <= 64 experts, every expert one token range of at most two
 // token tiles, the top-k (when logits are given, in the activation dtype) in at most 4 passes
-// of 64/G tokens. Returns G, or 0 when the routing kernels run instead.
+// of 64/G tokens. Returns G, or 0 when the routing kernels run instead. With logits and a 0
+// here, fused_forward asks again without them: the top-k launch runs and gate/up sorts its ids.
 int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logits, bool logits_dt_ok,
                       bool* multi) {
   *multi = false;
@@ -573,15 +574,22 @@ int fused_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H
   hipStream_t s = static_cast<hipStream_t>(stream);
   mark(0, s);
   bool rmulti = false;
-  const int rg = in_launch_route_g(p, T, E, top_k, true, logits_dtype == dtype, &rmulti);
+  int rg = in_launch_route_g(p, T, E, top_k, true, logits_dtype == dtype, &rmulti);
   InRoute rt{};
+  rt.num_slots = num_slots;
+  rt.E = static_cast<int>(E);
   if (rg > 0) {
     rt.logits = router_logits;
     rt.w_out = w;
     rt.ids_out = ids;
-    rt.num_slots = num_slots;
-    rt.E = static_cast<int>(E);
     rt.renorm = renormalize;
+  } else if ((rg = in_launch_route_g(p, T, E, top_k, false, true, &rmulti)) > 0) {
+    // a top-k too large to repeat in every workgroup: its own launch, the sort inside gate/up
+    hipError_t err = launch_topk_softmax(router_logits, logits_dtype, static_cast<int>(T),
+                                         static_cast<int>(E), static_cast<int>(top_k), renormalize,
+                                         w, ids, s);
+    if (err != hipSuccess) return static_cast<int>(err);
+    rt.ids_in = ids;
   } else {
     hipError_t err = launch_route(router_logits, logits_dtype, static_cast<int>(T), static_cast<int>(E),
                                   static_cast<int>(top_k), renormalize, w, ids, nullptr, expert_to_slot,

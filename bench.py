@@ -274,6 +274,8 @@ def run_tokens(args, wl, T, layers, L, dev):
     in_launch = on and not tiled and E <= 64 and (
         (T * k <= 64 and T <= 32 and T * group <= 256) or
         (T * k <= 256 and T <= 64 and T * group <= 512))
+    # larger top-k: its own launch, the sort inside the gate/up launch
+    sort_in_launch = in_launch or (on and not tiled and E <= 64 and T * k <= 256 and T <= 64)
     if args.layer:  # the layer call routes from the norm kernel's picks (one token: in the norm)
         in_launch = not tiled and E <= 64 and (T == 1 or (on and T * k <= 256 and T <= 64))
 
@@ -361,7 +363,9 @@ def run_tokens(args, wl, T, layers, L, dev):
         "pool_copies_rotated": copies,
         "expert_kernels": "tiled" if tiled else "streaming",
         "down_combine": "fused" if fused_down else "split",
-        "routing_launch": "inside the gate/up launch" if in_launch else "routing kernels",
+        "routing_launch": ("inside the gate/up launch" if in_launch else
+                           "top-k kernel, sort inside the gate/up launch" if sort_in_launch
+                           else "routing kernels"),
     }
     if Is:
         config.update({"shared_ffn": Is, "shared_gate": wl["gated"]})

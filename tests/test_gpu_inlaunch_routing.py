@@ -169,3 +169,32 @@ def test_layer_call_in_launch_routing_multi_wave(T, E, k):
     outs = _both(run)
     for a, b in zip(outs[True], outs[False]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T,H,I,E,k,P,logits_dt", [
+    (16, 256, 128, 64, 6, 70, torch.bfloat16),   # 16 tokens x 64 lanes: top-k in its own launch
+    (42, 128, 128, 64, 6, 64, torch.bfloat16),   # 252 assignments, three token tiles
+    (24, 256, 128, 32, 8, 40, torch.bfloat16),
+    (4, 256, 128, 8, 2, 8, torch.float32),       # logits in another dtype than the activations
+    (40, 128, 256, 60, 4, 60, torch.float32),
+])
+def test_fused_forward_topk_launch_sort_in_gateup(T, H, I, E, k, P, logits_dt):
+    """A top-k too large to repeat in every gate/up workgroup (or logits in another dtype) runs
+    as its own launch; the gate/up launch sorts its ids."""
+    dtype = torch.bfloat16
+    x, _ = _inputs(T, H, E, dtype, seed=T * 11 + E)
+    logits = (torch.randn((T, E), generator=torch.Generator(device=DEV).manual_seed(T + 1),
+                          device=DEV) * 2.0).to(logits_dt)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E + k + 2)
+    if P > E:
+        slots[3] = P + 1
+    outs = _both(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                           return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y, w, ids = outs[True]
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, "bf16")
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
