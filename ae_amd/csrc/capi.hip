@@ -20,6 +20,7 @@ constexpr size_t kAlign = 256;
 // 143 us, 1 split 154 us) as long as the chip is covered (DeepSeek-V2-Lite T=1: 1 split
 // 14.1 us, 11 splits 12.2 us).
 constexpr int64_t kTargetDownWaves = 2048;
+constexpr int64_t kDownFillBlocks = 512;  // one residency: two down workgroups per CU, 256 CUs
 // Tiled path (tiles.hip): its down workgroups to aim for (two per CU), and the default
 // expected tokens per active expert at which it takes over from the streaming kernels
 // (measured crossover: Mixtral 64 tokens per expert 613 vs 637 us, 32: 590 vs 502 us;
@@ -81,6 +82,7 @@ struct Plan {
   int tok_tiles = 1;
   int splits = 1;
   int split_steps = 0;
+  int down_rows = kDownRows;  // W2 row tiles per down wave
   size_t hdr = 0, ranges = 0, sorted_f = 0, w = 0, ids = 0;
   size_t tmask = 0, fpos = 0, fslot = 0;
   size_t act = 0, part = 0, total = 0;
@@ -208,27 +210,49 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     p.span = kTokTile * p.tok_tiles;
     p.max_ranges = p.max_active + p.N / p.span;
     const int64_t nchunks = I * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
-    const int64_t units = static_cast<int64_t>(active + 0.5) * (H / (kRowTile * kDownRows));
-    int64_t want = (kTargetDownWaves + units - 1) / units;
-    if (want < 1) want = 1;
-    // the fewest splits that reach the target, unless the chunk count's divisors overshoot it
-    // by more than 4x (a prime count leaves only 1 and itself)
-    s = divisor_at_least(nchunks, want);
-    if (s > 4 * want) s = divisor_at_most(nchunks, want);
+    const int64_t ex = static_cast<int64_t>(active + 0.5);
+    // Down-projection split for R row tiles per wave: the fewest splits that reach the wave
+    // target, unless the chunk count's divisors overshoot it by more than 4x (a prime count
+    // leaves only 1 and itself); the shared expert's waves stream about as many chunks as a
+    // routed wave. Returns the workgroups expected.
+    int64_t ss = 1;
+    auto down_split = [&](int R) {
+      const int64_t rgroups = (H / (kRowTile * R) + kExpertWaves - 1) / kExpertWaves;
+      const int64_t units = ex * (H / (kRowTile * R));
+      int64_t want = (kTargetDownWaves + units - 1) / units;
+      if (want < 1) want = 1;
+      s = divisor_at_least(nchunks, want);
+      if (s > 4 * want) s = divisor_at_most(nchunks, want);
+      int64_t blocks = ex * rgroups * s;
+      if (Is > 0) {
+        const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+        const int64_t per = nchunks / s;
+        ss = divisor_at_most(schunks, (schunks + per - 1) / per);
+        blocks += ((T + p.span - 1) / p.span) * rgroups * ss;
+      }
+      return blocks;
+    };
+    // Two row tiles per wave, unless that grid would not fill one residency of the chip (two
+    // workgroups per CU): then one, which doubles the workgroups. Measured, us per down launch,
+    // two vs one row tiles, same box: DeepSeek-V2-Lite 3 tokens (304 workgroups) 25.7 vs 22.2,
+    // 4 tokens (368) 26.7 vs 24.4, 6 tokens (496) 38.2 vs 34.8; Qwen1.5-MoE 4 tokens (304)
+    // 24.1 vs 24.1, 8 tokens (464) 27.6 vs 28.9. Full grids lose with one: Qwen1.5-MoE 16
+    // tokens (704) 41.0 vs 42.2, Mixtral 32 tokens 142.9 vs 147.7.
+    if (down_split(kDownRows) < kDownFillBlocks) {
+      p.down_rows = 1;
+      down_split(1);
+    }
     p.splits = static_cast<int>(s);
     p.split_steps = static_cast<int>(nchunks / s * kUnroll);
     if (Is > 0) {
-      // The shared expert's down projection is split so that its waves stream about as many
-      // chunks as a routed wave; its token ranges match the kernel's token-tile span.
+      // its token ranges match the kernel's token-tile span
       const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
-      const int64_t per = nchunks / s;
-      const int64_t ss = divisor_at_most(schunks, (schunks + per - 1) / per);
       p.Is = static_cast<int>(Is);
       p.s_splits = static_cast<int>(ss);
       p.s_split_steps = static_cast<int>(schunks / ss * kUnroll);
       p.s_tok_groups = static_cast<int>((T + p.span - 1) / p.span);
       p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + kExpertWaves - 1) / kExpertWaves));
-      p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves) * ss);
+      p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * p.down_rows) + kExpertWaves - 1) / kExpertWaves) * ss);
     }
   }
   size_t o = 0;
@@ -346,6 +370,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   a.part = reinterpret_cast<float*>(b + p.part);
   a.splits = p.splits;
   a.split_steps = p.split_steps;
+  a.down_rows = p.down_rows;
   a.f16out = dtype == kF32 && g_fp32_f16out ? 1 : 0;
   if (p.Is > 0) {
     a.sh.page = bt.shared_page;

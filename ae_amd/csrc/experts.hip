@@ -399,12 +399,11 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
 
 // The token passes of one down workgroup with MT token tiles per pass: wave `wave` owns W2
 // rows [32*rt, 32*rt + 32) over the K slice of split sp.
-template <int CP, int DT, int MT>
+template <int CP, int DT, int MT, int R>
 __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem& it, int rt,
                                             bool owner, int sp, int split_steps, u32x4* lds,
                                             u32x4* bsh) {
   using S = typename Elem<DT>::S;
-  constexpr int R = kDownRows;
   const int lane = lane_id();
   const int wave = wave_id();
   const int r = lane & 15, g = lane >> 4;
@@ -455,20 +454,22 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
 // Workgroup = (work item, K split, 4 consecutive pairs of W2 row tiles): wave w owns rows
 // [32*(4*group + w), +32). Waves past the last pair repeat it and store nothing. Token tiles
 // per pass as in gateup_kernel.
-template <int CP, int DT, int MT>
+template <int CP, int DT, int MT, int R>
 __device__ __forceinline__ void down_item(const ExpertArgs& a, const WorkItem& it, int rt,
                                           bool owner, int sp, int split_steps, u32x4* lds,
                                           u32x4* bsh) {
-  if (MT == 1 || it.m <= kTokTile) down_passes<CP, DT, 1>(a, it, rt, owner, sp, split_steps, lds, bsh);
-  else if (MT == 2 || it.m <= 2 * kTokTile) down_passes<CP, DT, (MT >= 2 ? 2 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
-  else if (MT == 3 || it.m <= 3 * kTokTile) down_passes<CP, DT, (MT >= 3 ? 3 : 1)>(a, it, rt, owner, sp, split_steps, lds, bsh);
-  else down_passes<CP, DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  if (MT == 1 || it.m <= kTokTile) down_passes<CP, DT, 1, R>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else if (MT == 2 || it.m <= 2 * kTokTile) down_passes<CP, DT, (MT >= 2 ? 2 : 1), R>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else if (MT == 3 || it.m <= 3 * kTokTile) down_passes<CP, DT, (MT >= 3 ? 3 : 1), R>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else down_passes<CP, DT, MT, R>(a, it, rt, owner, sp, split_steps, lds, bsh);
 }
 
-template <bool kMulti, int DT, int MT>
+// R: W2 row tiles per wave (kDownRows; 1 doubles the workgroups of a grid too small to fill
+// the chip).
+template <bool kMulti, int DT, int MT, int R = kDownRows>
 __global__ __launch_bounds__(kExpertThreads, 2) void down_kernel(ExpertArgs a) {
   const int wave = wave_id();
-  const int rtiles = a.H / (kRowTile * kDownRows);
+  const int rtiles = a.H / (kRowTile * R);
   const int groups = (rtiles + kExpertWaves - 1) / kExpertWaves;
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.down_blocks;
   const int splits = in_shared ? a.sh.splits : a.splits;
@@ -480,11 +481,11 @@ __global__ __launch_bounds__(kExpertThreads, 2) void down_kernel(ExpertArgs a) {
   const int rtraw = tg * kExpertWaves + wave;
   const bool owner = rtraw < rtiles;
   const int rt = owner ? rtraw : rtiles - 1;
-  __shared__ u32x4 lds_all[kExpertWaves][kDownRows * kTileSlots];
+  __shared__ u32x4 lds_all[kExpertWaves][R * kTileSlots];
   __shared__ u32x4 bsh[2 * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
-  if (kMulti && it.nr > 1) down_item<0, DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
-  else down_item<kNonTemporal, DT, MT>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  if (kMulti && it.nr > 1) down_item<0, DT, MT, R>(a, it, rt, owner, sp, split_steps, lds, bsh);
+  else down_item<kNonTemporal, DT, MT, R>(a, it, rt, owner, sp, split_steps, lds, bsh);
 }
 
 __device__ __forceinline__ float load_scalar(const void* base, int dtype, int64_t i) {
@@ -877,9 +878,11 @@ static void launch_stage_m(int stage, const ExpertArgs& a, int max_ranges, hipSt
     const int64_t blocks = a.sh.gateup_blocks + max_ranges * groups;
     gateup_kernel<kMulti, DT, MT, 0><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   } else {
-    const int64_t groups = (a.H / (kRowTile * kDownRows) + kExpertWaves - 1) / kExpertWaves;
+    const int R = a.down_rows == 1 ? 1 : kDownRows;
+    const int64_t groups = (a.H / (kRowTile * R) + kExpertWaves - 1) / kExpertWaves;
     const int64_t blocks = a.sh.down_blocks + max_ranges * groups * a.splits;
-    down_kernel<kMulti, DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
+    if (R == 1) down_kernel<kMulti, DT, MT, 1><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
+    else down_kernel<kMulti, DT, MT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   }
 }
 

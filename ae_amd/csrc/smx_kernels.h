@@ -25,6 +25,7 @@ constexpr int kTokTile = 16;                        // token columns per MFMA ti
 constexpr int kStepBytes = 64;                      // row bytes one 16-byte/lane load step covers
 constexpr int kUnroll = 4;                          // load steps per chunk (256 bytes per row)
 constexpr int kDownRows = 2;                        // row tiles per wave in the down projection
+                                                    // (1 for grids that would not fill the chip)
 constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 tokens)
 
 static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
@@ -103,6 +104,7 @@ struct ExpertArgs {
   int splits;           // K splits of the down projection
   int split_steps;      // load steps per split
   int f16out;           // fp32 runs: routed gate/up outputs rounded to fp16 (reference stores)
+  int down_rows;        // W2 row tiles per down wave: kDownRows, or 1
   InRoute rt;           // used by the gate/up launch with routing inside (route_g > 0)
   SharedArgs sh;
 };
