@@ -339,9 +339,13 @@ int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logit
   if (!g_route_in_gateup) return 0;
   if (p.tiled || T < 1 || E > kWave || T > p.span || (logits && !logits_dt_ok)) return 0;
   const int g = route_group(E);
-  if (T * k <= kWave && p.tok_tiles <= 2 && (!logits || T * g <= kWave * kSmallRoutePasses)) return g;
+  // the workgroup's LDS copy of the range records holds every range the launch's grid covers
+  if (T * k <= kWave && p.tok_tiles <= 2 && (!logits || T * g <= kWave * kSmallRoutePasses) &&
+      p.max_ranges <= kSmallRangesMax)
+    return g;
   // the multi-wave form: the workgroup's 4 waves run the top-k, one wave sorts
-  if (T * k <= kRouteInLaunchMax && T <= kWave && (!logits || T * g <= kRouteInLaunchTopkMax)) {
+  if (T * k <= kRouteInLaunchMax && T <= kWave && (!logits || T * g <= kRouteInLaunchTopkMax) &&
+      p.max_ranges <= kSortRangesMax) {
     *multi = true;
     return g;
   }

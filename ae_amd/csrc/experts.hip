@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
     __shared__ int16_t ids_l[kSortWaveMax];
     __shared__ int64_t slot_l[kWave];
     __shared__ SortWaveLds sw;
-    __shared__ RangeRec rr_l[kWave];
+    __shared__ RangeRec rr_l[kSortRangesMax];
     __shared__ int32_t sf_l[kSortWaveMax];
     __shared__ int32_t hdr_l[2];
     __shared__ RankScratch rs_all[kExpertWaves];
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
     }
   } else if constexpr (RG > 0) {
     __shared__ SmallRouteLds sc;
-    __shared__ RangeRec rr_l[kWave];
+    __shared__ RangeRec rr_l[kSmallRangesMax];
     __shared__ int32_t sf_l[kWave];
     __shared__ int32_t hdr_l[2];
     if (!in_shared) {
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
           g.fslot = a.rb.fpos ? a.rb.fslot : nullptr;
         }
         route_small_wave<DT, RG>(a.rt.logits, a.T, a.rt.E, a.k, a.rt.renorm, a.rt.ids_in, a.e2s,
-                                 a.rt.num_slots, sc, g, l);
+                                 a.rt.num_slots, a.rb.span, sc, g, l);
       }
       __syncthreads();
       hdr = hdr_l;

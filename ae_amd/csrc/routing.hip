@@ -283,12 +283,12 @@ __global__ __launch_bounds__(kWave) void route_small_kernel(
   o.w = w_out;
   o.ids = ids_out;
   o.hdr = out.hdr;
-  o.ranges = out.ranges;  // the host runs this kernel only when T <= span
+  o.ranges = out.ranges;
   o.sorted_f = out.sorted_f;
   o.tmask = out.tmask;
   o.fpos = out.fpos;
   o.fslot = out.fpos ? out.fslot : nullptr;
-  route_small_wave<LDT, G>(logits, T, E, k, renorm, ids_in, e2s, num_slots, sc, o, SmallRouteOut{});
+  route_small_wave<LDT, G>(logits, T, E, k, renorm, ids_in, e2s, num_slots, out.span, sc, o, SmallRouteOut{});
 }
 
 // ---------------------------------------------------------------------------------------

@@ -31,6 +31,15 @@ constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 
 static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
               "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");
 
+// In-launch routing (the gate/up kernel routes a small batch itself and keeps the range records
+// in the workgroup's LDS). The one-wave form takes at most 64 assignments, the one-wave sort
+// (sort_wave) at most kSortWaveMax, over at most 64 experts. Range records at most: one per
+// active expert plus one per further span (>= kTokTile sorted positions) of an expert's
+// assignments.
+constexpr int kSortWaveMax = 256;
+constexpr int kSmallRangesMax = kWave + kWave / kTokTile;
+constexpr int kSortRangesMax = kWave + kSortWaveMax / kTokTile;
+
 // Tiled expert kernels (tiles.hip), for experts that see many tokens: output tiles of
 // 128 token rows by 128 intermediate columns (gate/up) or 256 W2 rows (down) per workgroup.
 constexpr int kTileTok = 128;        // sorted positions per work range

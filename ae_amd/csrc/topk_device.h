@@ -314,7 +314,6 @@ __device__ __forceinline__ uint64_t same_expert_lanes(int e, bool valid, int nbi
 // tokens (128) 438.1 -> 436.5; Qwen1.5-MoE 64 tokens (256) 190.3 -> 189.7; DeepSeek-V2-Lite
 // 64 tokens (384) 198.4 -> 199.3, so the limit is 256.
 // ---------------------------------------------------------------------------------------
-constexpr int kSortWaveMax = 256;
 
 struct SortWaveLds {
   int cnt[kWave + 1];
@@ -440,8 +439,8 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
 struct SmallRouteOut {
   float* w = nullptr;           // [T*k] top-k weights
   int32_t* ids = nullptr;       // [T*k] top-k expert ids
-  int32_t* hdr = nullptr;       // [0] work ranges (= active experts), [1] dropped flag
-  RangeRec* ranges = nullptr;   // one per active expert (every expert is one range: T <= span)
+  int32_t* hdr = nullptr;       // [0] work ranges, [1] dropped flag
+  RangeRec* ranges = nullptr;   // [kSmallRangesMax] ceil(cnt / span) per active expert
   int32_t* sorted_f = nullptr;  // [T*k]
   int32_t* tmask = nullptr;     // [T]
   int32_t* fpos = nullptr;      // [T*k]
@@ -452,13 +451,19 @@ struct SmallRouteLds {
   RankScratch rs;
   int ids[kWave];
   int64_t slot[kWave];
+  int nr[kWave];  // ranges per active expert, then the first range of each (several-range case)
 };
 
-// Called by one whole wave; writes every non-null member of `a` and of `b`.
+
+// Called by one whole wave; writes every non-null member of `a` and of `b`. `span`: sorted
+// positions per work range. Top-k picks are distinct per token, so with logits (T <= span) every
+// expert is one range; caller ids may repeat an expert within a token, and an expert with more
+// than `span` assignments then gets ceil(cnt / span) ranges, numbered by a wave scan over the
+// active experts (the multi-wave sort's records, element for element).
 template <int LDT, int G>
 __device__ __forceinline__ void route_small_wave(const void* logits, int T, int E, int k, int renorm,
                                                  const int32_t* ids_in, const int64_t* e2s,
-                                                 int64_t num_slots, SmallRouteLds& sc,
+                                                 int64_t num_slots, int span, SmallRouteLds& sc,
                                                  const SmallRouteOut& a, const SmallRouteOut& b) {
   constexpr int TPW = kWave / G;  // tokens per pass
   const int lane = lane_id();
@@ -517,29 +522,51 @@ __device__ __forceinline__ void route_small_wave(const void* logits, int T, int 
   const int rank = __popcll(eq & below);
   const int nless = __popcll(less);
   const uint64_t first = ballot(ok && rank == 0);
+  const bool lead = ok && rank == 0;  // this lane writes its expert's records
+  const int cnt = __popcll(eq);
+  const int ai = __popcll(less & first);
+  const int nr = lead ? (cnt + span - 1) / span : 0;
+  int j0 = ai;
+  int nranges = __popcll(first);
+  if (ballot(nr > 1) != 0) {  // wave-uniform: some expert needs several ranges
+    if (lead) sc.nr[ai] = nr;
+    __builtin_amdgcn_wave_barrier();
+    const int v = lane < nranges ? sc.nr[lane] : 0;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int t = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += t;
+    }
+    nranges = __shfl(incl, kWave - 1, kWave);
+    __builtin_amdgcn_wave_barrier();
+    sc.nr[lane] = incl - v;  // first range of active expert `lane`
+    __builtin_amdgcn_wave_barrier();
+    if (lead) j0 = sc.nr[ai];
+  }
   if (ok) {
     const int pos = nless + rank;
     if (a.sorted_f) a.sorted_f[pos] = lane;
     if (b.sorted_f) b.sorted_f[pos] = lane;
     if (a.fpos) { a.fpos[lane] = pos; a.fslot[lane] = sl; }
     if (b.fpos) { b.fpos[lane] = pos; b.fslot[lane] = sl; }
-    if (rank == 0) {
-      const int ai = __popcll(less & first);
+    if (lead) {
       RangeRec rec{};
       rec.slot = sl;
       rec.off = nless;
-      rec.cnt = __popcll(eq);
+      rec.cnt = cnt;
       rec.key = ai;
-      rec.j0 = ai;
-      rec.nr = 1;
-      if (a.ranges) a.ranges[ai] = rec;
-      if (b.ranges) b.ranges[ai] = rec;
+      rec.j0 = j0;
+      rec.nr = nr;
+      for (int r = 0; r < nr; ++r) {
+        if (a.ranges) a.ranges[j0 + r] = rec;
+        if (b.ranges) b.ranges[j0 + r] = rec;
+      }
     }
   }
   if (lane == 0) {
-    const int na = __popcll(first);
-    if (a.hdr) { a.hdr[0] = na; a.hdr[1] = bad ? 1 : 0; }
-    if (b.hdr) { b.hdr[0] = na; b.hdr[1] = bad ? 1 : 0; }
+    if (a.hdr) { a.hdr[0] = nranges; a.hdr[1] = bad ? 1 : 0; }
+    if (b.hdr) { b.hdr[0] = nranges; b.hdr[1] = bad ? 1 : 0; }
   }
 }
 

@@ -8,9 +8,21 @@ with ties resolved to the lower expert index, then an optional renormalisation
 ``custom_routing_function`` replaces that selection: it is called as
 ``custom_routing_function(hidden_states=..., gating_output=..., topk=..., renormalize=...)``
 and its ``(weights, ids)`` are returned as fp32 / int32.
+
+``routed_scaling_factor`` is accepted and, on the paths this build takes, changes nothing:
+sglang 0.4.5.post3's ``select_experts`` hands it only to its grouped top-k, where it sets
+the weight of a shared expert fused into the top-k (``topk_weights[:, -1] =
+topk_weights[:, :-1].sum(-1) / routed_scaling_factor``, and only when the server's
+``n_share_experts_fusion`` is set, which defaults to 0); the ungrouped ``fused_topk`` and a
+custom routing function never see it. Scaling the routed output by the factor is the model
+block's job (DeepSeek-V2's MoE multiplies its routed output by it), which this build does in
+the block entry points (``fused_moe_shared_forward``, ``moe_layer_forward``). The reference
+itself never sets the factor (specmoe/layers/FusedMoE.py:287 defaults it to None and passes it
+through at :184,298,526). Parity with sglang is unpinned here: it is not vendored.
 """
 from __future__ import annotations
 
+import math
 from typing import Callable, Optional, Tuple
 
 import torch
@@ -27,7 +39,8 @@ def check_routing_options(use_grouped_topk: bool, topk_group: Optional[int],
     """Reject the select_experts options this build does not implement.
 
     Grouped top-k with a single group is plain top-k and is accepted; a custom routing
-    function is called as the reference calls it.
+    function is called as the reference calls it; routed_scaling_factor is accepted (it does
+    not change the weights of these selections, see the module docstring) but must be finite.
     """
     if use_grouped_topk and not (num_expert_group in (None, 1) and topk_group in (None, 1)):
         raise NotImplementedError("grouped top-k with more than one expert group")
@@ -35,8 +48,8 @@ def check_routing_options(use_grouped_topk: bool, topk_group: Optional[int],
         raise NotImplementedError("custom_routing_function together with grouped top-k")
     if correction_bias is not None:
         raise NotImplementedError("correction_bias (biased grouped top-k)")
-    if routed_scaling_factor not in (None, 1.0):
-        raise NotImplementedError("routed_scaling_factor other than 1.0")
+    if routed_scaling_factor is not None and not math.isfinite(float(routed_scaling_factor)):
+        raise ValueError(f"routed_scaling_factor must be finite, got {routed_scaling_factor}")
 
 
 def select_experts(

@@ -1,6 +1,9 @@
 """Shared helpers for the GPU parity tests: torch <-> oracle conversions and input builders."""
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 import torch
 
@@ -30,6 +33,32 @@ def max_rel_err(y: np.ndarray, want: np.ndarray) -> float:
 # Output tolerance per activation dtype: max |y - ref| / max |ref|. bf16 carries 8 mantissa
 # bits and four rounding points; the north-star bound is 1e-2.
 TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-4}
+TOL_BY_NAME = {"bf16": 1e-2, "f16": 2e-3, "f32": 1e-4}
+
+
+def elem_rel_err(y: np.ndarray, want: np.ndarray) -> np.ndarray:
+    """Elementwise |y - ref| / max(|ref|, 1e-3 * max|ref|): the relative error of every output,
+    with a floor so that outputs near zero are measured against the output scale."""
+    want = want.astype(np.float64)
+    floor = 1e-3 * max(float(np.abs(want).max()), 1e-30)
+    return np.abs(y.astype(np.float64) - want) / np.maximum(np.abs(want), floor)
+
+
+def parity(y: np.ndarray, want: np.ndarray, tol: float, case: str = "", **extra) -> dict:
+    """Both output metrics of one comparison. Asserts max |y - ref| / max |ref| <= tol and a
+    median elementwise relative error <= tol, and records the figures: with SMX_PARITY_LOG set,
+    one JSON line per comparison is appended to that file."""
+    el = elem_rel_err(y, want)
+    rec = {"case": case, "max_rel_err": max_rel_err(y, want), "tol": tol,
+           "elem_rel_err_median": float(np.median(el)), "elem_rel_err_p99": float(np.quantile(el, 0.99)),
+           "elem_rel_err_max": float(el.max()), "outputs": int(el.size), **extra}
+    path = os.environ.get("SMX_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(rec) + "\n")
+    assert rec["max_rel_err"] <= tol, rec
+    assert rec["elem_rel_err_median"] <= tol, rec
+    return rec
 
 
 def make_pool(E: int, H: int, I: int, dtype: torch.dtype, num_slots: int | None = None,

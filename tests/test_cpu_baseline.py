@@ -1,0 +1,52 @@
+"""The timed CPU baseline (oracle/torch_cpu.py, torch on MKL) against the numpy oracle: same
+routing ids, weights within fp32 rounding, outputs within the parity tolerance -- so the
+baseline bench.py times computes the same layer."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as ref
+from oracle.torch_cpu import TorchCpuMoE
+from tests.golden.synth import make_case
+from tests.helpers import TOL_BY_NAME, parity
+
+
+def _check(case, name):
+    x = torch.from_numpy(ref.to_f32(case["x"], case["dtype"]))
+    logits = torch.from_numpy(np.asarray(case["logits"], np.float32))
+    moe = TorchCpuMoE(case["pool"], case["slot_map"], case["H"], case["dtype"],
+                      shared_page=case["shared_page"])
+    sg = torch.from_numpy(case["shared_gate"]) if case["shared_gate"] is not None else None
+    y, w, ids = moe.forward(x, logits, case["k"], case["renorm"], shared_gate=sg)
+    if case["Is"]:
+        y_ref, w_ref, ids_ref = ref.fused_moe_shared_forward(
+            case["x"], case["logits"], case["pool"], case["slot_map"], case["k"], case["renorm"],
+            case["dtype"], shared_page=case["shared_page"], shared_gate_logits=case["shared_gate"])
+    else:
+        y_ref, w_ref, ids_ref = ref.fused_moe_forward(case["x"], case["logits"], case["pool"],
+                                                      case["slot_map"], case["k"], case["renorm"],
+                                                      case["dtype"])
+    np.testing.assert_array_equal(ids.numpy(), ids_ref)
+    np.testing.assert_allclose(w.numpy(), w_ref, rtol=1e-6, atol=0)
+    return parity(y.numpy(), y_ref, TOL_BY_NAME[case["dtype"]], case=f"torch_cpu vs oracle {name}")
+
+
+@pytest.mark.parametrize("name", ["c1_t32", "dsv2lite_t1", "qwen15_t4"])
+def test_torch_cpu_baseline_matches_oracle(name):
+    rec = _check(make_case(name), name)
+    print(rec)
+
+
+def test_torch_cpu_baseline_ties_and_small_bf16():
+    """Equal logits pick the lowest expert indices; a small bf16 layer agrees with the oracle."""
+    w, ids = TorchCpuMoE.route(torch.zeros((3, 8)), 2, True)
+    assert ids.tolist() == [[0, 1]] * 3
+    assert torch.equal(w, torch.full((3, 2), 0.5))
+    rng = np.random.default_rng(5)
+    T, H, I, E, k = 9, 128, 256, 8, 3
+    pool = ref.f32_to_bf16_bits((rng.standard_normal((E, 3 * I * H)) * 0.05).astype(np.float32))
+    x = ref.f32_to_bf16_bits(rng.standard_normal((T, H)).astype(np.float32))
+    logits = ref.round_to(rng.standard_normal((T, E)).astype(np.float32), "bf16")
+    case = dict(x=x, logits=logits, pool=pool, slot_map=np.arange(E), H=H, k=k, renorm=True,
+                dtype="bf16", Is=0, shared_page=None, shared_gate=None)
+    _check(case, "small")

@@ -8,8 +8,8 @@ import pytest
 import torch
 
 from oracle import moe_ref as ref
-from ae_amd.layers import (fused_moe_forward, fused_moe_shared_forward, moe_layer_forward,
-                           routing_in_gateup, stack_fused_moe)
+from ae_amd.layers import (fused_down_max_tokens, fused_moe_forward, fused_moe_shared_forward,
+                           moe_layer_forward, routing_in_gateup, stack_fused_moe)
 from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle
 
 pytestmark = pytest.mark.gpu
@@ -198,3 +198,51 @@ def test_fused_forward_topk_launch_sort_in_gateup(T, H, I, E, k, P, logits_dt):
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
     assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
+
+
+def _stack_all_paths(x, pool, slots, logits, w, ids, fused):
+    """stack_fused_moe with routing inside gate/up and with the routing kernels, for a fused-down
+    setting (None: the default rule)."""
+    with fused_down_max_tokens(fused):
+        return _both(lambda: stack_fused_moe(x.clone(), pool, slots, logits, w, ids, False))
+
+
+@pytest.mark.parametrize("T,k,fused", [
+    (16, 2, None),   # expert 0 takes all 32 assignments, span 16: two ranges, split down
+    (8, 4, 8),       # 32 assignments on one expert through the fused down + combine
+    (8, 4, 0),       # the same on the split down kernel + combine
+    (32, 2, None),   # 64 assignments, span 32: two ranges
+])
+def test_repeated_caller_ids_beyond_one_range(T, k, fused):
+    """Caller ids that repeat one expert within every token give that expert more assignments
+    than one token range holds: the one-wave routing must emit every range of it."""
+    H, I, E = 256, 128, 8
+    x, _ = _inputs(T, H, E, torch.bfloat16, seed=200 + T + k)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=201)
+    ids = torch.zeros((T, k), dtype=torch.int32, device=DEV)
+    w = torch.rand((T, k), generator=torch.Generator(device=DEV).manual_seed(202), device=DEV)
+    logits = torch.zeros((T, E), dtype=torch.bfloat16, device=DEV)
+    outs = _stack_all_paths(x, pool, slots, logits, w, ids, fused)
+    assert torch.equal(outs[True], outs[False])
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
+    assert max_rel_err(f32_of(outs[True]), y_ref) <= TOL[torch.bfloat16]
+
+
+def test_repeated_caller_ids_more_ranges_than_experts():
+    """64 experts, 16 tokens of top-8: tokens 0-7 cover every expert once, tokens 8-15 pick
+    expert 0 eight times each. Expert 0 then holds 65 assignments (5 ranges of 16), 68 ranges in
+    all -- more than one per expert, in the gate/up launch's multi-wave form."""
+    T, H, I, E, k = 16, 128, 128, 64, 8
+    x, _ = _inputs(T, H, E, torch.bfloat16, seed=210)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=211)
+    ids = torch.zeros((T, k), dtype=torch.int32)
+    ids[:8] = torch.arange(64, dtype=torch.int32).view(8, 8)
+    ids = ids.to(DEV)
+    w = torch.rand((T, k), generator=torch.Generator(device=DEV).manual_seed(212), device=DEV)
+    logits = torch.zeros((T, E), dtype=torch.bfloat16, device=DEV)
+    outs = _stack_all_paths(x, pool, slots, logits, w, ids, None)
+    assert torch.equal(outs[True], outs[False])
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
+    assert max_rel_err(f32_of(outs[True]), y_ref) <= TOL[torch.bfloat16]

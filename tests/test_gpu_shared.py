@@ -8,7 +8,7 @@ import torch
 from oracle import moe_ref as ref
 from ae_amd.layers import (DeepseekV2MoE, Qwen2MoeSparseMoeBlock, fused_moe_forward,
                            fused_moe_shared_forward, set_weight_attrs, tiled_min_tokens)
-from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle
+from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, parity, to_oracle
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -42,8 +42,10 @@ def _check(x, logits, pool, slots, k, renorm, page, sgate, scale):
     y_ref, w_ref, ids_ref = _oracle(x, logits, pool, slots, k, renorm, page, sgate, scale)
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
-    err = max_rel_err(f32_of(y), y_ref)
-    assert err <= TOL[x.dtype], err
+    T, H = x.shape
+    parity(f32_of(y), y_ref, TOL[x.dtype],
+           case=f"shared block T={T} H={H} I={pool.shape[1] // (3 * H)} E={logits.shape[1]} k={k} "
+                f"Is={0 if page is None else page.numel() // (3 * H)} {x.dtype}")
     return y
 
 
@@ -107,6 +109,35 @@ def test_deepseek_v2_lite_shape(T):
     pool, slots = make_pool(E, H, I, torch.bfloat16, num_slots=E, seed=41)
     page = _shared_page(H, Is, torch.bfloat16, seed=42)
     _check(x, logits, pool, slots, k, False, page, None, 1.0)
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_deepseek_v2_lite_layer_chain_in_place(T):
+    """Three DeepSeek-V2-Lite blocks with distinct weights run in place one after another on
+    one hidden-state buffer (each layer's output is the next one's input, as in the stack the
+    benchmark times), against the oracle: every layer fed the GPU's input of that layer, and
+    the whole chain fed its own outputs (three layers of 1e-2 each)."""
+    H, I, E, k, Is, L = 2048, 1408, 64, 6, 2816, 3
+    x0, _, _ = _inputs(T, H, E, torch.bfloat16, seed=60 + T)
+    layers = []
+    for l in range(L):
+        _, logits, _ = _inputs(T, H, E, torch.bfloat16, seed=70 + 10 * T + l)
+        pool, slots = make_pool(E, H, I, torch.bfloat16, num_slots=E, seed=80 + l)
+        layers.append((logits, pool, slots, _shared_page(H, Is, torch.bfloat16, seed=90 + l)))
+    buf = x0.clone()
+    y_chain = to_oracle(x0)
+    for l, (logits, pool, slots, page) in enumerate(layers):
+        x_in = buf.clone()
+        out = fused_moe_shared_forward(buf, logits, pool, slots, k, False, page, None, 1.0, inplace=True)
+        torch.cuda.synchronize()
+        assert out.data_ptr() == buf.data_ptr()
+        y_ref, _, _ = _oracle(x_in, logits, pool, slots, k, False, page, None, 1.0)
+        parity(f32_of(buf), y_ref, TOL[torch.bfloat16], case=f"dsv2lite chain T={T} layer {l}")
+        y_chain, _, _ = ref.fused_moe_shared_forward(
+            ref.f32_to_bf16_bits(y_chain) if y_chain.dtype != np.uint16 else y_chain,
+            f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, False, "bf16",
+            shared_page=to_oracle(page))
+    parity(f32_of(buf), y_chain, L * TOL[torch.bfloat16], case=f"dsv2lite chain T={T} end to end")
 
 
 def test_shared_block_deterministic_bitwise():

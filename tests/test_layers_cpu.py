@@ -61,8 +61,9 @@ def test_unsupported_options_raise():
         check_routing_options(True, 1, 1, lambda **kw: kw, None, None)
     with pytest.raises(NotImplementedError):
         check_routing_options(False, None, None, None, torch.zeros(4), None)
-    with pytest.raises(NotImplementedError):
-        check_routing_options(False, None, None, None, None, 2.5)
+    check_routing_options(False, None, None, None, None, 2.5)  # accepted (no effect on top-k)
+    with pytest.raises(ValueError):
+        check_routing_options(False, None, None, None, None, float("nan"))
     with pytest.raises(NotImplementedError):
         FusedMoE(4, 2, 8, 8, params_dtype=torch.float32, tp_size=1, quant_config=object())
 
