@@ -19,6 +19,8 @@ SMX_ERR_WORKSPACE = 1002
 SMX_ERR_MISALIGNED = 1003
 SMX_ERR_TIMEOUT = 1004
 SMX_ERR_NOT_FOUND = 1005
+SMX_ERR_SCRATCH = 1006
+SMX_NOALLOC_SCRATCH_BYTES = 32 << 20
 SMX_H2D_HIDDEN, SMX_H2D_KV_CACHE, SMX_H2D_DRAFT_KV_CACHE, SMX_H2D_WEIGHT = 1, 2, 3, 4
 
 # (name, restype, argtypes) of every exported entry point, in header order.
@@ -37,6 +39,9 @@ SIGNATURES = [
     ("smx_fused_moe_forward", ctypes.c_int,
      [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,
       _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),
+    ("smx_fused_moe_forward_noalloc", ctypes.c_int,
+     [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,
+      _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     ("smx_moe_shared_workspace_size", _sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
     ("smx_fused_moe_shared_forward", ctypes.c_int,
      [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,

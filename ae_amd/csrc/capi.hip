@@ -8,6 +8,14 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
+
+// Device-resident scratch of smx_fused_moe_forward_noalloc: the workspace of a call that may
+// not allocate. Each GPU the library runs on holds its own copy (allocated with the code object
+// when the library is first used on that device) until the process ends. Host code never passes
+// `scratch` itself to a kernel or a copy: in host code the name is a stand-in, not a device
+// address; the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) char scratch[SMX_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -447,6 +455,28 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   return SMX_OK;
 }
 
+// Per-device address of `scratch`, looked up with that device current on its first use.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return static_cast<int>(err);
+  if (dev < 0 || dev >= kMaxDevices) return SMX_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return static_cast<int>(err);
+    if (p == nullptr) return static_cast<int>(hipErrorInvalidSymbol);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SMX_OK;
+}
+
 int check_pool(const void* hidden, const void* out, const void* pool, int64_t num_slots,
                int64_t page_elems, const int64_t* e2s, int64_t H, int dtype, int64_t* I) {
   if (!hidden || !out || !pool || !e2s || num_slots <= 0 || page_elems <= 0) return SMX_ERR_INVALID_ARG;
@@ -474,6 +504,7 @@ const char* smx_error_string(int code) {
     case SMX_ERR_MISALIGNED: return "tensor base not 16-byte aligned";
     case SMX_ERR_TIMEOUT: return "timed out waiting for a transfer task";
     case SMX_ERR_NOT_FOUND: return "no such transfer task";
+    case SMX_ERR_SCRATCH: return "sizes need more workspace than the no-allocation scratch holds";
     default: return hipGetErrorString(static_cast<hipError_t>(code));
   }
 }
@@ -643,6 +674,30 @@ int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, i
   return fused_forward(hidden, out, dtype, T, H, router_logits, logits_dtype, E, top_k, renormalize,
                        pool, num_slots, page_elems, expert_to_slot, 0, BlockTerms{}, topk_weights_out,
                        topk_ids_out, workspace, workspace_bytes, stream);
+}
+
+int smx_fused_moe_forward_noalloc(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                                  const void* router_logits, int logits_dtype, int64_t E,
+                                  int64_t top_k, int renormalize, const void* pool,
+                                  int64_t num_slots, int64_t page_elems,
+                                  const int64_t* expert_to_slot, float* topk_weights_out,
+                                  int32_t* topk_ids_out, void* stream) {
+  if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype) ||
+      page_elems <= 0 || page_elems % (3 * H) != 0)
+    return SMX_ERR_INVALID_ARG;
+  if (T == 0) return SMX_OK;
+  const int64_t I = page_elems / (3 * H);
+  int rc = check_shape(T, H, I, E, top_k, dtype);
+  if (rc != SMX_OK) return rc;
+  // nothing in the workspace has to start at zero: every kernel writes what it later reads
+  const size_t need = workspace_for(T, H, I, E, top_k, dtype, 0, false);
+  if (need > SMX_NOALLOC_SCRATCH_BYTES) return SMX_ERR_SCRATCH;
+  void* ws = nullptr;
+  rc = scratch_of_current_device(&ws);
+  if (rc != SMX_OK) return rc;
+  return fused_forward(hidden, out, dtype, T, H, router_logits, logits_dtype, E, top_k, renormalize,
+                       pool, num_slots, page_elems, expert_to_slot, 0, BlockTerms{}, topk_weights_out,
+                       topk_ids_out, ws, SMX_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 size_t smx_moe_shared_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,

@@ -37,7 +37,9 @@ enum smx_status {
   SMX_ERR_WORKSPACE = 1002,       /* workspace smaller than smx_moe_workspace_size() */
   SMX_ERR_MISALIGNED = 1003,      /* a tensor base is not 16-byte aligned */
   SMX_ERR_TIMEOUT = 1004,         /* smx_h2d_wait: the task did not finish in time */
-  SMX_ERR_NOT_FOUND = 1005        /* smx_h2d_wait: no such task id (or it was cleared) */
+  SMX_ERR_NOT_FOUND = 1005,       /* smx_h2d_wait: no such task id (or it was cleared) */
+  SMX_ERR_SCRATCH = 1006          /* smx_fused_moe_forward_noalloc: sizes need more workspace
+                                     than SMX_NOALLOC_SCRATCH_BYTES */
 };
 
 /* Limits: 1 <= E <= 256; 1 <= top_k <= min(E, 16); H and I multiples of 128 for 16-bit
@@ -121,6 +123,28 @@ int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, i
                           const int64_t* expert_to_slot,
                           float* topk_weights_out, int32_t* topk_ids_out,
                           void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * smx_fused_moe_forward without a workspace: the call allocates nothing. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The intermediates live in a device-resident scratch array of the library,
+ * SMX_NOALLOC_SCRATCH_BYTES per GPU, which each GPU the library runs on holds from the
+ * library's load until the process ends. Calls whose smx_moe_workspace_size() exceeds it return
+ * SMX_ERR_SCRATCH before anything is launched (32 MiB holds every verify-step batch up to 128
+ * tokens of the Mixtral-8x7B, Qwen1.5-MoE and DeepSeek-V2-Lite layer shapes).
+ * Every call on one GPU shares that GPU's scratch and leaves its intermediates there: calls
+ * that overlap on one GPU (two streams, or two threads without ordering) race. Nothing in the
+ * scratch has to start at zero. Arguments and results otherwise as smx_fused_moe_forward, on the
+ * device current at the call.
+ */
+#define SMX_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int smx_fused_moe_forward_noalloc(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                                  const void* router_logits, int logits_dtype, int64_t E,
+                                  int64_t top_k, int renormalize,
+                                  const void* pool, int64_t num_slots, int64_t page_elems,
+                                  const int64_t* expert_to_slot,
+                                  float* topk_weights_out, int32_t* topk_ids_out, void* stream);
 
 /* Bytes of workspace smx_fused_moe_shared_forward needs (shared_I = 0: no shared expert). */
 size_t smx_moe_shared_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,

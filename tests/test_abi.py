@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 31, names
+    assert len(names) == 32, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -106,6 +106,28 @@ def test_forward_and_routing_reject_before_launch():
     assert L.smx_topk_softmax(A, 2, 4, 300, 2, 1, A, A, VP(0)) == _lib.SMX_ERR_UNSUPPORTED
     assert L.smx_moe_align_block_size(A, 10, 0, 16, A, A, A, VP(0)) == _lib.SMX_ERR_INVALID_ARG
     assert L.smx_moe_align_block_size(A, 20000, 8, 16, A, A, A, VP(0)) == _lib.SMX_ERR_UNSUPPORTED
+
+
+def test_noalloc_forward_rejects_before_touching_the_device():
+    """The no-allocation forward checks its arguments and its scratch bound before it looks up
+    the device's scratch (no GPU here), and names the scratch in its error."""
+    f = L.smx_fused_moe_forward_noalloc
+    args = [A, A, 2, 4, 256, A, 2, 4, 2, 1, A, 4, 3 * 256 * 256, A, VP(0), VP(0), VP(0)]
+    zero = list(args)
+    zero[3] = 0
+    assert f(*zero) == _lib.SMX_OK
+    bad = list(args)
+    bad[12] = 1000                                    # page not 3*I*H
+    assert f(*bad) == _lib.SMX_ERR_INVALID_ARG
+    bad = list(args)
+    bad[8] = 5                                        # top_k > E
+    assert f(*bad) == _lib.SMX_ERR_INVALID_ARG
+    # Mixtral shape: 128 tokens fit the 32 MiB scratch, 256 do not
+    big = [A, A, 2, 256, 4096, A, 2, 8, 2, 1, A, 8, 3 * 4096 * 14336, A, VP(0), VP(0), VP(0)]
+    assert L.smx_moe_workspace_size(128, 4096, 14336, 8, 2, 2) <= _lib.SMX_NOALLOC_SCRATCH_BYTES
+    assert L.smx_moe_workspace_size(256, 4096, 14336, 8, 2, 2) > _lib.SMX_NOALLOC_SCRATCH_BYTES
+    assert f(*big) == _lib.SMX_ERR_SCRATCH
+    assert b"scratch" in L.smx_error_string(_lib.SMX_ERR_SCRATCH)
 
 
 def test_profile_events_argument_checks():
