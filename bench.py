@@ -15,13 +15,21 @@ renormalisation. --layers N runs a stack of N layers with distinct weights per s
 (DeepSeek-V2-Lite has 26), --sweep-tokens runs one line per token count, --graph replays
 each step from a HIP graph.
 
+c1 is the reference's CPU-runnable configuration: hidden 1024, ffn 2816, 8 experts, top-2, fp32,
+32 tokens (4 sequences x 8 draft tokens), router logits x Wg^T with Wg ~ N(0, 0.02).
+
 Prints one JSON line per token count: value = algorithmic HBM bytes / measured time (GB/s),
 with us per step timed by HIP events around the K steps only; then the roofline of the
 dominant kernel (gate/up), timed in a second pass of K steps with HIP events that the
-library records on the launch stream around each kernel; and the CPU oracle timed on a
-bounded sample of the same workload.
+library records on the launch stream around each kernel; the parity of the layer call against
+the numpy oracle on the same inputs (ids, weight bits, both output error metrics); and the CPU
+baseline: a torch-CPU restatement of the same layer (GEMMs on MKL, weights converted to fp32
+once, outside the timing) on the host cores, median of >= 20 calls after 3 warm-up calls. The
+default Mixtral run also times 8, 16, 48 and 64 tokens (the rest of the metric's 8-64 range)
+with the same event-timed loop and reports them under "sweep".
 
-    python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu] [--no-parity]
+    python bench.py --workload c1
     python bench.py --workload dsv2lite --layers 26 --sweep-tokens 1,2,4,8,16,32,64,128 --no-cpu
 """
 from __future__ import annotations
@@ -38,6 +46,7 @@ import torch
 METRIC = "MoE layer us/verify-step + achieved HBM GB/s (% peak), Mixtral shape, 8-64 tokens"
 HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense bf16 matrix-core peak of one MI355X
+MFMA_FP32_PEAK_TFLOPS = 157.3   # dense fp32 matrix-core peak
 
 WORKLOADS = {
     "mixtral": dict(title="Mixtral-8x7B-shape MoE layer verify step", tokens=32, hidden=4096,
@@ -48,7 +57,13 @@ WORKLOADS = {
     "dsv2lite": dict(title="DeepSeek-V2-Lite-shape MoE block (2 shared experts) verify step",
                      tokens=32, hidden=2048, ffn=1408, experts=64, topk=6, shared_ffn=2816,
                      gated=False, renormalize=False),
+    "c1": dict(title="MoE layer H1024/I2816/E8/top-2 fp32 verify step (the reference's CPU-runnable "
+                     "configuration)", tokens=32, hidden=1024, ffn=2816, experts=8, topk=2,
+               shared_ffn=0, gated=False, renormalize=True, dtype="fp32"),
 }
+# The rest of the headline metric's 8-64 token range, timed beside the default Mixtral run.
+HEADLINE_SWEEP = (8, 16, 48, 64)
+DTYPES = {"bf16": (torch.bfloat16, 2, 2), "fp32": (torch.float32, 4, 0)}  # torch dtype, bytes, SMX code
 
 
 def parse():
@@ -72,11 +87,17 @@ def parse():
                          "unfused sequence (norm kernel, torch gate GEMM, MoE call)")
     ap.add_argument("--zipf", type=float, default=1.2,
                     help="Mixtral gate bias exponent (0 = unbiased)")
-    ap.add_argument("--rotate", type=int, default=2, help="copies of the weights rotated per step")
+    ap.add_argument("--rotate", type=int, default=None,
+                    help="copies of the weights rotated per step (default: enough copies for "
+                         ">= 1 GB of weights, at least 2)")
+    ap.add_argument("--dtype", choices=sorted(DTYPES), default=None,
+                    help="activation and weight dtype (default: the workload's, bf16 but c1 fp32)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-calls", type=int, default=12,
-                    help="CPU baseline sample: layer calls (the default is ~10 s of host work "
-                         "for the Mixtral layer at 32 tokens)")
+    ap.add_argument("--no-parity", action="store_true", help="skip the parity check against the oracle")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the 8/16/48/64-token lines of the default Mixtral run")
+    ap.add_argument("--cpu-runs", type=int, default=20,
+                    help="CPU baseline: timed layer calls (after 3 warm-up calls); the median is reported")
     ap.add_argument("--h2d", action="store_true",
                     help="measure host -> device streaming of expert pages through the transfer "
                          "engine (pinned host memory, chunked copies), alone and beside the MoE "
@@ -168,23 +189,28 @@ class Layer:
                 self.shared.append((torch.randn(3 * Is * H, generator=g, device=dev) * 0.02).to(dtype))
 
 
-def run_tokens(args, wl, T, layers, L, dev):
+def run_tokens(args, wl, T, layers, L, dev, light=False):
+    """Measure one token count. light: only the event-timed loop (the headline's sweep points);
+    otherwise also the per-kernel stage pass, the roofline, the parity check and the CPU
+    baseline. Returns the JSON object."""
     from ae_amd import _lib
     from ae_amd.layers._torch import ptr
 
     H, I, E, k, Is = args.hidden, args.ffn, args.experts, args.topk, wl["shared_ffn"]
-    dtype, es = torch.bfloat16, 2
+    dtype, es, dcode = DTYPES[args.dtype]
+    dname = "bf16" if args.dtype == "bf16" else "fp32"
     g = torch.Generator(device=dev).manual_seed(1000 + T)
     x = torch.randn((T, H), generator=g, device=dev).to(dtype)
-    if args.workload == "mixtral":
+    if args.workload in ("mixtral", "c1"):
         wg = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(dtype)
-        if args.zipf > 0:
+        if args.workload == "mixtral" and args.zipf > 0:
             p = torch.arange(1, E + 1, dtype=torch.float64) ** (-args.zipf)
             bias = torch.log(p / p.sum()).to(device=dev, dtype=dtype)
+            routing = f"zipf s={args.zipf}"
         else:
             bias = torch.zeros(E, dtype=dtype, device=dev)
+            routing = "gate N(0,0.02), unbiased"
         logits = torch.nn.functional.linear(x, wg) + bias
-        routing = f"zipf s={args.zipf}" if args.zipf > 0 else "unbiased"
     else:
         logits = (torch.randn((T, E), generator=g, device=dev) * 2.0).to(dtype)
         routing = "logits 2*N(0,1)"
@@ -193,9 +219,9 @@ def run_tokens(args, wl, T, layers, L, dev):
     w_out = torch.empty((T, k), dtype=torch.float32, device=dev)
     ids_out = torch.empty((T, k), dtype=torch.int32, device=dev)
     if Is:
-        nbytes = L.smx_moe_shared_workspace_size(T, H, I, E, k, Is, _lib.SMX_BF16)
+        nbytes = L.smx_moe_shared_workspace_size(T, H, I, E, k, Is, dcode)
     else:
-        nbytes = L.smx_moe_workspace_size(T, H, I, E, k, _lib.SMX_BF16)
+        nbytes = L.smx_moe_workspace_size(T, H, I, E, k, dcode)
     if nbytes == 0:
         raise SystemExit(f"unsupported shape T={T} H={H} I={I} E={E} k={k} shared={Is}")
     ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
@@ -205,14 +231,14 @@ def run_tokens(args, wl, T, layers, L, dev):
         norm_w = (1 + 0.1 * torch.randn(H, generator=g, device=dev)).to(dtype)
         gate_w = (torch.randn((E, H), generator=g, device=dev) * 0.02).to(dtype)
         sgate_w = (torch.randn(H, generator=g, device=dev) * 0.02).to(dtype) if wl["gated"] else None
-        lbytes = L.smx_moe_layer_workspace_size(T, H, I, E, k, Is, _lib.SMX_BF16)
+        lbytes = L.smx_moe_layer_workspace_size(T, H, I, E, k, Is, dcode)
         lws = torch.empty(lbytes, dtype=torch.uint8, device=dev)
 
     def call(layer, c, stream):
         if args.layer:
             sp = ctypes.c_void_p(stream.cuda_stream)
             rc = L.smx_moe_layer_forward(
-                ptr(x), ptr(residual), _lib.SMX_BF16, T, H, ptr(norm_w), 1e-5, ptr(gate_w), E, k,
+                ptr(x), ptr(residual), dcode, T, H, ptr(norm_w), 1e-5, ptr(gate_w), E, k,
                 renorm, ptr(layer.pools[c]), E, 3 * I * H, ptr(slots),
                 ptr(layer.shared[c] if Is else None), Is, ptr(sgate_w), 1.0, None, ptr(w_out),
                 ptr(ids_out), ptr(lws), lbytes, sp)
@@ -226,13 +252,13 @@ def run_tokens(args, wl, T, layers, L, dev):
         lg = logits if lg is None else lg
         if Is:
             rc = L.smx_fused_moe_shared_forward(
-                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(lg), _lib.SMX_BF16, E, k, renorm,
+                ptr(x), ptr(y), dcode, T, H, ptr(lg), dcode, E, k, renorm,
                 ptr(pool), E, 3 * I * H, ptr(slots), ptr(layer.shared[c]), Is, ptr(sgate), 1.0,
                 ptr(w_out), ptr(ids_out), ptr(ws), nbytes, sp)
             _lib.check("smx_fused_moe_shared_forward", rc)
         else:
             rc = L.smx_fused_moe_forward(
-                ptr(x), ptr(y), _lib.SMX_BF16, T, H, ptr(lg), _lib.SMX_BF16, E, k, renorm,
+                ptr(x), ptr(y), dcode, T, H, ptr(lg), dcode, E, k, renorm,
                 ptr(pool), E, 3 * I * H, ptr(slots), ptr(w_out), ptr(ids_out), ptr(ws), nbytes, sp)
             _lib.check("smx_fused_moe_forward", rc)
 
@@ -244,10 +270,13 @@ def run_tokens(args, wl, T, layers, L, dev):
         for layer in layers:
             call(layer, i % copies, s or stream)
 
-    # ---- routing facts for the algorithmic byte count (same logits for every layer)
+    # ---- routing facts for the algorithmic byte count (same logits for every layer); the
+    # outputs of this first call are the ones the parity check compares with the oracle
     call(layers[0], 0, stream)
     torch.cuda.synchronize()
+    y_first = (x if args.layer else y).clone()
     ids_np = ids_out.cpu().numpy()
+    w_first = w_out.cpu().numpy().copy()
     active = sorted(set(int(v) for v in ids_np.reshape(-1)))
     counts = [int((ids_np == e).sum()) for e in range(E)]
     weight_bytes = len(active) * 3 * H * I * es + 3 * H * Is * es
@@ -268,7 +297,8 @@ def run_tokens(args, wl, T, layers, L, dev):
     fd = L.smx_fused_down_max_tokens()
     units = T * (k * -(-I * es // 1024) + -(-Is * es // 1024))
     fused_down = not tiled and 1 <= T <= 8 and (T <= fd if fd >= 0 else units <= 48)
-    # and whether the routing runs inside the gate/up launch (small batches, logits in bf16)
+    # and whether the routing runs inside the gate/up launch (small batches, logits in the
+    # activation dtype)
     group = 8 if E <= 8 else 16 if E <= 16 else 32 if E <= 32 else 64
     on = bool(L.smx_routing_in_gateup())
     in_launch = on and not tiled and E <= 64 and (
@@ -318,6 +348,11 @@ def run_tokens(args, wl, T, layers, L, dev):
     wall = time.perf_counter() - wall0
     ms_step = t_start.elapsed_time(t_end) / args.steps
     us_step = 1000.0 * ms_step
+    value = step_bytes / (us_step * 1e-6) / 1e9
+    if light:
+        return {"us_per_step": round(us_step, 2), "gbs": round(value, 1),
+                "hbm_frac": round(value / HBM_PEAK_GBS, 4), "algorithmic_bytes": step_bytes,
+                "active_experts": len(active), "steps": args.steps}
 
     # ---- stage pass (eager, 1 layer): the same steps again with HIP events recorded by the
     # library on the launch stream before routing and after each kernel
@@ -355,7 +390,6 @@ def run_tokens(args, wl, T, layers, L, dev):
         u1.record(stream)
         torch.cuda.synchronize()
         unfused_us = 1000.0 * u0.elapsed_time(u1) / args.steps
-    value = step_bytes / (us_step * 1e-6) / 1e9
     config = {
         "workload": f"{wl['title']}, {T} tokens" + (f", {len(layers)} layers" if len(layers) > 1 else ""),
         "tokens": T, "hidden": H, "ffn": I, "experts": E, "top_k": k,
@@ -375,8 +409,9 @@ def run_tokens(args, wl, T, layers, L, dev):
         config["hip_graph"] = True
     if args.layer:
         config["layer_call"] = "residual add + RMSNorm + router gate + top-k + MoE"
+    headline = args.workload == "mixtral" and not args.layer and len(layers) == 1
     out = {
-        "metric": METRIC if args.workload == "mixtral" and not args.layer else
+        "metric": METRIC if headline else
         f"{'post-attention layer call (add+RMSNorm+gate+top-k+MoE)' if args.layer else 'MoE'} "
         f"{'stack' if len(layers) > 1 else 'layer'} us/verify-step + achieved HBM GB/s, {args.workload}",
         "value": round(value, 1),
@@ -388,9 +423,10 @@ def run_tokens(args, wl, T, layers, L, dev):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: N(0,0.02) expert weights, N(0,1) hidden states, "
-                + ("gate N(0,0.02) + Zipf bias" if args.workload == "mixtral" else "router logits 2*N(0,1)"),
+        "dtype": dname,
+        "data": f"synthetic: N(0,0.02) expert weights, N(0,1) hidden states, "
+                + ("gate N(0,0.02) + Zipf bias" if args.workload == "mixtral" and args.zipf > 0 else
+                   "gate N(0,0.02)" if args.workload in ("mixtral", "c1") else "router logits 2*N(0,1)"),
         "config": config,
         "us_per_step": round(us_step, 2),
         "layer_hbm_frac": round(value / HBM_PEAK_GBS, 4),
@@ -418,13 +454,14 @@ def run_tokens(args, wl, T, layers, L, dev):
                            "combine": 0.0 if fused_down else round(stage_us[3], 2)}
         if tiled:  # many tokens per expert: the matrix cores bound the tiled kernels
             tflops = gateup_flops / (stage_us[1] * 1e-6) / 1e12
+            peak = MFMA_BF16_PEAK_TFLOPS if dname == "bf16" else MFMA_FP32_PEAK_TFLOPS
             out["roofline"] = {
                 "kernel": "tile_gateup_kernel (W1/W3 x 128-token MFMA tiles + SiLU*up epilogue)",
                 "bound": "mfma",
                 "achieved": round(tflops, 1),
-                "peak": MFMA_BF16_PEAK_TFLOPS,
+                "peak": peak,
                 "unit": "TFLOP/s",
-                "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                "frac": round(tflops / peak, 4),
                 "traffic": None,
                 "algorithmic_flops": gateup_flops,
                 "hbm_gbs": round(gateup_bytes / (stage_us[1] * 1e-6) / 1e9, 1),
@@ -442,10 +479,15 @@ def run_tokens(args, wl, T, layers, L, dev):
                 "algorithmic_bytes": gateup_bytes,
                 "us_per_launch": round(stage_us[1], 2),
             }
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(args, wl, x, logits, sgate, layers[0], slots,
-                                           layer_bytes)
-    print(json.dumps(out), flush=True)
+    oracle_out = None
+    parity = not args.no_parity and len(layers) == 1 and not args.layer
+    if parity or not args.no_cpu:
+        host = _host_inputs(args, wl, x, logits, sgate, layers[0], slots)
+        if parity:
+            out["parity"], oracle_out = parity_check(args, host, y_first, w_first, ids_np)
+        if not args.no_cpu:
+            out["cpu_baseline"] = cpu_baseline(args, host, layer_bytes, T, oracle_out)
+    return out
 
 
 def main():
@@ -471,8 +513,13 @@ def main():
     for key in ("hidden", "ffn", "experts", "topk"):
         if getattr(args, key) is None:
             setattr(args, key, wl[key])
+    if args.dtype is None:
+        args.dtype = wl.get("dtype", "bf16")
     tokens = ([int(v) for v in args.sweep_tokens.split(",")] if args.sweep_tokens
               else [args.tokens if args.tokens is not None else wl["tokens"]])
+    # the default run is the headline: Mixtral at 32 tokens, plus the rest of the 8-64 range
+    headline_sweep = (args.workload == "mixtral" and not args.sweep_tokens and args.tokens is None
+                      and args.layers == 1 and not args.layer and not args.graph and not args.no_sweep)
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     L = _lib.lib()
@@ -482,11 +529,20 @@ def main():
         _lib.check("smx_set_fused_down_max_tokens",
                    L.smx_set_fused_down_max_tokens(args.fused_down_max_tokens))
     g = torch.Generator(device=dev).manual_seed(0)
+    es = DTYPES[args.dtype][1]
+    page_bytes = 3 * args.hidden * args.ffn * es
+    if args.rotate is None:  # enough copies that no step finds its weights in a cache
+        pool_bytes = args.experts * page_bytes + 3 * args.hidden * wl["shared_ffn"] * es
+        args.rotate = max(2, -(-(1 << 30) // pool_bytes))
     copies = args.rotate if args.layers == 1 else 1  # a stack of layers is its own rotation
     layers = [Layer(g, dev, args.hidden, args.ffn, args.experts, wl["shared_ffn"], copies,
-                    torch.bfloat16) for _ in range(args.layers)]
+                    DTYPES[args.dtype][0]) for _ in range(args.layers)]
     for T in tokens:
-        run_tokens(args, wl, T, layers, L, dev)
+        out = run_tokens(args, wl, T, layers, L, dev)
+        if headline_sweep:
+            out["sweep"] = {str(t): run_tokens(args, wl, t, layers, L, dev, light=True)
+                            for t in HEADLINE_SWEEP}
+        print(json.dumps(out), flush=True)
 
 
 PCIE_GEN5_X16_GBS = 64.0  # host link of one MI355X, per direction, before protocol overhead
@@ -618,57 +674,126 @@ def h2d_bench(args):
     print(json.dumps(out), flush=True)
 
 
-def cpu_baseline(args, wl, x, logits, sgate, layer, slots, layer_bytes):
-    """The numpy oracle on the host cores, on the same workload (one layer); a bounded sample
-    of --cpu-calls layer calls (inputs copied to host memory before timing)."""
+def _host_inputs(args, wl, x, logits, sgate, layer, slots):
+    """The layer's inputs on the host, as the oracle reads them (bf16 as bit patterns)."""
+    import numpy as np
+
+    def store(t):
+        t = t.detach().cpu().contiguous()
+        if t.dtype == torch.bfloat16:
+            return t.view(torch.int16).numpy().view(np.uint16)
+        return t.numpy()
+
+    return dict(x=store(x), logits=logits.float().cpu().numpy(), pool=store(layer.pools[0]),
+                slots=slots.cpu().numpy(), shared=store(layer.shared[0]) if layer.shared else None,
+                sgate=sgate.float().cpu().numpy().reshape(-1) if sgate is not None else None,
+                dtype="bf16" if args.dtype == "bf16" else "f32", k=args.topk,
+                renorm=wl["renormalize"])
+
+
+def parity_check(args, h, y_gpu, w_gpu, ids_gpu):
+    """The first layer call's outputs against the numpy oracle on the same inputs (same logit
+    bits): ids equal, weight bits equal, max |y - ref| / max |ref| and the elementwise
+    |y - ref| / max(|ref|, 1e-3 max |ref|). Returns (parity object, oracle output)."""
     import numpy as np
     from oracle import moe_ref as ref
 
-    def bits(t):
-        return t.cpu().view(torch.int16).numpy().view(np.uint16)
-
-    xb = bits(x)
-    lf = logits.float().cpu().numpy()
-    pb = bits(layer.pools[0])
-    sl = slots.cpu().numpy()
-    shared = bits(layer.shared[0]) if layer.shared else None
-    sg = sgate.float().cpu().numpy().reshape(-1) if sgate is not None else None
-    renorm = wl["renormalize"]
-
-    def run(n):
-        if shared is None:
-            return ref.fused_moe_forward(xb[:n], lf[:n], pb, sl, args.topk, renorm, ref.BF16)
-        return ref.fused_moe_shared_forward(xb[:n], lf[:n], pb, sl, args.topk, renorm, ref.BF16,
-                                            shared, None if sg is None else sg[:n])
-
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max(int(i["num_threads"]) for i in threadpool_info() if i.get("user_api") == "blas")
-    except Exception:
-        cores = len(os.sched_getaffinity(0))
-    run(1)  # warm BLAS
     t0 = time.perf_counter()
-    for _ in range(args.cpu_calls):
-        run(xb.shape[0])
-    dt = (time.perf_counter() - t0) / args.cpu_calls
-    cpu_model = ""
+    if h["shared"] is None:
+        y_ref, w_ref, ids_ref = ref.fused_moe_forward(h["x"], h["logits"], h["pool"], h["slots"],
+                                                      h["k"], h["renorm"], h["dtype"])
+    else:
+        y_ref, w_ref, ids_ref = ref.fused_moe_shared_forward(
+            h["x"], h["logits"], h["pool"], h["slots"], h["k"], h["renorm"], h["dtype"],
+            shared_page=h["shared"], shared_gate_logits=h["sgate"])
+    oracle_s = time.perf_counter() - t0
+    y = y_gpu.float().cpu().numpy().astype(np.float64)
+    want = y_ref.astype(np.float64)
+    floor = 1e-3 * max(float(np.abs(want).max()), 1e-30)
+    el = np.abs(y - want) / np.maximum(np.abs(want), floor)
+    tol = 1e-2 if args.dtype == "bf16" else 1e-4
+    max_rel = float(np.abs(y - want).max()) / max(float(np.abs(want).max()), 1e-30)
+    return {
+        "against": "numpy oracle (oracle/moe_ref.py) on the same inputs and logit bits",
+        "ids_equal": bool(np.array_equal(ids_gpu, ids_ref)),
+        "weight_bits_equal": bool(np.array_equal(np.ascontiguousarray(w_gpu, np.float32).view(np.uint32),
+                                                 np.ascontiguousarray(w_ref, np.float32).view(np.uint32))),
+        "max_rel_err": float(f"{max_rel:.3e}"),
+        "elem_rel_err_median": float(f"{np.median(el):.3e}"),
+        "elem_rel_err_p99": float(f"{np.quantile(el, 0.99):.3e}"),
+        "elem_rel_err_max": float(f"{el.max():.3e}"),
+        "tol_max_rel_err": tol,
+        "pass": bool(np.array_equal(ids_gpu, ids_ref)) and max_rel <= tol,
+        "oracle_s": round(oracle_s, 2),
+    }, y_ref
+
+
+def cpu_baseline(args, h, layer_bytes, T, oracle_y=None):
+    """The torch-CPU restatement of the layer (oracle/torch_cpu.py: GEMMs on MKL, the pool's
+    pages converted to fp32 once before timing) on the host cores: 3 warm-up calls, then the
+    median of --cpu-runs calls of the same workload (inputs already in host memory)."""
+    import numpy as np
+    from oracle.torch_cpu import TorchCpuMoE
+
+    affinity = len(os.sched_getaffinity(0))
+    threads = min(affinity, int(os.environ.get("OMP_NUM_THREADS", affinity)))
+    torch.set_num_threads(threads)
+    moe = TorchCpuMoE(h["pool"], h["slots"], args.hidden, h["dtype"], shared_page=h["shared"])
+    if h["dtype"] == "bf16":
+        xf = torch.from_numpy(h["x"].view(np.int16)).view(torch.bfloat16).float()
+    else:
+        xf = torch.from_numpy(h["x"]).float()
+    lf = torch.from_numpy(h["logits"])
+    sg = torch.from_numpy(h["sgate"]) if h["sgate"] is not None else None
+
+    def run():
+        return moe.forward(xf, lf, h["k"], h["renorm"], shared_gate=sg)
+
+    for _ in range(3):
+        y_cpu, _, _ = run()
+    times = []
+    for _ in range(args.cpu_runs):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    dt = float(np.median(times))
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break  # the first processor's block
+                key, _, val = line.partition(":")
+                info[key.strip()] = val.strip()
     except OSError:
         pass
-    return {
+    flags = set(info.get("flags", "").split())
+    cpu_model = (f"{info.get('model name', '?')} (family {info.get('cpu family', '?')}, model "
+                 f"{info.get('model', '?')}, stepping {info.get('stepping', '?')}, "
+                 f"{'AVX-512' if 'avx512f' in flags else 'AVX2' if 'avx2' in flags else 'no AVX2'})")
+    out = {
         "value": round(layer_bytes / dt / 1e9, 3),
         "unit": "GB/s",
-        "cores": cores,
+        "cores": threads,
         "kind": "port",
         "us_per_step": round(dt * 1e6, 1),
-        "sample": f"{args.cpu_calls} layer calls of the same workload through the numpy oracle "
-                  f"(fp32 OpenBLAS GEMMs on bf16-rounded values), {cores} threads, {cpu_model}",
+        "sample": f"median of {args.cpu_runs} calls (after 3 warm-up calls) of the same layer and "
+                  f"{T} tokens through a torch-CPU restatement of the layer "
+                  f"(oracle/torch_cpu.py: fp32 MKL GEMMs on "
+                  f"{'bf16-rounded values' if h['dtype'] == 'bf16' else 'fp32 values'}, weights "
+                  f"converted to fp32 before timing), {threads} threads",
+        "cpu_model": cpu_model,
+        "affinity_cpus": affinity,
+        "torch_threads": torch.get_num_threads(),
+        "blas": "MKL" if torch.backends.mkl.is_available() else "torch CPU BLAS",
+        "us_min": round(min(times) * 1e6, 1),
+        "us_max": round(max(times) * 1e6, 1),
     }
+    if oracle_y is not None:
+        want = oracle_y.astype(np.float64)
+        out["max_rel_err_vs_oracle"] = float(
+            f"{float(np.abs(y_cpu.numpy() - want).max()) / max(float(np.abs(want).max()), 1e-30):.3e}")
+    return out
 
 
 if __name__ == "__main__":
