@@ -75,6 +75,8 @@ SIGNATURES = [
     ("smx_fp32_gemm_outputs_fp16", _i32, []),
     ("smx_set_routing_in_gateup", ctypes.c_int, [_i32]),
     ("smx_routing_in_gateup", _i32, []),
+    ("smx_set_gateup_waves", ctypes.c_int, [_i32]),
+    ("smx_gateup_waves", _i32, []),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

@@ -54,6 +54,25 @@ int64_t g_rows_max_tokens = -1;
 bool g_fp32_f16out = false;
 // Small batches route inside the gate/up launch (smx_set_routing_in_gateup).
 bool g_route_in_gateup = true;
+// Waves per gate/up workgroup (smx_set_gateup_waves): 0 = the default rule (gateup_waves).
+int g_gateup_waves = 0;
+// The default rule: 4 waves per workgroup, unless that grid would leave part of the chip's
+// CUs without a workgroup (fewer workgroups than kGateupFillBlocks); then 2 or 1, whichever
+// first reaches it (more, smaller workgroups: each workgroup's stream is bound by its own
+// loads in flight, so a grid on a fraction of the CUs streams at that fraction of the rate).
+constexpr int64_t kGateupFillBlocks = 512;
+
+// tiles: 16-row weight tiles of one routed expert; s_tiles: of the shared expert (0: none);
+// items: routed work items expected; s_groups: the shared expert's token ranges.
+int gateup_waves(int64_t tiles, int64_t s_tiles, int64_t items, int64_t s_groups, int tok_tiles) {
+  if (tok_tiles > 2) return kExpertWaves;
+  if (g_gateup_waves > 0) return g_gateup_waves;
+  for (int w : {kExpertWaves, 2, 1}) {
+    const int64_t blocks = items * ((tiles + w - 1) / w) + s_groups * ((s_tiles + w - 1) / w);
+    if (blocks >= kGateupFillBlocks) return w;
+  }
+  return 1;
+}
 
 bool fused_down(int64_t T, int64_t H, int64_t I, int64_t k, int64_t Is, int dtype) {
   if (T < 1 || T > kRowsMaxTokens || H % 4 != 0) return false;
@@ -91,6 +110,7 @@ struct Plan {
   int splits = 1;
   int split_steps = 0;
   int down_rows = kDownRows;  // W2 row tiles per down wave
+  int gu_waves = kExpertWaves;  // waves per gate/up workgroup
   size_t hdr = 0, ranges = 0, sorted_f = 0, w = 0, ids = 0;
   size_t tmask = 0, fpos = 0, fslot = 0;
   size_t act = 0, part = 0, total = 0;
@@ -252,6 +272,9 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     }
     p.splits = static_cast<int>(s);
     p.split_steps = static_cast<int>(nchunks / s * kUnroll);
+    // every expert is one token range (T <= span) wherever fewer waves per workgroup apply
+    if (T <= p.span)
+      p.gu_waves = gateup_waves(I / kRowTile, Is / kRowTile, ex, (T + p.span - 1) / p.span, p.tok_tiles);
     if (Is > 0) {
       // its token ranges match the kernel's token-tile span
       const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
@@ -259,7 +282,7 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
       p.s_splits = static_cast<int>(ss);
       p.s_split_steps = static_cast<int>(schunks / ss * kUnroll);
       p.s_tok_groups = static_cast<int>((T + p.span - 1) / p.span);
-      p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + kExpertWaves - 1) / kExpertWaves));
+      p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + p.gu_waves - 1) / p.gu_waves));
       p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * p.down_rows) + kExpertWaves - 1) / kExpertWaves) * ss);
     }
   }
@@ -383,6 +406,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   a.splits = p.splits;
   a.split_steps = p.split_steps;
   a.down_rows = p.down_rows;
+  a.gu_waves = p.gu_waves;
   a.f16out = dtype == kF32 && g_fp32_f16out ? 1 : 0;
   if (p.Is > 0) {
     a.sh.page = bt.shared_page;
@@ -902,6 +926,14 @@ int smx_set_routing_in_gateup(int on) {
 }
 
 int smx_routing_in_gateup(void) { return g_route_in_gateup ? 1 : 0; }
+
+int smx_set_gateup_waves(int waves) {
+  if (waves != 0 && waves != 1 && waves != 2 && waves != 4) return SMX_ERR_INVALID_ARG;
+  g_gateup_waves = waves;
+  return SMX_OK;
+}
+
+int smx_gateup_waves(void) { return g_gateup_waves; }
 
 int smx_set_profile_events(void* const* events, int count) {
   if (events == nullptr || count == 0) {

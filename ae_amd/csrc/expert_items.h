@@ -96,9 +96,13 @@ struct WorkItem {
 // run the routing's work ranges (j = range, then tg). Returns false for a workgroup past the
 // ranges of this batch.
 // hdr and ranges: the routing's records (global memory, or a workgroup's own copy in LDS).
-template <typename S>
+// W: waves per workgroup (a workgroup covers W weight tiles of its item). The K-walk rotation
+// index is that of the 4-wave workgroup covering the same tiles (rot_items: workgroups per
+// item at 4 waves), so the accumulation order of every output does not depend on W.
+template <typename S, int W = kExpertWaves>
 __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
-                                          WorkItem& w, const int32_t* hdr, const RangeRec* ranges) {
+                                          int rot_items, WorkItem& w, const int32_t* hdr,
+                                          const RangeRec* ranges) {
   const int64_t elem = static_cast<int64_t>(sizeof(S));
   const int b = blockIdx.x;
   if (b < shared_blocks) {
@@ -110,7 +114,7 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
     w.off = v * span;
     w.m = min(span, a.T - w.off);
     w.tg = b - v * per_item;
-    w.rot = w.tg;
+    w.rot = w.tg * W / kExpertWaves;
     w.nr = 1;
     w.shared = true;
     return true;
@@ -153,10 +157,16 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
   w.page = static_cast<const char*>(a.pool) + slot * w.page_bytes;
   w.I = a.I;
   w.tg = g;
-  w.rot = (key + 1) * per_item + g;
+  w.rot = (key + 1) * rot_items + g * W / kExpertWaves;
   w.nr = nr;
   w.shared = false;
   return j < nranges;
+}
+
+template <typename S>
+__device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
+                                          WorkItem& w, const int32_t* hdr, const RangeRec* ranges) {
+  return work_item<S, kExpertWaves>(a, shared_blocks, per_item, per_item, w, hdr, ranges);
 }
 
 }  // namespace smx

@@ -19,6 +19,8 @@
 // (specmoe/layers/fused_moe_kernel.py:319-349): C1 rounded to the activation dtype (:203),
 // silu_and_mul (:337), the down GEMM scaled by the routing weight before rounding (:197-203),
 // and the fp32 top-k sum rounded once (:344-347).
+#include <type_traits>
+
 #include "expert_items.h"
 #include "topk_device.h"
 
@@ -69,38 +71,46 @@ __device__ __forceinline__ void load_raw(Raw<R>& c, const WeightStream& w, int c
           w.rsrc, w.lane_off, cbase + r * w.tile_stride + i * w.row4, CP);
 }
 
-// Token operand, shared by the workgroup. The 4 waves of a workgroup work on the same expert
-// and step through K together. Each chunk of the MT token tiles (16 token rows x 256 bytes
-// each) is loaded once per workgroup -- wave w loads rows 4w..4w+3 of every tile, one
-// 4-row x 256-byte instruction per tile -- into a double-buffered LDS tile with the same
-// padded layout as the weight tiles, and every wave reads its MFMA B fragments from there.
-// One barrier per chunk; every wave of a workgroup runs the same number of chunks.
-template <int MT>
+// Token operand, shared by the workgroup. The W waves of a workgroup (W = 4, 2 or 1) work on
+// the same expert and step through K together. Each chunk of the MT token tiles (16 token rows
+// x 256 bytes each) is loaded once per workgroup -- wave w loads the 4-row groups w, w + W, ...
+// of every tile, one 4-row x 256-byte instruction per group (4 / W per tile) -- into a
+// double-buffered LDS tile with the same padded layout as the weight tiles, and every wave reads
+// its MFMA B fragments from there. One barrier per chunk; every wave of a workgroup runs the
+// same number of chunks.
+template <int MT, int W>
 struct SharedTokens {
+  static constexpr int kGroups = 4 / W;  // 4-row groups per tile loaded by one wave
   __amdgpu_buffer_rsrc_t rsrc;
-  uint32_t base;     // byte offset of the K range (wave-uniform)
-  uint32_t off[MT];  // per lane: offset of row 4*wave + l/16 of tile j, + 16*(l%16)
+  uint32_t base;                 // byte offset of the K range (wave-uniform)
+  uint32_t off[MT][kGroups];     // per lane: offset of row 4*(wave + W*n) + l/16 of tile j, + 16*(l%16)
 };
 
-template <int MT>
+template <int MT, int W>
 struct RawTokens {
-  u32x4 v[MT];
+  u32x4 v[MT][4 / W];
 };
 
-template <int MT>
-__device__ __forceinline__ void load_tokens(RawTokens<MT>& rb, const SharedTokens<MT>& t, int chunk) {
+template <int MT, int W>
+__device__ __forceinline__ void load_tokens(RawTokens<MT, W>& rb, const SharedTokens<MT, W>& t, int chunk) {
   const uint32_t cbase = t.base + static_cast<uint32_t>(chunk) * (kStepBytes * kUnroll);
 #pragma unroll
-  for (int j = 0; j < MT; ++j) rb.v[j] = __builtin_amdgcn_raw_buffer_load_b128(t.rsrc, t.off[j], cbase, 0);
+  for (int j = 0; j < MT; ++j)
+#pragma unroll
+    for (int n = 0; n < 4 / W; ++n)
+      rb.v[j][n] = __builtin_amdgcn_raw_buffer_load_b128(t.rsrc, t.off[j][n], cbase, 0);
 }
 
-template <int MT>
-__device__ __forceinline__ void store_tokens(const RawTokens<MT>& rb, u32x4* bt) {
+template <int MT, int W>
+__device__ __forceinline__ void store_tokens(const RawTokens<MT, W>& rb, u32x4* bt) {
   const int lane = lane_id();
   const int wave = wave_id();
-  u32x4* wr = bt + kPitch * (4 * wave + (lane >> 4)) + (lane & 15);
 #pragma unroll
-  for (int j = 0; j < MT; ++j) wr[j * kTileSlots] = rb.v[j];
+  for (int n = 0; n < 4 / W; ++n) {
+    u32x4* wr = bt + kPitch * (4 * (wave + W * n) + (lane >> 4)) + (lane & 15);
+#pragma unroll
+    for (int j = 0; j < MT; ++j) wr[j * kTileSlots] = rb.v[j][n];
+  }
 }
 
 // One step of the workgroup's two-deep pipeline, for chunk c. On entry this chunk's weights
@@ -112,11 +122,11 @@ __device__ __forceinline__ void store_tokens(const RawTokens<MT>& rb, u32x4* bt)
 // chunks of weights stay in flight while this one is multiplied. Then chunk c+1's token rows,
 // issued a step ago, are published into `bt_next`; barrier. Token loads are issued before
 // weight loads, so waiting for a token chunk never waits for the weights issued with it.
-template <int CP, int DT, int R, int MT, bool kIssue, bool kNext>
-__device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT>& tnext,
-                                        RawTokens<MT>& tfree, u32x4* lds, const u32x4* bt,
+template <int CP, int DT, int R, int MT, int W, bool kIssue, bool kNext>
+__device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT, W>& tnext,
+                                        RawTokens<MT, W>& tfree, u32x4* lds, const u32x4* bt,
                                         u32x4* bt_next, const WeightStream& w,
-                                        const SharedTokens<MT>& t, int issue_chunk,
+                                        const SharedTokens<MT, W>& t, int issue_chunk,
                                         f32x4 (&acc)[R][MT]) {
   const int lane = lane_id();
   u32x4* wr = lds + kPitch * (lane >> 4) + (lane & 15);
@@ -163,11 +173,11 @@ __device__ __forceinline__ void issue_weights(Raw<R>& a, Raw<R>& b, const Weight
 // acc[r][mt] += A_r (16 rows x nchunks*256 bytes) . B_mt, the workgroup streaming the token
 // chunks through `bsh` (two buffers of MT tiles) while each wave streams its own weights;
 // chunks 0 and 1 of the weights are already in flight in `a` and `b` (issue_weights).
-template <int CP, int DT, int R, int MT>
-__device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTokens<MT>& t,
+template <int CP, int DT, int R, int MT, int W>
+__device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTokens<MT, W>& t,
                                           const ChunkOrder& ord, u32x4* lds, u32x4* bsh,
                                           f32x4 (&acc)[R][MT], Raw<R>& a, Raw<R>& b) {
-  RawTokens<MT> t0, t1;
+  RawTokens<MT, W> t0, t1;
   u32x4* b0 = bsh;
   u32x4* b1 = bsh + MT * kTileSlots;
   const int nchunks = ord.n;
@@ -177,19 +187,19 @@ __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTok
   wg_barrier();
   int c = 0;
   for (; c + 3 < nchunks; c += 2) {
-    wg_step<CP, DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
-    wg_step<CP, DT, R, MT, true, true>(b, t0, t1, lds, b1, b0, w, t, ord.at(c + 3), acc);
+    wg_step<CP, DT, R, MT, W, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
+    wg_step<CP, DT, R, MT, W, true, true>(b, t0, t1, lds, b1, b0, w, t, ord.at(c + 3), acc);
   }
   const int rem = nchunks - c;  // 1, 2 or 3 chunks left
   if (rem == 3) {
-    wg_step<CP, DT, R, MT, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
-    wg_step<CP, DT, R, MT, false, true>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
-    wg_step<CP, DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
+    wg_step<CP, DT, R, MT, W, false, true>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
   } else if (rem == 2) {
-    wg_step<CP, DT, R, MT, false, true>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
-    wg_step<CP, DT, R, MT, false, false>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, false, true>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, false, false>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
   } else {
-    wg_step<CP, DT, R, MT, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
   }
 }
 
@@ -197,7 +207,7 @@ __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTok
 // weight-row tile p (gate rows [16p, 16p+16) and the matching up rows); `owner` is false for
 // a wave past the expert's last tile (it streams tile p again and stores nothing).
 // `sorted`: the routing's sorted flat assignments (global memory, or the workgroup's LDS copy).
-template <int CP, int DT, int MT>
+template <int CP, int DT, int MT, int W>
 __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkItem& it, int p,
                                               bool owner, u32x4* lds, u32x4* bsh,
                                               const int32_t* sorted) {
@@ -219,21 +229,23 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<2> wa, wb;
     issue_weights<CP>(wa, wb, ws, ord);
-    SharedTokens<MT> tb;
+    SharedTokens<MT, W> tb;
     tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
     tb.base = 0;
 #pragma unroll
-    for (int j = 0; j < MT; ++j) {
-      const int q = min(q0 + j * kTokTile + 4 * wave + (lane >> 4), m - 1);
-      const int tok = it.shared ? off + q : sorted[off + q] / a.k;
-      tb.off[j] = static_cast<uint32_t>(tok * row_bytes + (lane & 15) * 16);
-    }
+    for (int j = 0; j < MT; ++j)
+#pragma unroll
+      for (int n = 0; n < 4 / W; ++n) {
+        const int q = min(q0 + j * kTokTile + 4 * (wave + W * n) + (lane >> 4), m - 1);
+        const int tok = it.shared ? off + q : sorted[off + q] / a.k;
+        tb.off[j][n] = static_cast<uint32_t>(tok * row_bytes + (lane & 15) * 16);
+      }
     f32x4 acc[2][MT];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<CP, DT, 2, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
+    stream_wg<CP, DT, 2, MT, W>(ws, tb, ord, lds, bsh, acc, wa, wb);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -251,19 +263,19 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   }
 }
 
-// Workgroup = (work item, 4 consecutive weight tiles): wave w owns tile 4*tg + w. A wave
+// Workgroup = (work item, W consecutive weight tiles): wave w owns tile W*tg + w. A wave
 // past the expert's last tile streams the last tile again and stores nothing, so every
 // wave of a workgroup runs the same chunks and barriers. The token tiles per pass follow
 // the item's token count (up to MT): an expert with few tokens streams its weights with
 // one tile of 16 tokens.
-template <int CP, int DT, int MT>
+template <int CP, int DT, int MT, int W>
 __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem& it, int p,
                                             bool owner, u32x4* lds, u32x4* bsh,
                                             const int32_t* sorted) {
-  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1>(a, it, p, owner, lds, bsh, sorted);
-  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1)>(a, it, p, owner, lds, bsh, sorted);
-  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1)>(a, it, p, owner, lds, bsh, sorted);
-  else gateup_passes<CP, DT, MT>(a, it, p, owner, lds, bsh, sorted);
+  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1, W>(a, it, p, owner, lds, bsh, sorted);
+  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1), W>(a, it, p, owner, lds, bsh, sorted);
+  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1), W>(a, it, p, owner, lds, bsh, sorted);
+  else gateup_passes<CP, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
 }
 
 // kMulti: the launch may hold experts split into several token ranges (T > span). Their
@@ -278,13 +290,13 @@ __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem&
 // workgroup's 4 waves run the top-k (RG lanes per token; or load caller ids), then wave 0 sorts
 // the assignments (sort_wave) into the workgroup's LDS; the first routed workgroup also
 // writes the records and top-k results, and its threads the token mask.
-template <bool kMulti, int DT, int MT, int RG, bool RM = false>
-__global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a) {
+template <bool kMulti, int DT, int MT, int RG, bool RM = false, int W = kExpertWaves>
+__global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
   const int wave = wave_id();
   const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
   const int Iw = in_shared ? a.sh.I : a.I;
   const int tiles = Iw / kRowTile;
-  const int groups = (tiles + kExpertWaves - 1) / kExpertWaves;
+  const int groups = (tiles + W - 1) / W;
   const int32_t* hdr = a.rb.hdr;
   const RangeRec* ranges = a.rb.ranges;
   const int32_t* sorted = a.rb.sorted_f;
@@ -295,7 +307,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
     __shared__ RangeRec rr_l[kSortRangesMax];
     __shared__ int32_t sf_l[kSortWaveMax];
     __shared__ int32_t hdr_l[2];
-    __shared__ RankScratch rs_all[kExpertWaves];
+    __shared__ RankScratch rs_all[W];
     if (!in_shared) {
       const int lane = lane_id();
       const int tid = threadIdx.x;
@@ -305,7 +317,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
       const int64_t my_slot = tid < E ? a.e2s[tid] : -1;
       if (a.rt.logits != nullptr) {
         constexpr int TPW = TopkGroup<RG, 1>::kTokens;
-        const int stride = kExpertWaves * TPW;
+        const int stride = W * TPW;
         for (int t0 = wave * TPW + lane / RG; t0 - lane / RG < a.T; t0 += stride * kTokBatch) {
           topk_batch<DT, RG, 1>(a.rt.logits, a.T, E, a.k, a.rt.renorm != 0, t0, stride, rs_all[wave],
                                 [&](int t, int slot, float wv, int id) {
@@ -318,7 +330,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
           });
         }
       } else {
-        for (int f = tid; f < N; f += kExpertThreads) {
+        for (int f = tid; f < N; f += W * kWave) {
           const int x = a.rt.ids_in[f];
           ids_l[f] = static_cast<int16_t>((x >= 0 && x < E) ? x : -2);
         }
@@ -326,7 +338,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
       if (tid < kWave) slot_l[tid] = (my_slot >= 0 && my_slot < a.rt.num_slots) ? my_slot : -1;
       __syncthreads();
       if (writer) {
-        for (int t = tid; t < a.T; t += kExpertThreads) {
+        for (int t = tid; t < a.T; t += W * kWave) {
           uint32_t m = 0;
           for (int j = 0; j < a.k; ++j) {
             const int e = ids_l[t * a.k + j];
@@ -386,15 +398,16 @@ __global__ __launch_bounds__(kExpertThreads, 2) void gateup_kernel(ExpertArgs a)
     }
   }
   WorkItem it;
-  if (!work_item<typename Elem<DT>::S>(a, a.sh.gateup_blocks, groups, it, hdr, ranges)) return;
-  const int praw = it.tg * kExpertWaves + wave;
+  const int groups4 = (tiles + kExpertWaves - 1) / kExpertWaves;
+  if (!work_item<typename Elem<DT>::S, W>(a, a.sh.gateup_blocks, groups, groups4, it, hdr, ranges)) return;
+  const int praw = it.tg * W + wave;
   const bool owner = praw < tiles;
   const int p = owner ? praw : tiles - 1;
-  __shared__ u32x4 lds_all[kExpertWaves][2 * kTileSlots];
+  __shared__ u32x4 lds_all[W][2 * kTileSlots];
   __shared__ u32x4 bsh[2 * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
-  if (kMulti && it.nr > 1) gateup_item<0, DT, MT>(a, it, p, owner, lds, bsh, sorted);
-  else gateup_item<kNonTemporal, DT, MT>(a, it, p, owner, lds, bsh, sorted);
+  if (kMulti && it.nr > 1) gateup_item<0, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
+  else gateup_item<kNonTemporal, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
 }
 
 // The token passes of one down workgroup with MT token tiles per pass: wave `wave` owns W2
@@ -423,20 +436,20 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<R> wa, wb;
     issue_weights<CP>(wa, wb, ws, ord);
-    SharedTokens<MT> tb;
+    SharedTokens<MT, kExpertWaves> tb;
     tb.rsrc = make_rsrc(act, static_cast<uint32_t>(static_cast<int64_t>(rows) * row_bytes));
     tb.base = static_cast<uint32_t>(k0_bytes);
 #pragma unroll
     for (int j = 0; j < MT; ++j) {
       const int q = min(q0 + j * kTokTile + 4 * wave + (lane >> 4), m - 1);
-      tb.off[j] = static_cast<uint32_t>((off + q) * row_bytes + (lane & 15) * 16);
+      tb.off[j][0] = static_cast<uint32_t>((off + q) * row_bytes + (lane & 15) * 16);
     }
     f32x4 acc[R][MT];
 #pragma unroll
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<CP, DT, R, MT>(ws, tb, ord, lds, bsh, acc, wa, wb);
+    stream_wg<CP, DT, R, MT, kExpertWaves>(ws, tb, ord, lds, bsh, acc, wa, wb);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -871,12 +884,27 @@ hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Gate/up launch of W waves per workgroup (fewer waves only for batches of at most two
+// token tiles with every expert one token range: the grids that can leave CUs idle).
+template <bool kMulti, int DT, int MT, int RG, bool RM>
+static void launch_gateup_w(const ExpertArgs& a, int max_ranges, hipStream_t s) {
+  auto go = [&](auto wc) {
+    constexpr int W = decltype(wc)::value;
+    const int64_t groups = (a.I / kRowTile + W - 1) / W;
+    const unsigned blocks = static_cast<unsigned>(a.sh.gateup_blocks + max_ranges * groups);
+    gateup_kernel<kMulti, DT, MT, RG, RM, W><<<blocks, W * kWave, 0, s>>>(a);
+  };
+  if constexpr (!kMulti && MT <= 2) {
+    if (a.gu_waves == 1) return go(std::integral_constant<int, 1>{});
+    if (a.gu_waves == 2) return go(std::integral_constant<int, 2>{});
+  }
+  go(std::integral_constant<int, kExpertWaves>{});
+}
+
 template <bool kMulti, int DT, int MT>
 static void launch_stage_m(int stage, const ExpertArgs& a, int max_ranges, hipStream_t s) {
   if (stage == 0) {
-    const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
-    const int64_t blocks = a.sh.gateup_blocks + max_ranges * groups;
-    gateup_kernel<kMulti, DT, MT, 0><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
+    launch_gateup_w<kMulti, DT, MT, 0, false>(a, max_ranges, s);
   } else {
     const int R = a.down_rows == 1 ? 1 : kDownRows;
     const int64_t groups = (a.H / (kRowTile * R) + kExpertWaves - 1) / kExpertWaves;
@@ -916,13 +944,11 @@ static hipError_t launch_stage(int stage, int dtype, const ExpertArgs& a, int ma
 
 template <int DT, int MT, bool RM>
 static void launch_gateup_routed(const ExpertArgs& a, int max_ranges, int route_g, hipStream_t s) {
-  const int64_t groups = (a.I / kRowTile + kExpertWaves - 1) / kExpertWaves;
-  const unsigned blocks = static_cast<unsigned>(a.sh.gateup_blocks + max_ranges * groups);
   switch (route_g) {
-    case 8: gateup_kernel<false, DT, MT, 8, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
-    case 16: gateup_kernel<false, DT, MT, 16, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
-    case 32: gateup_kernel<false, DT, MT, 32, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
-    default: gateup_kernel<false, DT, MT, 64, RM><<<blocks, kExpertThreads, 0, s>>>(a); break;
+    case 8: launch_gateup_w<false, DT, MT, 8, RM>(a, max_ranges, s); break;
+    case 16: launch_gateup_w<false, DT, MT, 16, RM>(a, max_ranges, s); break;
+    case 32: launch_gateup_w<false, DT, MT, 32, RM>(a, max_ranges, s); break;
+    default: launch_gateup_w<false, DT, MT, 64, RM>(a, max_ranges, s); break;
   }
 }
 

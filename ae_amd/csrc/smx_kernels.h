@@ -114,6 +114,9 @@ struct ExpertArgs {
   int split_steps;      // load steps per split
   int f16out;           // fp32 runs: routed gate/up outputs rounded to fp16 (reference stores)
   int down_rows;        // W2 row tiles per down wave: kDownRows, or 1
+  int gu_waves;         // waves per gate/up workgroup: kExpertWaves, or 2 or 1 (more, smaller
+                        // workgroups for grids that would leave CUs idle); sh.gateup_blocks and
+                        // the launch's grid follow it
   InRoute rt;           // used by the gate/up launch with routing inside (route_g > 0)
   SharedArgs sh;
 };

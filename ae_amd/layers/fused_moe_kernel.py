@@ -122,6 +122,26 @@ def routing_in_gateup(on: bool) -> Iterator[None]:
         set_routing_in_gateup(prev)
 
 
+def set_gateup_waves(waves: Optional[int]) -> Optional[int]:
+    """Set the waves per workgroup of the weight-streaming gate/up kernel (4, 2 or 1; None: the
+    library's rule, which uses fewer waves -- a larger grid of smaller workgroups -- when four
+    would leave CUs without work). Outputs do not depend on it. Returns the previous setting
+    (None for the rule). Process-wide."""
+    prev = int(_lib.lib().smx_gateup_waves())
+    _lib.call("smx_set_gateup_waves", 0 if waves is None else int(waves))
+    return None if prev == 0 else prev
+
+
+@contextlib.contextmanager
+def gateup_waves(waves: Optional[int]) -> Iterator[None]:
+    """Scope a set_gateup_waves setting (restored on exit)."""
+    prev = set_gateup_waves(waves)
+    try:
+        yield
+    finally:
+        set_gateup_waves(prev)
+
+
 def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:
     H = hidden_states.shape[1]
     _, page_size = w1.shape

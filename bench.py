@@ -109,6 +109,9 @@ def parse():
     ap.add_argument("--fused-down-max-tokens", type=int, default=None,
                     help="largest batch whose down projection and combine run as one kernel "
                          "(0 = never; default: the library's)")
+    ap.add_argument("--gateup-waves", type=int, default=None, choices=[0, 1, 2, 4],
+                    help="waves per workgroup of the weight-streaming gate/up kernel (0 = the "
+                         "library's rule)")
     ap.add_argument("--library-gemm", action="store_true",
                     help="only time torch.matmul (the ROCm library GEMM) on one expert's dense "
                          "gate/up and down shapes, the practical reference for the tiled kernels")
@@ -528,6 +531,8 @@ def main():
     if args.fused_down_max_tokens is not None:
         _lib.check("smx_set_fused_down_max_tokens",
                    L.smx_set_fused_down_max_tokens(args.fused_down_max_tokens))
+    if args.gateup_waves is not None:
+        _lib.check("smx_set_gateup_waves", L.smx_set_gateup_waves(args.gateup_waves))
     g = torch.Generator(device=dev).manual_seed(0)
     es = DTYPES[args.dtype][1]
     page_bytes = 3 * args.hidden * args.ffn * es

@@ -327,6 +327,19 @@ int smx_set_routing_in_gateup(int on);
 int smx_routing_in_gateup(void);
 
 /*
+ * Waves per workgroup of the weight-streaming gate/up kernel: 4, 2 or 1 (the kernel's work is
+ * the same -- one wave per 16 intermediate rows of an expert; only the grouping of waves into
+ * workgroups, and with it the grid, changes), or 0 (the default rule): 4, unless that grid
+ * would hold fewer than 512 workgroups (two per CU), then 2 or 1, whichever first reaches 512.
+ * Applies to batches of at most 32 tokens; larger ones always use 4. Outputs are identical
+ * for every setting (same per-wave K walk and rounding). Process-wide, like
+ * smx_set_tiled_min_tokens. Part of the expert-kernel configuration that replaces the
+ * reference's per-call Triton tile choice (specmoe/layers/fused_moe_kernel.py:293-306).
+ */
+int smx_set_gateup_waves(int waves);
+int smx_gateup_waves(void);
+
+/*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
  * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
  * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and

@@ -1,0 +1,104 @@
+"""Waves per gate/up workgroup (4, 2, 1): the grid changes, the per-wave work and K walk do
+not, so every setting gives the same bits -- routing from logits inside the gate/up launch or
+from the routing kernels, caller ids, shared-expert blocks -- and matches the oracle, through
+the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_ref as ref
+from ae_amd.layers import (fused_moe_forward, fused_moe_shared_forward, gateup_waves,
+                           routing_in_gateup, stack_fused_moe)
+from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, parity, to_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _inputs(T, H, E, dtype, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dtype)
+    logits = (torch.randn((T, E), generator=g, device=DEV) * 2.0).to(dtype)
+    return x, logits
+
+
+def _each_waves(fn):
+    outs = {}
+    for w in (4, 2, 1, None):
+        with gateup_waves(w):
+            outs[w] = fn()
+        torch.cuda.synchronize()
+    return outs
+
+
+def _assert_same(outs):
+    base = outs[4]
+    for w, o in outs.items():
+        for a, b in zip(base, o):
+            assert torch.equal(a, b), f"gate/up waves {w} differ from 4"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("in_launch", [True, False])
+@pytest.mark.parametrize("T,H,I,E,k,P", [
+    (1, 256, 128, 8, 2, 8),
+    (1, 256, 384, 64, 6, 64),      # 24 weight tiles per expert over 64 experts
+    (3, 128, 256, 64, 6, 70),      # some slots unmapped
+    (16, 256, 128, 8, 2, 8),       # one token tile
+    (32, 256, 256, 8, 2, 12),      # two token tiles
+])
+def test_fused_forward_same_bits_every_waves(dtype, in_launch, T, H, I, E, k, P):
+    x, logits = _inputs(T, H, E, dtype, seed=T * 5 + I)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E + k + I)
+    if P > E:
+        slots[1] = P + 5  # an expert outside the pool: its assignments are dropped
+    with routing_in_gateup(in_launch):
+        outs = _each_waves(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True,
+                                                     inplace=False, return_routing=True))
+    _assert_same(outs)
+    y, w, ids = outs[1]
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, TORCH_TO_ORACLE[dtype])
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    parity(f32_of(y), y_ref, TOL[dtype], case=f"gate/up waves 1 T={T} I={I} E={E}")
+
+
+@pytest.mark.parametrize("T", [1, 2, 5])
+def test_shared_block_same_bits_every_waves(T):
+    """DeepSeek-V2-Lite-like block (64 experts, top-6, no renormalisation, a shared expert of
+    twice the routed ffn, routed scaling 2.5) at small shapes: the shared expert's workgroups
+    follow the waves setting too."""
+    H, I, E, k, Is = 256, 128, 64, 6, 384
+    dtype = torch.bfloat16
+    x, logits = _inputs(T, H, E, dtype, seed=40 + T)
+    pool, slots = make_pool(E, H, I, dtype, seed=41)
+    g = torch.Generator(device=DEV).manual_seed(42)
+    page = (torch.randn(3 * Is * H, generator=g, device=DEV) * 0.02).to(dtype)
+    outs = _each_waves(lambda: fused_moe_shared_forward(
+        x.clone(), logits, pool, slots, k, False, page, None, 2.5, inplace=False,
+        return_routing=True))
+    _assert_same(outs)
+    y = outs[1][0]
+    y_ref, _, _ = ref.fused_moe_shared_forward(
+        to_oracle(x), f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, False,
+        TORCH_TO_ORACLE[dtype], shared_page=to_oracle(page), shared_gate_logits=None,
+        routed_scaling_factor=2.5)
+    parity(f32_of(y), y_ref, TOL[dtype], case=f"shared block gate/up waves 1 T={T}")
+
+
+def test_caller_ids_same_bits_every_waves():
+    """stack_fused_moe with caller ids, one of them repeated within a token."""
+    T, H, I, E, k = 4, 256, 128, 16, 4
+    dtype = torch.bfloat16
+    x, logits = _inputs(T, H, E, dtype, seed=77)
+    pool, slots = make_pool(E, H, I, dtype, seed=78)
+    g = torch.Generator(device=DEV).manual_seed(79)
+    ids = torch.randint(0, E, (T, k), generator=g, device=DEV, dtype=torch.int32)
+    ids[2, 1] = ids[2, 0]
+    w = torch.rand((T, k), generator=g, device=DEV, dtype=torch.float32)
+    outs = _each_waves(lambda: (stack_fused_moe(x.clone(), pool, slots, logits, w, ids, False),))
+    _assert_same(outs)
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
+    parity(f32_of(outs[1][0]), y_ref, TOL[dtype], case="caller ids gate/up waves 1")
