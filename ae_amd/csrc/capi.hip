@@ -58,9 +58,11 @@ bool g_route_in_gateup = true;
 int g_gateup_waves = 0;
 // The default rule: 4 waves per workgroup, unless that grid would leave part of the chip's
 // CUs without a workgroup (fewer workgroups than kGateupFillBlocks); then 2 or 1, whichever
-// first reaches it (more, smaller workgroups: each workgroup's stream is bound by its own
-// loads in flight, so a grid on a fraction of the CUs streams at that fraction of the rate).
-constexpr int64_t kGateupFillBlocks = 512;
+// first reaches it. Measured, us per layer, 4 / 2 / 1 waves (same box): DeepSeek-V2-Lite 2
+// tokens (286 workgroups at 4) 51.8 / 48.1 / 50.0, 1 token (176) 31.1 / 31.9 / 31.8, 4 tokens
+// (506) 73.3 / 73.9 / 82.6; Qwen1.5-MoE 1 token (176) 31.2 / 30.3 / 30.5; Mixtral 1 token
+// (448) 113.5 / 118.7 / 114.1.
+constexpr int64_t kGateupFillBlocks = 320;
 
 // tiles: 16-row weight tiles of one routed expert; s_tiles: of the shared expert (0: none);
 // items: routed work items expected; s_groups: the shared expert's token ranges.

@@ -747,13 +747,13 @@ __device__ __forceinline__ u32x4 load16(uint64_t addr) {
     return *reinterpret_cast<GlobalU32x4>(addr);
 }
 
-template <int DT, int CP>
+// PRE: a shared expert whose rows have more than kRowsDepth units (the host's choice).
+template <int DT, int CP, bool PRE>
 __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs a) {
   using S = typename Elem<DT>::S;
   __shared__ RowTerm terms[kRowsMaxTerms];
   __shared__ int fpos_l[kRowsMaxAssign];
   __shared__ float w_l[kRowsMaxAssign];
-  __shared__ float z_l[kRowsMaxTokens];
   __shared__ float vals[kRowsWaves][kRowsMaxTerms];
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -764,17 +764,67 @@ __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs 
   const int units = (rowb + kRowsUnit - 1) / kRowsUnit;
   const bool shared = a.page_s != nullptr;
   const bool gated = a.block && shared && a.sgate != nullptr;
-  // Term table: routed assignment f becomes term fpos[f]. The loads are independent of one
-  // another (one latency).
+  const int Ts = shared ? a.T : 0;  // shared-expert terms 0..T-1, then the routed terms
+  const int rowb_s = a.Is * static_cast<int>(sizeof(S));
+  const int units_s = (rowb_s + kRowsUnit - 1) / kRowsUnit;
+  RowCursor ic;  // issue cursor
+  u32x4 wr[kRowsDepth], ar[kRowsDepth];
+  int nterms = Ts;
+  // Issue the cursor's unit into ring slot d and advance; past the last unit the cursor
+  // stays on it (reloads in bounds, never consumed).
+  auto issue = [&](int d) {
+    const int o = ic.u * kRowsUnit + lane * 16;
+    const int oc = o < ic.rowb ? o : ic.rowb - 16;
+    wr[d] = load16<CP>(ic.w + static_cast<uint64_t>(oc));
+    ar[d] = load16<0>(ic.a + static_cast<uint64_t>(oc));
+    if (++ic.u == ic.units) {
+      if (ic.tau + 1 < nterms) row_cursor_at(ic, terms, ic.tau + 1, h);
+      else ic.u = ic.units - 1;
+    }
+  };
+  // Term table: the shared expert's row for token t is term t; routed assignment f becomes
+  // term Ts + fpos[f]. Its loads are independent of one another (one latency) and are issued
+  // first, by every lane (from clamped, in-bounds indices, N >= 1) so that no branch hides
+  // their count: loads complete in issue order, and the table is then waited for without
+  // waiting for the weight loads issued after it.
+  const int fi = tid < N ? tid : N - 1;
+  const int tt = fi / a.k;
+  const int jt = fi - tt * a.k;
+  const uint32_t m = static_cast<uint32_t>(a.tmask[tt]);
+  const int pos = a.fpos[fi];
+  const int64_t slot = a.fslot[fi];
+  const float wt = a.w[fi];
+  // lane t's shared-expert gate logit (used by lane t at the end). Its load converts under a
+  // dtype branch, which waits for it at once: issued here, that wait covers only the table.
+  const float zt = gated ? load_scalar(a.sgate, a.sgate_dtype, lane < a.T ? lane : a.T - 1) : 0.0f;
   int routed = 0;
+  __builtin_amdgcn_sched_barrier(0);
+  // PRE: the shared expert's rows need no routing record, so the first kRowsDepth units of
+  // token 0's shared term (which has more units than that: the cursor stays inside it, and no
+  // table entry is needed) are issued before the table is used; its latency overlaps them.
+  if constexpr (PRE) {
+    ic.tau = 0;
+    ic.u = 0;
+    ic.rowb = rowb_s;
+    ic.units = units_s;
+    ic.w = reinterpret_cast<uint64_t>(a.page_s) +
+           (2ull * static_cast<uint64_t>(a.H) + static_cast<uint64_t>(h)) * static_cast<uint64_t>(rowb_s);
+    ic.a = reinterpret_cast<uint64_t>(a.act_s);
+#pragma unroll
+    for (int d = 0; d < kRowsDepth; ++d) issue(d);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (shared && tid < a.T) {
+    RowTerm r;
+    r.w = reinterpret_cast<uint64_t>(a.page_s) + 2ull * static_cast<uint64_t>(a.H) * static_cast<uint64_t>(rowb_s);
+    r.a = reinterpret_cast<uint64_t>(a.act_s) + static_cast<uint64_t>(tid) * static_cast<uint64_t>(rowb_s);
+    r.rowb = rowb_s;
+    r.units = units_s;
+    terms[tid] = r;
+  }
   if (tid < N) {
-    const int t = tid / a.k;
-    const int j = tid - t * a.k;
-    const uint32_t m = static_cast<uint32_t>(a.tmask[t]);
-    const int pos = a.fpos[tid];
-    const int64_t slot = a.fslot[tid];
-    w_l[tid] = a.w[tid];
-    routed = (m >> j) & 1u;
+    w_l[tid] = wt;
+    routed = (m >> jt) & 1u;
     fpos_l[tid] = routed ? pos : -1;
     if (routed) {
       RowTerm r;
@@ -783,44 +833,21 @@ __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs 
       r.a = reinterpret_cast<uint64_t>(a.act) + static_cast<uint64_t>(pos) * static_cast<uint64_t>(rowb);
       r.rowb = rowb;
       r.units = units;
-      terms[pos] = r;
+      terms[Ts + pos] = r;
     }
   }
-  if (tid < a.T) z_l[tid] = gated ? load_scalar(a.sgate, a.sgate_dtype, tid) : 0.0f;
   const int nr = __syncthreads_count(routed);
-  const int rowb_s = a.Is * static_cast<int>(sizeof(S));
-  const int units_s = (rowb_s + kRowsUnit - 1) / kRowsUnit;
-  if (shared && tid < a.T) {
-    RowTerm r;
-    r.w = reinterpret_cast<uint64_t>(a.page_s) + 2ull * static_cast<uint64_t>(a.H) * static_cast<uint64_t>(rowb_s);
-    r.a = reinterpret_cast<uint64_t>(a.act_s) + static_cast<uint64_t>(tid) * static_cast<uint64_t>(rowb_s);
-    r.rowb = rowb_s;
-    r.units = units_s;
-    terms[nr + tid] = r;
-  }
-  __syncthreads();
-  const int nterms = nr + (shared ? a.T : 0);
-  const int total = nr * units + (shared ? a.T * units_s : 0);
+  nterms = Ts + nr;
+  const int total = nr * units + Ts * units_s;
   if (total > 0) {
-    RowCursor ic, cc;
-    row_cursor_at(ic, terms, 0, h);
-    cc = ic;
-    u32x4 wr[kRowsDepth], ar[kRowsDepth];
+    RowCursor cc;
+    row_cursor_at(cc, terms, 0, h);
     float part = 0.0f;
-    // Issue the cursor's unit into ring slot d and advance; past the last unit the cursor
-    // stays on it (reloads in bounds, never consumed).
-    auto issue = [&](int d) {
-      const int o = ic.u * kRowsUnit + lane * 16;
-      const int oc = o < ic.rowb ? o : ic.rowb - 16;
-      wr[d] = load16<CP>(ic.w + static_cast<uint64_t>(oc));
-      ar[d] = load16<0>(ic.a + static_cast<uint64_t>(oc));
-      if (++ic.u == ic.units) {
-        if (ic.tau + 1 < nterms) row_cursor_at(ic, terms, ic.tau + 1, h);
-        else ic.u = ic.units - 1;
-      }
-    };
+    if constexpr (!PRE) {
+      ic = cc;
 #pragma unroll
-    for (int d = 0; d < kRowsDepth; ++d) issue(d);
+      for (int d = 0; d < kRowsDepth; ++d) issue(d);
+    }
     for (int i = 0; i < total; i += kRowsDepth) {
 #pragma unroll
       for (int d = 0; d < kRowsDepth; ++d) {
@@ -846,14 +873,14 @@ __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs 
   for (int j = 0; j < a.k; ++j) {
     const int f = t * a.k + j;
     const int p = fpos_l[f];
-    if (p >= 0) y += round_out<DT>(vals[wave][p] * w_l[f], a.f16out);
+    if (p >= 0) y += round_out<DT>(vals[wave][Ts + p] * w_l[f], a.f16out);
   }
   if (a.block) {
     y = Elem<DT>::round(y);
     if (a.scale != 1.0f) y = Elem<DT>::round(y * a.scale);
     if (shared) {
-      float sh = Elem<DT>::round(vals[wave][nr + t]);
-      if (gated) sh = Elem<DT>::round(Elem<DT>::round(1.0f / (1.0f + __expf(-z_l[t]))) * sh);
+      float sh = Elem<DT>::round(vals[wave][t]);
+      if (gated) sh = Elem<DT>::round(Elem<DT>::round(1.0f / (1.0f + __expf(-zt))) * sh);
       y += sh;
     }
   }
@@ -867,19 +894,24 @@ hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s) {
   // a token's expert rows are read once at T = 1 (streaming hint); larger batches may read a
   // row twice in a row (two tokens of one expert) and keep it in L2
   const bool once = a.T == 1;
+  const int64_t rowb_s = static_cast<int64_t>(a.Is) * dtype_bytes(dtype);
+  const bool pre = a.page_s != nullptr && (rowb_s + kRowsUnit - 1) / kRowsUnit > kRowsDepth;
+  auto go = [&](auto dt, auto cp, auto pr) {
+    down_rows_kernel<decltype(dt)::value, decltype(cp)::value, decltype(pr)::value>
+        <<<blocks, kRowsWaves * kWave, 0, s>>>(a);
+  };
+  auto by_pre = [&](auto dt, auto cp) {
+    if (pre) go(dt, cp, std::true_type{});
+    else go(dt, cp, std::false_type{});
+  };
+  auto by_cp = [&](auto dt) {
+    if (once) by_pre(dt, std::integral_constant<int, kNonTemporal>{});
+    else by_pre(dt, std::integral_constant<int, 0>{});
+  };
   switch (dtype) {
-    case kF32:
-      if (once) down_rows_kernel<kF32, kNonTemporal><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
-      else down_rows_kernel<kF32, 0><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
-      break;
-    case kF16:
-      if (once) down_rows_kernel<kF16, kNonTemporal><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
-      else down_rows_kernel<kF16, 0><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
-      break;
-    default:
-      if (once) down_rows_kernel<kBF16, kNonTemporal><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
-      else down_rows_kernel<kBF16, 0><<<blocks, kRowsWaves * kWave, 0, s>>>(a);
-      break;
+    case kF32: by_cp(std::integral_constant<int, kF32>{}); break;
+    case kF16: by_cp(std::integral_constant<int, kF16>{}); break;
+    default: by_cp(std::integral_constant<int, kBF16>{}); break;
   }
   return hipGetLastError();
 }

@@ -31,14 +31,18 @@ struct TopkGroup {
 // Lane j of a group reads experts j + G*i of token t. Experts past E read -inf (never
 // selected); a token past T reads zeros so that its arithmetic stays finite (its results
 // are discarded).
+// Every lane loads (from a clamped, in-bounds index; T >= 1) and then selects, so that the loads
+// of several passes are all in flight before the first is waited for (a load under a branch is
+// waited for inside the branch).
 template <int LDT, int G, int PL>
 __device__ __forceinline__ void load_logits(const void* logits, int t, int T, int E, float (&v)[PL]) {
   const int j = lane_id() % G;
+  const int64_t row = static_cast<int64_t>(t < T ? t : T - 1) * E;
 #pragma unroll
   for (int i = 0; i < PL; ++i) {
     const int e = j + G * i;
-    v[i] = e >= E ? -__builtin_inff()
-                  : (t < T ? load_as_f32<LDT>(logits, static_cast<int64_t>(t) * E + e) : 0.0f);
+    const float x = load_as_f32<LDT>(logits, row + (e < E ? e : E - 1));
+    v[i] = e >= E ? -__builtin_inff() : (t < T ? x : 0.0f);
   }
 }
 
@@ -187,6 +191,46 @@ __device__ __forceinline__ void group_topk_softmax(float (&p)[NB][PL], int E, in
       if (j < k) w_out[b] = w_out[b] / sum;
     }
   }
+}
+
+// Top-k by selection rounds, for one expert per lane (E <= G), where the latency of one token
+// pass matters (the one-wave routing of small batches): the softmax as above, then k rounds of
+// (group max of p by DPP, the lowest lane of the group holding that max from one ballot). Equal
+// p are equal bits (p >= +0, no NaN), so the lowest lane among them is the key order of the
+// ranking (larger p first, ties to the lower expert index): the same picks in the same order.
+// Lane j picked in round r gets slot_out = r (else -1). Renormalisation divides by the picks'
+// sum taken in rank order.
+template <int G>
+__device__ __forceinline__ void group_topk_select(float& p, int E, int k, bool renorm, float& w_out,
+                                                  int& id_out, int& slot_out) {
+#pragma clang fp contract(off)
+  const int lane = lane_id();
+  const int j = lane % G;
+  const int base = lane - j;
+  const bool valid = j < E;
+  const float m = group_reduce<G>(p, [](float a, float c) { return fmaxf(a, c); });
+  const float ex = valid ? exp_nonpos(p - m) : 0.0f;
+  const float s = group_reduce<G>(ex, [](float a, float c) { return a + c; });
+  const float pr = ex * (1.0f / s);
+  // below every probability: never the max while k <= E (a NaN probability, from NaN logits,
+  // ranks there too, so every round still picks one lane)
+  float q = (valid && pr == pr) ? pr : -1.0f;
+  int slot = -1;
+  float sum = 0.0f;
+  for (int r = 0; r < k; ++r) {
+    const float mx = group_reduce<G>(q, [](float a, float c) { return fmaxf(a, c); });
+    const uint64_t eq = ballot(q == mx);
+    const uint64_t gm = G == kWave ? eq : (eq >> base) & ((uint64_t{1} << G) - 1);
+    const int pick = __builtin_ctzll(gm);
+    if (j == pick) {
+      slot = r;
+      q = -2.0f;
+    }
+    sum = (r == 0) ? mx : sum + mx;
+  }
+  slot_out = slot;
+  id_out = j;
+  w_out = renorm ? pr / sum : pr;
 }
 
 // Top-k by ranking, for one expert per lane (E <= 64). The softmax is as above; then lane j
@@ -472,25 +516,26 @@ __device__ __forceinline__ void route_small_wave(const void* logits, int T, int 
   int e = -2;
   if (logits != nullptr) {
     const int passes = (T + TPW - 1) / TPW;
+    // every pass's loads are issued (in bounds: load_logits clamps) before any is waited for
     float v[kSmallRoutePasses][1];
 #pragma unroll
     for (int ps = 0; ps < kSmallRoutePasses; ++ps)
-      if (ps < passes) load_logits<LDT, G, 1>(logits, ps * TPW + lane / G, T, E, v[ps]);
+      load_logits<LDT, G, 1>(logits, ps * TPW + lane / G, T, E, v[ps]);
 #pragma unroll
     for (int ps = 0; ps < kSmallRoutePasses; ++ps) {
       if (ps >= passes) break;
-      float pv[1][1] = {{v[ps][0]}};
-      float w[1];
-      int id[1], slot[1];
-      group_topk_rank<G, 1>(pv, E, k, renorm != 0, sc.rs, w, id, slot);
+      float pv = v[ps][0];
+      float w;
+      int id, slot;
+      group_topk_select<G>(pv, E, k, renorm != 0, w, id, slot);
       const int t = ps * TPW + lane / G;
-      if (t < T && slot[0] >= 0) {
-        const int f = t * k + slot[0];
-        if (a.w) a.w[f] = w[0];
-        if (a.ids) a.ids[f] = id[0];
-        if (b.w) b.w[f] = w[0];
-        if (b.ids) b.ids[f] = id[0];
-        sc.ids[f] = id[0];
+      if (t < T && slot >= 0) {
+        const int f = t * k + slot;
+        if (a.w) a.w[f] = w;
+        if (a.ids) a.ids[f] = id;
+        if (b.w) b.w[f] = w;
+        if (b.ids) b.ids[f] = id;
+        sc.ids[f] = id;
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -525,7 +570,7 @@ __device__ __forceinline__ void route_small_wave(const void* logits, int T, int 
   const bool lead = ok && rank == 0;  // this lane writes its expert's records
   const int cnt = __popcll(eq);
   const int ai = __popcll(less & first);
-  const int nr = lead ? (cnt + span - 1) / span : 0;
+  const int nr = lead ? (cnt <= span ? 1 : (cnt + span - 1) / span) : 0;
   int j0 = ai;
   int nranges = __popcll(first);
   if (ballot(nr > 1) != 0) {  // wave-uniform: some expert needs several ranges

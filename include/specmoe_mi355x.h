@@ -330,7 +330,7 @@ int smx_routing_in_gateup(void);
  * Waves per workgroup of the weight-streaming gate/up kernel: 4, 2 or 1 (the kernel's work is
  * the same -- one wave per 16 intermediate rows of an expert; only the grouping of waves into
  * workgroups, and with it the grid, changes), or 0 (the default rule): 4, unless that grid
- * would hold fewer than 512 workgroups (two per CU), then 2 or 1, whichever first reaches 512.
+ * would hold fewer than 320 workgroups, then 2 or 1, whichever first reaches 320.
  * Applies to batches of at most 32 tokens; larger ones always use 4. Outputs are identical
  * for every setting (same per-wave K walk and rounding). Process-wide, like
  * smx_set_tiled_min_tokens. Part of the expert-kernel configuration that replaces the
