@@ -307,7 +307,6 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     __shared__ RangeRec rr_l[kSortRangesMax];
     __shared__ int32_t sf_l[kSortWaveMax];
     __shared__ int32_t hdr_l[2];
-    __shared__ RankScratch rs_all[W];
     if (!in_shared) {
       const int lane = lane_id();
       const int tid = threadIdx.x;
@@ -319,7 +318,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
         constexpr int TPW = TopkGroup<RG, 1>::kTokens;
         const int stride = W * TPW;
         for (int t0 = wave * TPW + lane / RG; t0 - lane / RG < a.T; t0 += stride * kTokBatch) {
-          topk_batch<DT, RG, 1>(a.rt.logits, a.T, E, a.k, a.rt.renorm != 0, t0, stride, rs_all[wave],
+          topk_batch<DT, RG, 1>(a.rt.logits, a.T, E, a.k, a.rt.renorm != 0, t0, stride,
                                 [&](int t, int slot, float wv, int id) {
             const int f = t * a.k + slot;
             if (writer) {
@@ -680,7 +679,7 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
 // tokens need is read from HBM once and then from L2), then the shared expert's T rows.
 // Arithmetic: term = round(w * dot) per routed assignment, summed in j order; block form as
 // combine_kernel. The dot runs in fp32 over the lane's elements in K order, then a fixed
-// butterfly across lanes.
+// reduction across lanes (DPP steps within rows of 16, then the four row sums).
 // Units in flight per wave, measured on the DeepSeek-V2-Lite block at one token (us per
 // layer): 2: 34.5, 3: 32.9, 4: 32.4, 6: 33.0, 8: 33.3, 12: 34.3, 16: 36.4, 24: 37.3 (the split
 // down kernel + combine: 37.1). 2 or 4 waves per row taking interleaved units, and a cursor
@@ -855,7 +854,7 @@ __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs 
           const int o = cc.u * kRowsUnit + lane * 16;
           if (o < cc.rowb) part = dot16<DT>(wr[d], ar[d], part);
           if (++cc.u == cc.units) {  // the term's last unit: its dot goes to LDS
-            const float v = wave_sum_butterfly(part);
+            const float v = group_reduce<kWave>(part, [](float x, float y) { return x + y; });
             if (lane == 0) vals[wave][cc.tau] = v;
             part = 0.0f;
             if (cc.tau + 1 < nterms) row_cursor_at(cc, terms, cc.tau + 1, h);

@@ -23,11 +23,9 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restric
   const int waves = blockDim.x / kWave;
   const int lane = lane_id();
   const int stride = gridDim.x * waves * TPW;  // tokens per pass of the whole grid
-  __shared__ RankScratch rs_all[4];
-  RankScratch& rs = rs_all[threadIdx.x / kWave];
   for (int t0 = (blockIdx.x * waves + threadIdx.x / kWave) * TPW + lane / G; t0 - lane / G < T;
        t0 += stride * kTokBatch) {
-    topk_batch<LDT, G, PL>(logits, T, E, k, renorm != 0, t0, stride, rs, [&](int t, int slot, float wv, int id) {
+    topk_batch<LDT, G, PL>(logits, T, E, k, renorm != 0, t0, stride, [&](int t, int slot, float wv, int id) {
       w[static_cast<int64_t>(t) * k + slot] = wv;
       ids[static_cast<int64_t>(t) * k + slot] = id;
     });
@@ -97,37 +95,44 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
 
   // wave 0: per-expert totals and per-wave prefixes, then exclusive scans over experts
   // (each lane owns 4 consecutive experts), the per-wave start positions and the compact
-  // active-expert table.
+  // active-expert table. Every per-wave count is read at once (the array covers every wave
+  // and expert index; counts past the launched waves or past E are masked), and the start
+  // positions are written once.
   if (wave == 0) {
     const int bm = out.bm > 0 ? out.bm : 1;
     const int span = out.span > 0 ? out.span : 1;
+    int cw[4][kRouteMaxWaves];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int w = 0; w < kRouteMaxWaves; ++w) cw[i][w] = sh.cntw[w][lane * 4 + i];
     int c[4], sc = 0, sp = 0, sa = 0, sr = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
       c[i] = 0;
-      if (e < E) {
-        for (int w = 0; w < nw; ++w) {
-          const int v = sh.cntw[w][e];
-          sh.cntw[w][e] = c[i];  // per-wave exclusive prefix, in wave order
-          c[i] += v;
-        }
-        sh.cnt[e] = c[i];
-      }
-      sc += c[i];
-      sp += (c[i] + bm - 1) / bm * bm;
-      sa += c[i] > 0;
-      sr += (c[i] + span - 1) / span;
-    }
-    int ic = sc, ip = sp, ia = sa, ir = sr;
 #pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int tc = __shfl_up(ic, off, kWave);
-      const int tp = __shfl_up(ip, off, kWave);
-      const int ta = __shfl_up(ia, off, kWave);
-      const int tr = __shfl_up(ir, off, kWave);
-      if (lane >= off) { ic += tc; ip += tp; ia += ta; ir += tr; }
+      for (int w = 0; w < kRouteMaxWaves; ++w) {
+        const int v = (e < E && w < nw) ? cw[i][w] : 0;
+        cw[i][w] = c[i];  // per-wave exclusive prefix, in wave order
+        c[i] += v;
+      }
+      if (e < E) sh.cnt[e] = c[i];
     }
+    // per expert: block-padded count and work ranges (small divisions by the runtime bm, span)
+    const float rbm = 1.0f / bm, rspan = 1.0f / span;
+    int pd[4], nrg[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pd[i] = div_small(c[i] + bm - 1, bm, rbm) * bm;
+      nrg[i] = div_small(c[i] + span - 1, span, rspan);
+      sc += c[i];
+      sp += pd[i];
+      sa += c[i] > 0;
+      sr += nrg[i];
+    }
+    const int ic = wave_incl_scan(sc), ip = wave_incl_scan(sp), ia = wave_incl_scan(sa),
+              ir = wave_incl_scan(sr);
     if (lane == kWave - 1) sh.nranges = ir;
     int bc = ic - sc, bp = ip - sp, ba = ia - sa, br = ir - sr;
 #pragma unroll
@@ -135,7 +140,9 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
       const int e = lane * 4 + i;
       if (e <= E) { sh.off[e] = bc; sh.seg[e] = bp; }
       if (e < E) {
-        for (int w = 0; w < nw; ++w) sh.cntw[w][e] += bc;
+#pragma unroll
+        for (int w = 0; w < kRouteMaxWaves; ++w)
+          if (w < nw) sh.cntw[w][e] = cw[i][w] + bc;
         if (out.ranges && c[i] > 0) {
           RangeRec rec{};
           rec.slot = kCheckSlots ? sh.slot[e] : -1;
@@ -143,14 +150,14 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
           rec.cnt = c[i];
           rec.key = ba;
           rec.j0 = br;
-          rec.nr = (c[i] + span - 1) / span;
+          rec.nr = nrg[i];
           for (int r = 0; r < rec.nr; ++r) out.ranges[br + r] = rec;
         }
       }
       bc += c[i];
-      bp += (c[i] + bm - 1) / bm * bm;
+      bp += pd[i];
       ba += c[i] > 0;
-      br += (c[i] + span - 1) / span;
+      br += nrg[i];
     }
     if (E == 4 * kWave && lane == kWave - 1) { sh.off[E] = bc; sh.seg[E] = bp; }
   }
@@ -235,10 +242,9 @@ __global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
   // so that this load's latency overlaps the logit loads.
   const int64_t my_slot = threadIdx.x < E ? e2s[threadIdx.x] : -1;
   if (logits != nullptr) {
-    __shared__ RankScratch rs_all[kRouteMaxWaves];
     const int stride = nw * TPW;
     for (int t0 = wave * TPW + lane / G; t0 - lane / G < T; t0 += stride * kTokBatch) {
-      topk_batch<LDT, G, PL>(logits, T, E, k, renorm != 0, t0, stride, rs_all[wave],
+      topk_batch<LDT, G, PL>(logits, T, E, k, renorm != 0, t0, stride,
                              [&](int t, int slot, float wv, int id) {
         const int f = t * k + slot;
         if (w_out) w_out[f] = wv;
@@ -255,11 +261,16 @@ __global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
   if (threadIdx.x < E) sh.slot[threadIdx.x] = (my_slot >= 0 && my_slot < num_slots) ? my_slot : -1;
   __syncthreads();
   if (out.tmask) {
+    // all of a token's ids, then all their slots, read at once (two LDS latencies per token)
     for (int t = threadIdx.x; t < T; t += blockDim.x) {
+      int e[kMaxTopK];
+#pragma unroll
+      for (int j = 0; j < kMaxTopK; ++j) e[j] = j < k ? sh.ids[t * k + min(j, k - 1)] : -1;
       uint32_t m = 0;
-      for (int j = 0; j < k; ++j) {
-        const int e = sh.ids[t * k + j];
-        if (e >= 0 && sh.slot[e] >= 0) m |= 1u << j;
+#pragma unroll
+      for (int j = 0; j < kMaxTopK; ++j) {
+        const int64_t sl = sh.slot[e[j] >= 0 ? e[j] : 0];
+        if (e[j] >= 0 && sl >= 0) m |= 1u << j;
       }
       out.tmask[t] = static_cast<int32_t>(m);
     }
@@ -313,7 +324,6 @@ __global__ __launch_bounds__(kNormThreads) void norm_gate_kernel(NormGateArgs a)
   __shared__ float sb[kNormMaxH];
   __shared__ float red[kNormWaves];
   __shared__ float lg[kMaxExperts];
-  __shared__ RankScratch rs;
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   const int lane = lane_id();
@@ -425,7 +435,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_gate_kernel(NormGateArgs a)
   float w[1];
   int id[1], slot[1];
   if constexpr (PL == 1) {
-    group_topk_rank<G, 1>(v, a.E, a.k, a.renorm != 0, rs, w, id, slot);
+    group_topk_select<G>(v[0][0], a.E, a.k, a.renorm != 0, w[0], id[0], slot[0]);
   } else {
     group_topk_softmax<G, PL, 1>(v, a.E, a.k, a.renorm != 0, w, id);
     slot[0] = j < a.k ? j : -1;

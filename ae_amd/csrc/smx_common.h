@@ -126,22 +126,35 @@ __device__ __forceinline__ float exp_nonpos(float d) {
   return p * scale;
 }
 
-// ---------------------------------------------------------------------------------------
-// Wave64 reductions. The xor butterfly gives every lane the same value (fp add is
-// commutative), and its pairing order is fixed: lane sums l and l^32 first, then l^16, ...
-// ---------------------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum_butterfly(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, kWave);
-  return v;
-}
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// Inclusive prefix sum over the 64 lanes of a wave by DPP (VALU operand modifiers, no LDS
+// round trip): row_shr 1, 2, 4, 8 within each row of 16 lanes, then row_bcast:15 adds row 0's
+// (row 2's) total to rows 1 (3), and row_bcast:31 adds the first 32 lanes' total to rows 2
+// and 3. Lanes whose DPP source is outside the row, or whose row is masked, add 0.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 -> rows 2, 3
   return v;
 }
 
-__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+// Value of lane 63 (a wave-uniform scalar).
+__device__ __forceinline__ int last_lane(int v) { return __builtin_amdgcn_readlane(v, kWave - 1); }
+
+// c / d for 0 <= c < 2^23 and d >= 1, with rd = 1.0f / d: the float quotient is within one of
+// the integer quotient, and one correction step makes it exact (a few VALU operations instead
+// of an integer division's ~30).
+__device__ __forceinline__ int div_small(int c, int d, float rd) {
+  int q = static_cast<int>(static_cast<float>(c) * rd);
+  const int r = c - q * d;
+  if (r < 0) --q;
+  else if (r >= d) ++q;
+  return q;
+}
 
 // Wave index within the workgroup, in a scalar register: the compiler cannot see that
 // threadIdx.x / 64 is the same across a wave, and values derived from it (buffer offsets)

@@ -193,13 +193,14 @@ __device__ __forceinline__ void group_topk_softmax(float (&p)[NB][PL], int E, in
   }
 }
 
-// Top-k by selection rounds, for one expert per lane (E <= G), where the latency of one token
-// pass matters (the one-wave routing of small batches): the softmax as above, then k rounds of
-// (group max of p by DPP, the lowest lane of the group holding that max from one ballot). Equal
-// p are equal bits (p >= +0, no NaN), so the lowest lane among them is the key order of the
-// ranking (larger p first, ties to the lower expert index): the same picks in the same order.
+// Top-k for one expert per lane (E <= G <= 64): the softmax as above, then k selection rounds,
+// each a group max of p (DPP steps) and the lowest lane of the group holding that max (one
+// ballot). Equal p are equal bits (p >= +0, no NaN), so the lowest lane among them is the
+// lower expert index: descending p, ties to the lower index, as select_experts orders them.
 // Lane j picked in round r gets slot_out = r (else -1). Renormalisation divides by the picks'
-// sum taken in rank order.
+// sum taken in pick order. Against a ranking by 64-bit keys compared from LDS (each lane
+// counting the larger keys of its group, ~1 us per token pass at E = 64: the LDS reads
+// issue two at a time), the rounds are a few dozen dependent VALU steps each.
 template <int G>
 __device__ __forceinline__ void group_topk_select(float& p, int E, int k, bool renorm, float& w_out,
                                                   int& id_out, int& slot_out) {
@@ -233,68 +234,13 @@ __device__ __forceinline__ void group_topk_select(float& p, int E, int k, bool r
   w_out = renorm ? pr / sum : pr;
 }
 
-// Top-k by ranking, for one expert per lane (E <= 64). The softmax is as above; then lane j
-// of a group forms the exact 64-bit key (bits(p) << 8) | (255 - j) -- p >= 0, so larger keys
-// mean larger p, ties to the lower expert index -- and its rank is the number of larger keys
-// in its group, read back from the wave's LDS slice (independent compares instead of k
-// dependent arg-max rounds). Lane j with rank r < k is the r-th pick: slot_out = r (else -1).
-// Renormalisation divides by the picks' sum taken in rank order.
-struct RankScratch {
-  uint64_t key[kTokBatch][kWave];
-  float pick[kTokBatch][kWave];
-};
-
-template <int G, int NB>
-__device__ __forceinline__ void group_topk_rank(float (&p)[NB][1], int E, int k, bool renorm,
-                                                RankScratch& rs, float (&w_out)[NB],
-                                                int (&id_out)[NB], int (&slot_out)[NB]) {
-#pragma clang fp contract(off)
-  const int lane = lane_id();
-  const int j = lane % G;
-  const int base = lane - j;
-  const bool valid = j < E;
-  uint64_t key[NB];
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    const float m = group_reduce<G>(p[b][0], [](float a, float c) { return fmaxf(a, c); });
-    const float ex = valid ? exp_nonpos(p[b][0] - m) : 0.0f;
-    const float s = group_reduce<G>(ex, [](float a, float c) { return a + c; });
-    p[b][0] = ex * (1.0f / s);
-    key[b] = valid ? ((static_cast<uint64_t>(__float_as_uint(p[b][0])) << 8) | static_cast<uint64_t>(255 - j)) : 0ull;
-    rs.key[b][lane] = key[b];
-  }
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int b = 0; b < NB; ++b) {
-    int rank = 0;
-#pragma unroll
-    for (int g = 0; g < G; ++g) rank += rs.key[b][base + g] > key[b] ? 1 : 0;
-    slot_out[b] = (valid && rank < k) ? rank : -1;
-    w_out[b] = p[b][0];
-    id_out[b] = j;
-  }
-  if (renorm) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-      if (slot_out[b] >= 0) rs.pick[b][base + slot_out[b]] = w_out[b];
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      float sum = rs.pick[b][base];
-      for (int r = 1; r < k; ++r) sum = sum + rs.pick[b][base + r];
-      w_out[b] = w_out[b] / sum;
-    }
-  }
-  __builtin_amdgcn_wave_barrier();  // the slice is reused by the next batch
-}
-
 // The tokens of kTokBatch consecutive wave-passes: token t = first + b * stride for this
 // lane's group. All logit loads are issued before any token is computed, so a wave pays one
 // load latency per batch. fn(t, w, id) is called on every lane (t may be >= T).
 // fn(t, slot, w, id) is called for every pick of token t (t < T): slot in [0, k).
 template <int LDT, int G, int PL, typename Fn>
 __device__ __forceinline__ void topk_batch(const void* logits, int T, int E, int k, bool renorm,
-                                           int first, int stride, RankScratch& rs, Fn&& fn) {
+                                           int first, int stride, Fn&& fn) {
   float v[kTokBatch][PL];
 #pragma unroll
   for (int b = 0; b < kTokBatch; ++b) load_logits<LDT, G, PL>(logits, first + b * stride, T, E, v[b]);
@@ -302,7 +248,8 @@ __device__ __forceinline__ void topk_batch(const void* logits, int T, int E, int
   int id[kTokBatch];
   int slot[kTokBatch];
   if constexpr (PL == 1) {
-    group_topk_rank<G, kTokBatch>(v, E, k, renorm, rs, w, id, slot);
+#pragma unroll
+    for (int b = 0; b < kTokBatch; ++b) group_topk_select<G>(v[b][0], E, k, renorm, w[b], id[b], slot[b]);
   } else {
     group_topk_softmax<G, PL, kTokBatch>(v, E, k, renorm, w, id);
     const int j = lane_id() % G;
@@ -392,21 +339,14 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
   const int ce = lane < E ? run[lane] : 0;
   const int bm = out.bm > 0 ? out.bm : 1;
   const int span = out.span > 0 ? out.span : 1;
-  const int pad = (ce + bm - 1) / bm * bm;
+  const int pad = div_small(ce + bm - 1, bm, 1.0f / bm) * bm;
   const int act = ce > 0 ? 1 : 0;
-  const int nr = (ce + span - 1) / span;
-  int ic = ce, ip = pad, ia = act, ir = nr;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const int tc = __shfl_up(ic, o, kWave);
-    const int tp = __shfl_up(ip, o, kWave);
-    const int ta = __shfl_up(ia, o, kWave);
-    const int tr = __shfl_up(ir, o, kWave);
-    if (lane >= o) { ic += tc; ip += tp; ia += ta; ir += tr; }
-  }
+  const int nr = div_small(ce + span - 1, span, 1.0f / span);
+  const int ic = wave_incl_scan(ce), ip = wave_incl_scan(pad), ia = wave_incl_scan(act),
+            ir = wave_incl_scan(nr);
   const int off = ic - ce, seg = ip - pad, ai = ia - act, br = ir - nr;
-  const int seg_total = __shfl(ip, kWave - 1, kWave);
-  const int ranges_total = __shfl(ir, kWave - 1, kWave);
+  const int seg_total = last_lane(ip);
+  const int ranges_total = last_lane(ir);
   const bool any_bad = ballot(bad) != 0;
   if (lane < E) {
     sc.cnt[lane] = ce;
@@ -492,7 +432,6 @@ struct SmallRouteOut {
 };
 
 struct SmallRouteLds {
-  RankScratch rs;
   int ids[kWave];
   int64_t slot[kWave];
   int nr[kWave];  // ranges per active expert, then the first range of each (several-range case)
@@ -577,13 +516,8 @@ __device__ __forceinline__ void route_small_wave(const void* logits, int T, int 
     if (lead) sc.nr[ai] = nr;
     __builtin_amdgcn_wave_barrier();
     const int v = lane < nranges ? sc.nr[lane] : 0;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const int t = __shfl_up(incl, o, kWave);
-      if (lane >= o) incl += t;
-    }
-    nranges = __shfl(incl, kWave - 1, kWave);
+    const int incl = wave_incl_scan(v);
+    nranges = last_lane(incl);
     __builtin_amdgcn_wave_barrier();
     sc.nr[lane] = incl - v;  // first range of active expert `lane`
     __builtin_amdgcn_wave_barrier();
