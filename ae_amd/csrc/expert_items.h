@@ -39,8 +39,12 @@ struct ChunkOrder {
 // on a few residues, was slower than none at H = 4096). The down projection's rows (pitch I)
 // are walked in order: its K splits already start at different chunks, and rotating them
 // measured no gain.
+// (index >> 2) < 2^23 for every launch: index < (active experts + 1) * (workgroups per item)
+// + workgroups per item. The modulo is taken with a float reciprocal (div_small): a runtime
+// integer division costs ~20 dependent VALU steps, on every workgroup's path to its first load.
 __device__ __forceinline__ ChunkOrder rotated_order(int n, int index) {
-  return ChunkOrder{n, (index >> 2) % n};
+  const int q = index >> 2;
+  return ChunkOrder{n, q - div_small(q, n, 1.0f / static_cast<float>(n)) * n};
 }
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
@@ -105,8 +109,9 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
                                           const RangeRec* ranges) {
   const int64_t elem = static_cast<int64_t>(sizeof(S));
   const int b = blockIdx.x;
+  const float rpi = 1.0f / static_cast<float>(per_item);  // grids hold fewer than 2^23 workgroups
   if (b < shared_blocks) {
-    const int v = b / per_item;
+    const int v = div_small(b, per_item, rpi);
     const int span = a.rb.span;
     w.page = static_cast<const char*>(a.sh.page);
     w.page_bytes = 3 * static_cast<int64_t>(a.H) * a.sh.I * elem;
@@ -120,7 +125,7 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
     return true;
   }
   const int rb = b - shared_blocks;
-  const int j = rb / per_item;  // one of the expert's ranges; uniform across the workgroup
+  const int j = div_small(rb, per_item, rpi);  // one of the expert's ranges; uniform across the workgroup
   // j is below the launch's range bound, so the record may be read before the range count is
   // known (the loads then share one latency); records past the count are unused.
   const int nranges = uniform(hdr[0]);

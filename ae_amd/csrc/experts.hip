@@ -226,6 +226,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   const ChunkOrder ord = rotated_order(static_cast<int>(row_bytes / (kStepBytes * kUnroll)), it.rot);
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   const int f16out = it.shared ? 0 : a.f16out;
+  const float rk = 1.0f / static_cast<float>(a.k);  // flat assignment f -> token f / k
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<2> wa, wb;
     issue_weights<CP>(wa, wb, ws, ord);
@@ -237,7 +238,7 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
 #pragma unroll
       for (int n = 0; n < 4 / W; ++n) {
         const int q = min(q0 + j * kTokTile + 4 * (wave + W * n) + (lane >> 4), m - 1);
-        const int tok = it.shared ? off + q : sorted[off + q] / a.k;
+        const int tok = it.shared ? off + q : div_small(sorted[off + q], a.k, rk);
         tb.off[j][n] = static_cast<uint32_t>(tok * row_bytes + (lane & 15) * 16);
       }
     f32x4 acc[2][MT];
@@ -488,7 +489,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void down_kernel(ExpertArgs a) {
   const int split_steps = in_shared ? a.sh.split_steps : a.split_steps;
   WorkItem it;
   if (!work_item<typename Elem<DT>::S>(a, a.sh.down_blocks, groups * splits, it, a.rb.hdr, a.rb.ranges)) return;
-  const int sp = it.tg / groups;
+  const int sp = div_small(it.tg, groups, 1.0f / static_cast<float>(groups));
   const int tg = it.tg - sp * groups;
   const int rtraw = tg * kExpertWaves + wave;
   const bool owner = rtraw < rtiles;
@@ -605,10 +606,13 @@ constexpr int kCombineRowOuts = 8;
 
 template <int DT>
 __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(CombineArgs c) {
-  const int64_t idx = (static_cast<int64_t>(blockIdx.x) * kCombineRowThreads + threadIdx.x) * kCombineRowOuts;
-  if (idx >= static_cast<int64_t>(c.T) * c.H) return;
-  const int t = static_cast<int>(idx / c.H);
-  const int h = static_cast<int>(idx - static_cast<int64_t>(t) * c.H);
+  // thread g owns outputs [8g, 8g + 8): token g / (H/8); T*H/8 < 2^31 (one chunk of the call)
+  const int per_t = c.H / kCombineRowOuts;
+  const int g = static_cast<int>(blockIdx.x) * kCombineRowThreads + static_cast<int>(threadIdx.x);
+  if (g >= c.T * per_t) return;
+  const int t = c.T * per_t < (1 << 23) ? div_small(g, per_t, 1.0f / static_cast<float>(per_t)) : g / per_t;
+  const int h = (g - t * per_t) * kCombineRowOuts;
+  const int64_t idx = static_cast<int64_t>(t) * c.H + h;
   const uint32_t vm = static_cast<uint32_t>(c.tmask[t]);
   const int64_t split_stride = static_cast<int64_t>(c.T) * c.k * c.H;
   f32x4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
@@ -787,7 +791,7 @@ __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs 
   // their count: loads complete in issue order, and the table is then waited for without
   // waiting for the weight loads issued after it.
   const int fi = tid < N ? tid : N - 1;
-  const int tt = fi / a.k;
+  const int tt = div_small(fi, a.k, 1.0f / static_cast<float>(a.k));
   const int jt = fi - tt * a.k;
   const uint32_t m = static_cast<uint32_t>(a.tmask[tt]);
   const int pos = a.fpos[fi];
