@@ -77,6 +77,8 @@ SIGNATURES = [
     ("smx_routing_in_gateup", _i32, []),
     ("smx_set_gateup_waves", ctypes.c_int, [_i32]),
     ("smx_gateup_waves", _i32, []),
+    ("smx_set_gateup_item_walk", ctypes.c_int, [_i32]),
+    ("smx_gateup_item_walk", _i32, []),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
 ]
 

@@ -56,6 +56,9 @@ bool g_fp32_f16out = false;
 bool g_route_in_gateup = true;
 // Waves per gate/up workgroup (smx_set_gateup_waves): 0 = the default rule (gateup_waves).
 int g_gateup_waves = 0;
+// Gate/up grids larger than one residency of the chip run as workgroups walking several items
+// (smx_set_gateup_item_walk).
+bool g_gateup_walk = true;
 // The default rule: 4 waves per workgroup, unless that grid would leave part of the chip's
 // CUs without a workgroup (fewer workgroups than kGateupFillBlocks); then 2 or 1, whichever
 // first reaches it. Measured, us per layer, 4 / 2 / 1 waves (same box): DeepSeek-V2-Lite 2
@@ -409,6 +412,8 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   a.split_steps = p.split_steps;
   a.down_rows = p.down_rows;
   a.gu_waves = p.gu_waves;
+  // the walk pays where every item's prologue would be the top-k from logits and the sort
+  a.gu_items = g_gateup_walk && route_g > 0 && rt.logits != nullptr ? 1 : 0;
   a.f16out = dtype == kF32 && g_fp32_f16out ? 1 : 0;
   if (p.Is > 0) {
     a.sh.page = bt.shared_page;
@@ -936,6 +941,13 @@ int smx_set_gateup_waves(int waves) {
 }
 
 int smx_gateup_waves(void) { return g_gateup_waves; }
+
+int smx_set_gateup_item_walk(int on) {
+  g_gateup_walk = on != 0;
+  return SMX_OK;
+}
+
+int smx_gateup_item_walk(void) { return g_gateup_walk ? 1 : 0; }
 
 int smx_set_profile_events(void* const* events, int count) {
   if (events == nullptr || count == 0) {

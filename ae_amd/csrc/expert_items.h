@@ -103,12 +103,13 @@ struct WorkItem {
 // W: waves per workgroup (a workgroup covers W weight tiles of its item). The K-walk rotation
 // index is that of the 4-wave workgroup covering the same tiles (rot_items: workgroups per
 // item at 4 waves), so the accumulation order of every output does not depend on W.
+// b: the work item's index in the launch (the workgroup index, or for a workgroup that walks
+// several items, the item it is on).
 template <typename S, int W = kExpertWaves>
-__device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
+__device__ __forceinline__ bool work_item(const ExpertArgs& a, int b, int shared_blocks, int per_item,
                                           int rot_items, WorkItem& w, const int32_t* hdr,
                                           const RangeRec* ranges) {
   const int64_t elem = static_cast<int64_t>(sizeof(S));
-  const int b = blockIdx.x;
   const float rpi = 1.0f / static_cast<float>(per_item);  // grids hold fewer than 2^23 workgroups
   if (b < shared_blocks) {
     const int v = div_small(b, per_item, rpi);
@@ -171,7 +172,8 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
 template <typename S>
 __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks, int per_item,
                                           WorkItem& w, const int32_t* hdr, const RangeRec* ranges) {
-  return work_item<S, kExpertWaves>(a, shared_blocks, per_item, per_item, w, hdr, ranges);
+  return work_item<S, kExpertWaves>(a, static_cast<int>(blockIdx.x), shared_blocks, per_item,
+                                    per_item, w, hdr, ranges);
 }
 
 }  // namespace smx

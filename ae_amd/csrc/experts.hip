@@ -291,13 +291,17 @@ __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem&
 // workgroup's 4 waves run the top-k (RG lanes per token; or load caller ids), then wave 0 sorts
 // the assignments (sort_wave) into the workgroup's LDS; the first routed workgroup also
 // writes the records and top-k results, and its threads the token mask.
-template <bool kMulti, int DT, int MT, int RG, bool RM = false, int W = kExpertWaves>
+// P: the workgroup walks the items b = blockIdx.x, + gridDim.x, ... < a.gu_items (a grid of at
+// most one residency of the chip, for batches with more items than that): the routing (with
+// RG > 0) is done once per workgroup, at the start, and every later item starts with its weight
+// loads instead of a routing prologue under load. Every such workgroup routes; the first writes
+// the records.
+template <bool kMulti, int DT, int MT, int RG, bool RM = false, int W = kExpertWaves, bool P = false>
 __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
   const int wave = wave_id();
-  const bool in_shared = static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
-  const int Iw = in_shared ? a.sh.I : a.I;
-  const int tiles = Iw / kRowTile;
-  const int groups = (tiles + W - 1) / W;
+  // routing: whether this workgroup has a routed item, and whether it writes the records
+  const bool in_shared = P ? false : static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
+  const bool writer_wg = P ? blockIdx.x == 0 : static_cast<int>(blockIdx.x) == a.sh.gateup_blocks;
   const int32_t* hdr = a.rb.hdr;
   const RangeRec* ranges = a.rb.ranges;
   const int32_t* sorted = a.rb.sorted_f;
@@ -313,7 +317,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
       const int tid = threadIdx.x;
       const int N = a.T * a.k;
       const int E = a.rt.E;
-      const bool writer = static_cast<int>(blockIdx.x) == a.sh.gateup_blocks;
+      const bool writer = writer_wg;
       const int64_t my_slot = tid < E ? a.e2s[tid] : -1;
       if (a.rt.logits != nullptr) {
         constexpr int TPW = TopkGroup<RG, 1>::kTokens;
@@ -378,7 +382,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
         l.hdr = hdr_l;
         l.ranges = rr_l;
         l.sorted_f = sf_l;
-        if (static_cast<int>(blockIdx.x) == a.sh.gateup_blocks) {
+        if (writer_wg) {
           g.w = a.rt.w_out;
           g.ids = a.rt.ids_out;
           g.hdr = a.rb.hdr;
@@ -397,17 +401,24 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
       sorted = sf_l;
     }
   }
-  WorkItem it;
-  const int groups4 = (tiles + kExpertWaves - 1) / kExpertWaves;
-  if (!work_item<typename Elem<DT>::S, W>(a, a.sh.gateup_blocks, groups, groups4, it, hdr, ranges)) return;
-  const int praw = it.tg * W + wave;
-  const bool owner = praw < tiles;
-  const int p = owner ? praw : tiles - 1;
   __shared__ u32x4 lds_all[W][2 * kTileSlots];
   __shared__ u32x4 bsh[2 * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
-  if (kMulti && it.nr > 1) gateup_item<0, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
-  else gateup_item<kNonTemporal, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
+  const int nitems = P ? a.gu_items : static_cast<int>(blockIdx.x) + 1;
+  for (int b = blockIdx.x; b < nitems; b += gridDim.x) {
+    const int Iw = b < a.sh.gateup_blocks ? a.sh.I : a.I;
+    const int tiles = Iw / kRowTile;
+    const int groups = (tiles + W - 1) / W;
+    const int groups4 = (tiles + kExpertWaves - 1) / kExpertWaves;
+    WorkItem it;
+    if (!work_item<typename Elem<DT>::S, W>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr, ranges))
+      continue;
+    const int praw = it.tg * W + wave;
+    const bool owner = praw < tiles;
+    const int p = owner ? praw : tiles - 1;
+    if (kMulti && it.nr > 1) gateup_item<0, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
+    else gateup_item<kNonTemporal, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
+  }
 }
 
 // The token passes of one down workgroup with MT token tiles per pass: wave `wave` owns W2
@@ -919,15 +930,44 @@ hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Resident 4-wave expert workgroups of the current device: two per CU (their launch bounds).
+static int resident_slots() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 512;
+  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  const int slots = 2 * cus;
+  if (dev < 64) cached[dev] = slots;
+  return slots;
+}
+
 // Gate/up launch of W waves per workgroup (fewer waves only for batches of at most two
-// token tiles with every expert one token range: the grids that can leave CUs idle).
+// token tiles with every expert one token range: the grids that can leave CUs idle). A
+// 4-wave grid with more items than one residency of the chip (a.gu_items > 0 asks for it)
+// runs as G workgroups that walk ceil(items / G) items each (G a multiple of 8, so that every
+// workgroup stays on one XCD's items), when such a G keeps at least 7/8 of the slots busy.
 template <bool kMulti, int DT, int MT, int RG, bool RM>
 static void launch_gateup_w(const ExpertArgs& a, int max_ranges, hipStream_t s) {
   auto go = [&](auto wc) {
     constexpr int W = decltype(wc)::value;
     const int64_t groups = (a.I / kRowTile + W - 1) / W;
-    const unsigned blocks = static_cast<unsigned>(a.sh.gateup_blocks + max_ranges * groups);
-    gateup_kernel<kMulti, DT, MT, RG, RM, W><<<blocks, W * kWave, 0, s>>>(a);
+    const int64_t items = a.sh.gateup_blocks + max_ranges * groups;
+    const int slots = resident_slots();
+    if constexpr (W == kExpertWaves) {
+      // the fewest workgroups that walk equal item counts, if that keeps 7/8 of the slots busy
+      const int64_t per = (items + slots - 1) / slots;
+      const int64_t g = ((items + per - 1) / per + 7) / 8 * 8;
+      if (a.gu_items > 0 && items > slots && 8 * g >= 7 * static_cast<int64_t>(slots)) {
+        ExpertArgs b = a;
+        b.gu_items = static_cast<int>(items);
+        gateup_kernel<kMulti, DT, MT, RG, RM, W, true><<<static_cast<unsigned>(g), W * kWave, 0, s>>>(b);
+        return;
+      }
+    }
+    gateup_kernel<kMulti, DT, MT, RG, RM, W><<<static_cast<unsigned>(items), W * kWave, 0, s>>>(a);
   };
   if constexpr (!kMulti && MT <= 2) {
     if (a.gu_waves == 1) return go(std::integral_constant<int, 1>{});

@@ -117,6 +117,8 @@ struct ExpertArgs {
   int gu_waves;         // waves per gate/up workgroup: kExpertWaves, or 2 or 1 (more, smaller
                         // workgroups for grids that would leave CUs idle); sh.gateup_blocks and
                         // the launch's grid follow it
+  int gu_items;         // host: nonzero lets a gate/up grid larger than one residency of the
+                        // chip run as workgroups that walk several items; kernel: the item count
   InRoute rt;           // used by the gate/up launch with routing inside (route_g > 0)
   SharedArgs sh;
 };

@@ -142,6 +142,25 @@ def gateup_waves(waves: Optional[int]) -> Iterator[None]:
         set_gateup_waves(prev)
 
 
+def set_gateup_item_walk(on: bool) -> bool:
+    """Let gate/up grids larger than one residency of the chip run as workgroups that walk
+    several work items (default) or launch one workgroup per item. Outputs do not depend on
+    it. Returns the previous setting. Process-wide."""
+    prev = bool(_lib.lib().smx_gateup_item_walk())
+    _lib.call("smx_set_gateup_item_walk", 1 if on else 0)
+    return prev
+
+
+@contextlib.contextmanager
+def gateup_item_walk(on: bool) -> Iterator[None]:
+    """Scope a set_gateup_item_walk setting (restored on exit)."""
+    prev = set_gateup_item_walk(on)
+    try:
+        yield
+    finally:
+        set_gateup_item_walk(prev)
+
+
 def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:
     H = hidden_states.shape[1]
     _, page_size = w1.shape

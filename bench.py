@@ -112,6 +112,9 @@ def parse():
     ap.add_argument("--gateup-waves", type=int, default=None, choices=[0, 1, 2, 4],
                     help="waves per workgroup of the weight-streaming gate/up kernel (0 = the "
                          "library's rule)")
+    ap.add_argument("--gateup-item-walk", type=int, default=None, choices=[0, 1],
+                    help="gate/up grids beyond one residency as workgroups walking several items "
+                         "(1, the library's default) or one workgroup per item (0)")
     ap.add_argument("--library-gemm", action="store_true",
                     help="only time torch.matmul (the ROCm library GEMM) on one expert's dense "
                          "gate/up and down shapes, the practical reference for the tiled kernels")
@@ -533,6 +536,8 @@ def main():
                    L.smx_set_fused_down_max_tokens(args.fused_down_max_tokens))
     if args.gateup_waves is not None:
         _lib.check("smx_set_gateup_waves", L.smx_set_gateup_waves(args.gateup_waves))
+    if args.gateup_item_walk is not None:
+        _lib.check("smx_set_gateup_item_walk", L.smx_set_gateup_item_walk(args.gateup_item_walk))
     g = torch.Generator(device=dev).manual_seed(0)
     es = DTYPES[args.dtype][1]
     page_bytes = 3 * args.hidden * args.ffn * es

@@ -340,6 +340,19 @@ int smx_set_gateup_waves(int waves);
 int smx_gateup_waves(void);
 
 /*
+ * Gate/up grids of the weight-streaming path with more workgroups than the chip holds at once
+ * (two per CU) run, with `on` (the default), as a grid of at most that many workgroups that each
+ * walk several work items in turn: the routing done inside the launch (small batches) then runs
+ * once per workgroup instead of once per item, and each later item starts with its weight
+ * loads. 0 launches one workgroup per item. Outputs are identical either way (same items, same
+ * per-wave K walk). Process-wide, like smx_set_tiled_min_tokens.
+ * Part of the expert-kernel configuration that replaces the reference's per-call Triton grid
+ * (specmoe/layers/fused_moe_kernel.py:293-306).
+ */
+int smx_set_gateup_item_walk(int on);
+int smx_gateup_item_walk(void);
+
+/*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records
  * events[0] before routing and events[1..4] after the routing, gate/up, down and combine
  * kernels, on the call's stream; `events` = NULL (count 0) turns it off. Process-wide and

@@ -1,14 +1,14 @@
-"""Waves per gate/up workgroup (4, 2, 1): the grid changes, the per-wave work and K walk do
-not, so every setting gives the same bits -- routing from logits inside the gate/up launch or
-from the routing kernels, caller ids, shared-expert blocks -- and matches the oracle, through
-the C ABI."""
+"""Gate/up grid shapes: waves per workgroup (4, 2, 1) and workgroups walking several items. The
+grid changes, the per-wave work and K walk do not, so every setting gives the same bits --
+routing from logits inside the gate/up launch or from the routing kernels, caller ids,
+shared-expert blocks -- and matches the oracle, through the C ABI."""
 import numpy as np
 import pytest
 import torch
 
 from oracle import moe_ref as ref
-from ae_amd.layers import (fused_moe_forward, fused_moe_shared_forward, gateup_waves,
-                           routing_in_gateup, stack_fused_moe)
+from ae_amd.layers import (fused_moe_forward, fused_moe_shared_forward, gateup_item_walk,
+                           gateup_waves, routing_in_gateup, stack_fused_moe)
 from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, parity, to_oracle
 
 pytestmark = pytest.mark.gpu
@@ -102,3 +102,56 @@ def test_caller_ids_same_bits_every_waves():
     y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
                                 w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
     parity(f32_of(outs[1][0]), y_ref, TOL[dtype], case="caller ids gate/up waves 1")
+
+
+def _each_walk(fn):
+    outs = {}
+    for on in (True, False):
+        with gateup_item_walk(on):
+            outs[on] = fn()
+        torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("in_launch", [True, False])
+@pytest.mark.parametrize("T,H,I,E,k", [
+    (32, 256, 8192, 8, 2),    # ~1000 gate/up items on 512 slots, routing inside the launch
+    (64, 256, 4096, 16, 4),   # four token tiles: the top-k launch, the sort in the gate/up launch
+    (130, 256, 4096, 8, 2),   # experts over several token ranges (records from the routing kernel)
+])
+def test_item_walk_same_bits(in_launch, T, H, I, E, k):
+    """Gate/up grids larger than one residency: walking several items per workgroup gives the
+    same bits as one workgroup per item, and matches the oracle."""
+    dtype = torch.bfloat16
+    x, logits = _inputs(T, H, E, dtype, seed=T + I)
+    pool, slots = make_pool(E, H, I, dtype, seed=E + I)
+    with routing_in_gateup(in_launch):
+        outs = _each_walk(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True,
+                                                    inplace=False, return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y, w, ids = outs[True]
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, TORCH_TO_ORACLE[dtype])
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    parity(f32_of(y), y_ref, TOL[dtype], case=f"item walk T={T} I={I} E={E}")
+
+
+def test_item_walk_shared_block_same_bits():
+    """DeepSeek-V2-Lite-like block at 32 tokens (shared-expert items first, then routed)."""
+    T, H, I, E, k, Is = 32, 256, 1536, 64, 6, 3072
+    dtype = torch.bfloat16
+    x, logits = _inputs(T, H, E, dtype, seed=91)
+    pool, slots = make_pool(E, H, I, dtype, seed=92)
+    g = torch.Generator(device=DEV).manual_seed(93)
+    page = (torch.randn(3 * Is * H, generator=g, device=DEV) * 0.02).to(dtype)
+    outs = _each_walk(lambda: fused_moe_shared_forward(
+        x.clone(), logits, pool, slots, k, False, page, None, 1.0, inplace=False,
+        return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y_ref, _, _ = ref.fused_moe_shared_forward(
+        to_oracle(x), f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, False,
+        TORCH_TO_ORACLE[dtype], shared_page=to_oracle(page), shared_gate_logits=None,
+        routed_scaling_factor=1.0)
+    parity(f32_of(outs[True][0]), y_ref, TOL[dtype], case="item walk shared block T=32")
