@@ -80,6 +80,7 @@ SIGNATURES = [
     ("smx_set_gateup_item_walk", ctypes.c_int, [_i32]),
     ("smx_gateup_item_walk", _i32, []),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
+    ("smx_stream_read", ctypes.c_int, [_c_void_p, _sz, _sz, _c_void_p, _c_void_p]),
 ]
 
 _lock = threading.Lock()

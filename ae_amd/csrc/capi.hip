@@ -59,12 +59,14 @@ int g_gateup_waves = 0;
 // Gate/up grids larger than one residency of the chip run as workgroups walking several items
 // (smx_set_gateup_item_walk).
 bool g_gateup_walk = true;
-// The default rule: 4 waves per workgroup, unless that grid would leave part of the chip's
-// CUs without a workgroup (fewer workgroups than kGateupFillBlocks); then 2 or 1, whichever
-// first reaches it. Measured, us per layer, 4 / 2 / 1 waves (same box): DeepSeek-V2-Lite 2
-// tokens (286 workgroups at 4) 51.8 / 48.1 / 50.0, 1 token (176) 31.1 / 31.9 / 31.8, 4 tokens
-// (506) 73.3 / 73.9 / 82.6; Qwen1.5-MoE 1 token (176) 31.2 / 30.3 / 30.5; Mixtral 1 token
-// (448) 113.5 / 118.7 / 114.1.
+// The default rule: 4 waves per workgroup, unless the 4-wave grid has a little more than one
+// workgroup per CU (more than kChipCUs but fewer than kGateupFillBlocks): then some CUs hold two
+// of them and finish last, and 2 waves per workgroup (twice the workgroups) spread the load.
+// Measured, us per layer, 4 / 2 / 1 waves (same box): DeepSeek-V2-Lite 2 tokens (286
+// workgroups at 4) 51.8 / 48.1 / 50.0 (later 49.8 / 46.1); 1 token (176) 31.1 / 31.9 / 31.8
+// (later 30.3 / 31.1; rocprof gate/up 18.5 / 19.7 us); 4 tokens (506) 73.3 / 73.9 / 82.6;
+// Qwen1.5-MoE 1 token (176) 31.2 / 30.3 / 30.5; Mixtral 1 token (448) 113.5 / 118.7 / 114.1.
+constexpr int64_t kChipCUs = 256;
 constexpr int64_t kGateupFillBlocks = 320;
 
 // tiles: 16-row weight tiles of one routed expert; s_tiles: of the shared expert (0: none);
@@ -72,11 +74,9 @@ constexpr int64_t kGateupFillBlocks = 320;
 int gateup_waves(int64_t tiles, int64_t s_tiles, int64_t items, int64_t s_groups, int tok_tiles) {
   if (tok_tiles > 2) return kExpertWaves;
   if (g_gateup_waves > 0) return g_gateup_waves;
-  for (int w : {kExpertWaves, 2, 1}) {
-    const int64_t blocks = items * ((tiles + w - 1) / w) + s_groups * ((s_tiles + w - 1) / w);
-    if (blocks >= kGateupFillBlocks) return w;
-  }
-  return 1;
+  const int64_t blocks4 = items * ((tiles + kExpertWaves - 1) / kExpertWaves) +
+                          s_groups * ((s_tiles + kExpertWaves - 1) / kExpertWaves);
+  return blocks4 > kChipCUs && blocks4 < kGateupFillBlocks ? 2 : kExpertWaves;
 }
 
 bool fused_down(int64_t T, int64_t H, int64_t I, int64_t k, int64_t Is, int dtype) {

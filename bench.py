@@ -118,6 +118,10 @@ def parse():
     ap.add_argument("--library-gemm", action="store_true",
                     help="only time torch.matmul (the ROCm library GEMM) on one expert's dense "
                          "gate/up and down shapes, the practical reference for the tiled kernels")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="only time smx_stream_read (plain streaming reads, one launch each) at the "
+                         "sizes of the small-batch expert launches: the practical floor of a read "
+                         "of that size in one launch, and of the gate/up + down pair")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 1 GiB device copy 10 times (HBM counter calibration)")
     return ap.parse_args()
@@ -138,6 +142,57 @@ def copy_calibration():
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n,
                       "launches": 10}), flush=True)
+
+
+def read_floor(steps):
+    """Best time per launch of a plain streaming read (smx_stream_read) over workgroup sizes, at
+    the byte counts of the DeepSeek-V2-Lite block's launches at one token (gate/up 92.3 MB, down
+    46.1 MB, both 138.4 MB) and a few more; regions rotate over 4 GiB so that no launch finds its
+    bytes in a cache. Also the gate/up + down pair as two launches back to back."""
+    from ae_amd import _lib
+    L = _lib.lib()
+    pool_bytes = 4 << 30
+    # 12 regions 300 MiB apart: every read below (at most 289 MB, or the 140 MB pair) stays in
+    # its region and inside the buffer (11 * 300 MiB + 289 MB < 4 GiB)
+    regions, stride = 12, 300 << 20
+    buf = torch.empty(pool_bytes, dtype=torch.uint8, device="cuda").fill_(1)
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    base = buf.data_ptr()
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    unit = 16 << 10
+
+    def timed(launches):  # launches: list of (offset, bytes, per_wg); returns us per pass
+        for _ in range(5):
+            for off, nb, pw in launches:
+                _lib.check("smx_stream_read", L.smx_stream_read(base + off, nb, pw, sink.data_ptr(), sp))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            for off, nb, pw in launches:
+                _lib.check("smx_stream_read", L.smx_stream_read(base + off + (i % regions) * stride,
+                                                                nb, pw, sink.data_ptr(), sp))
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / steps
+
+    best = {}
+    for mb in (23.0, 46.1, 92.3, 138.4, 289.0):
+        rows = []
+        for pw in (32 << 10, 64 << 10, 128 << 10, 256 << 10):
+            nb = int(mb * 1e6) // pw * pw
+            us = timed([(0, nb, pw)])
+            rows.append({"per_workgroup_kib": pw >> 10, "workgroups": nb // pw, "us": round(us, 2),
+                         "tbs": round(nb / us / 1e6, 3)})
+        b = min(rows, key=lambda r: r["us"] / (r["workgroups"] * r["per_workgroup_kib"]))
+        best[mb] = b
+        print(json.dumps({"read_floor_mb": mb, "best": b, "all": rows}), flush=True)
+    g, d = best[92.3], best[46.1]
+    pg, pd = g["per_workgroup_kib"] << 10, d["per_workgroup_kib"] << 10
+    ng, nd = int(92.3e6) // pg * pg, int(46.1e6) // pd * pd
+    us = timed([(0, ng, pg), (ng + (1 << 20), nd, pd)])
+    print(json.dumps({"read_floor_pair_mb": [92.3, 46.1], "us": round(us, 2),
+                      "tbs": round((ng + nd) / us / 1e6, 3),
+                      "hbm_frac": round((ng + nd) / us / 1e6 / (HBM_PEAK_GBS / 1000), 4)}), flush=True)
 
 
 def library_gemm():
@@ -503,6 +558,9 @@ def main():
               "(the multi-GPU sharding of this path is a design, not a measured run)",
               file=sys.stderr)
         sys.exit(2)
+    if args.read_floor:
+        read_floor(args.steps)
+        return
     if args.copy_calibration:
         copy_calibration()
         return

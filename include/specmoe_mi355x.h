@@ -330,7 +330,8 @@ int smx_routing_in_gateup(void);
  * Waves per workgroup of the weight-streaming gate/up kernel: 4, 2 or 1 (the kernel's work is
  * the same -- one wave per 16 intermediate rows of an expert; only the grouping of waves into
  * workgroups, and with it the grid, changes), or 0 (the default rule): 4, unless that grid
- * would hold fewer than 320 workgroups, then 2 or 1, whichever first reaches 320.
+ * holds more workgroups than the chip's 256 CUs but fewer than 320 (some CUs would run two
+ * while most run one), then 2.
  * Applies to batches of at most 32 tokens; larger ones always use 4. Outputs are identical
  * for every setting (same per-wave K walk and rounding). Process-wide, like
  * smx_set_tiled_min_tokens. Part of the expert-kernel configuration that replaces the
@@ -362,6 +363,18 @@ int smx_gateup_item_walk(void);
  * 740-741, 783-784), at kernel granularity.
  */
 int smx_set_profile_events(void* const* events, int count);
+
+/*
+ * Measurement: reads `bytes` of device memory at `src` (16-byte aligned) in one launch, one
+ * 256-thread workgroup per `bytes_per_workgroup` contiguous bytes (a multiple of 16 KiB that
+ * divides `bytes`), with 16-byte non-temporal loads, four in flight per lane; `sink` (4 bytes of
+ * device memory) is written only if the data's XOR equals a fixed marker. Timed around it, this
+ * is the practical floor of a read of that size in one launch (launch, ramp and tail
+ * included), which bench.py reports beside the expert kernels' small-batch launches.
+ * No counterpart in the reference: measurement only.
+ */
+int smx_stream_read(const void* src, size_t bytes, size_t bytes_per_workgroup, void* sink,
+                    void* stream);
 
 #ifdef __cplusplus
 }
