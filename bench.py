@@ -147,14 +147,12 @@ def copy_calibration():
 def read_floor(steps):
     """Best time per launch of a plain streaming read (smx_stream_read) over workgroup sizes, at
     the byte counts of the DeepSeek-V2-Lite block's launches at one token (gate/up 92.3 MB, down
-    46.1 MB, both 138.4 MB) and a few more; regions rotate over 4 GiB so that no launch finds its
-    bytes in a cache. Also the gate/up + down pair as two launches back to back."""
+    46.1 MB, both 138.4 MB), 289 MB and 1 GiB; the source rotates over regions of a 4 GiB buffer
+    so that no launch finds its bytes in a cache. Also the gate/up + down pair as two launches
+    back to back."""
     from ae_amd import _lib
     L = _lib.lib()
     pool_bytes = 4 << 30
-    # 12 regions 300 MiB apart: every read below (at most 289 MB, or the 140 MB pair) stays in
-    # its region and inside the buffer (11 * 300 MiB + 289 MB < 4 GiB)
-    regions, stride = 12, 300 << 20
     buf = torch.empty(pool_bytes, dtype=torch.uint8, device="cuda").fill_(1)
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     base = buf.data_ptr()
@@ -162,6 +160,11 @@ def read_floor(steps):
     unit = 16 << 10
 
     def timed(launches):  # launches: list of (offset, bytes, per_wg); returns us per pass
+        # passes rotate over regions at least 300 MiB (and at least one pass) apart, as many as
+        # fit in the buffer (at most 12): no pass finds its bytes in a cache
+        span = max(off + nb for off, nb, _ in launches)
+        stride = -(-max(span, 300 << 20) // (1 << 20)) * (1 << 20)
+        regions = min(12, pool_bytes // stride)
         for _ in range(5):
             for off, nb, pw in launches:
                 _lib.check("smx_stream_read", L.smx_stream_read(base + off, nb, pw, sink.data_ptr(), sp))
@@ -176,7 +179,7 @@ def read_floor(steps):
         return e0.elapsed_time(e1) * 1000.0 / steps
 
     best = {}
-    for mb in (23.0, 46.1, 92.3, 138.4, 289.0):
+    for mb in (23.0, 46.1, 92.3, 138.4, 289.0, 1073.7):
         rows = []
         for pw in (32 << 10, 64 << 10, 128 << 10, 256 << 10):
             nb = int(mb * 1e6) // pw * pw
