@@ -10,6 +10,10 @@
  *     caller's `workspace` (size from smx_moe_workspace_size);
  *   - returns 0 on success, an SMX_ERR_* code (>= 1000) for a rejected argument, or the
  *     hipError_t of a failed launch. smx_error_string() names every code.
+ * Calls are safe from several host threads on different streams with different workspaces.
+ * The smx_set_* configuration functions are not: they set process-wide values that every
+ * later call reads without synchronisation, so change them only while no MoE call is being
+ * issued on another thread (the reference drives the MoE layer from one thread).
  *
  * Tensors are row-major and densely packed. Element types are SMX_F32 / SMX_F16 / SMX_BF16.
  *
