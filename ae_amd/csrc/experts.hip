@@ -614,6 +614,7 @@ __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(Combi
 // per-(token, 256 outputs) workgroups of combine_kernel are bound by workgroup dispatch.
 constexpr int kCombineRowThreads = 256;
 constexpr int kCombineRowOuts = 8;
+constexpr int kCombineRowBatch = 8;  // assignments whose partials are loaded together
 
 template <int DT>
 __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(CombineArgs c) {
@@ -624,23 +625,54 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
   const int t = c.T * per_t < (1 << 23) ? div_small(g, per_t, 1.0f / static_cast<float>(per_t)) : g / per_t;
   const int h = (g - t * per_t) * kCombineRowOuts;
   const int64_t idx = static_cast<int64_t>(t) * c.H + h;
-  const uint32_t vm = static_cast<uint32_t>(c.tmask[t]);
   const int64_t split_stride = static_cast<int64_t>(c.T) * c.k * c.H;
+  // The token's shared-expert partials and gate logit are loaded first, with everything else,
+  // so that the thread waits for one round of loads per split (not one per assignment).
+  const bool shared = c.block && c.part_s != nullptr;
+  const bool gated = shared && c.sgate != nullptr;
+  const float zs = gated ? load_scalar(c.sgate, c.sgate_dtype, t) : 0.0f;
+  const uint32_t vm = static_cast<uint32_t>(c.tmask[t]);
   f32x4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < c.k; ++j) {
-    if (!((vm >> j) & 1u)) continue;
-    const int64_t f = static_cast<int64_t>(t) * c.k + j;
-    const float* src = c.part + f * c.H + h;
-    f32x4 v0 = {0.f, 0.f, 0.f, 0.f}, v1 = {0.f, 0.f, 0.f, 0.f};
-    for (int sp = 0; sp < c.splits; ++sp) {
-      v0 += *reinterpret_cast<const f32x4*>(src + sp * split_stride);
-      v1 += *reinterpret_cast<const f32x4*>(src + sp * split_stride + 4);
-    }
-    const float wf = c.w[f];
+  // kCombineRowBatch assignments at a time: their weights and partials (from clamped j, in
+  // bounds: every row f = t*k + j of part exists) are loaded together, then summed over the
+  // splits in split order and added over j in order -- the arithmetic of combine_kernel.
+  for (int j0 = 0; j0 < c.k; j0 += kCombineRowBatch) {
+    const float* src0 = c.part + (static_cast<int64_t>(t) * c.k) * c.H + h;
+    float wf[kCombineRowBatch];
+    f32x4 v0[kCombineRowBatch], v1[kCombineRowBatch];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      y0[e] += round_out<DT>(v0[e] * wf, c.f16out);
-      y1[e] += round_out<DT>(v1[e] * wf, c.f16out);
+    for (int jj = 0; jj < kCombineRowBatch; ++jj) {
+      const int j = min(j0 + jj, c.k - 1);
+      wf[jj] = c.w[static_cast<int64_t>(t) * c.k + j];
+      v0[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+      v1[jj] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int sp = 0; sp < c.splits; ++sp) {
+      f32x4 a0[kCombineRowBatch], a1[kCombineRowBatch];
+#pragma unroll
+      for (int jj = 0; jj < kCombineRowBatch; ++jj) {
+        const int j = min(j0 + jj, c.k - 1);
+        const float* src = src0 + static_cast<int64_t>(j) * c.H + sp * split_stride;
+        a0[jj] = *reinterpret_cast<const f32x4*>(src);
+        a1[jj] = *reinterpret_cast<const f32x4*>(src + 4);
+      }
+      __builtin_amdgcn_sched_barrier(0);  // every load of the split issued before the first add
+#pragma unroll
+      for (int jj = 0; jj < kCombineRowBatch; ++jj) {
+        v0[jj] += a0[jj];
+        v1[jj] += a1[jj];
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < kCombineRowBatch; ++jj) {
+      const int j = j0 + jj;
+      if (j < c.k && ((vm >> j) & 1u)) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y0[e] += round_out<DT>(v0[jj][e] * wf[jj], c.f16out);
+          y1[e] += round_out<DT>(v1[jj][e] * wf[jj], c.f16out);
+        }
+      }
     }
   }
   if (c.block) {
@@ -654,7 +686,7 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
         y1[e] = Elem<DT>::round(y1[e] * c.scale);
       }
     }
-    if (c.part_s) {
+    if (shared) {
       const int64_t sstride = static_cast<int64_t>(c.T) * c.H;
       const float* src = c.part_s + static_cast<int64_t>(t) * c.H + h;
       f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
@@ -662,9 +694,8 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
         d0 += *reinterpret_cast<const f32x4*>(src + sp * sstride);
         d1 += *reinterpret_cast<const f32x4*>(src + sp * sstride + 4);
       }
-      const bool gated = c.sgate != nullptr;
       float gs = 1.0f;
-      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + __expf(-load_scalar(c.sgate, c.sgate_dtype, t))));
+      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + __expf(-zs)));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float s0 = Elem<DT>::round(d0[e]), s1 = Elem<DT>::round(d1[e]);

@@ -497,7 +497,9 @@ static int group_for(int E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 
 // assignments, between 4 and 16.
 static int route_waves(int T, int N, int tokens_per_pass) {
   const int by_tokens = (T + tokens_per_pass * kTokBatch - 1) / (tokens_per_pass * kTokBatch);
-  const int by_assign = (N + 255) / 256;
+  // one 64-assignment chunk per wave where 16 waves allow: a wave's chunks run one after
+  // another (LDS round trips and a ballot per id bit each), the waves side by side
+  const int by_assign = (N + kWave - 1) / kWave;
   int w = by_tokens > by_assign ? by_tokens : by_assign;
   return w < 4 ? 4 : (w > kRouteMaxWaves ? kRouteMaxWaves : w);
 }
