@@ -271,7 +271,15 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     // 4 tokens (368) 26.7 vs 24.4, 6 tokens (496) 38.2 vs 34.8; Qwen1.5-MoE 4 tokens (304)
     // 24.1 vs 24.1, 8 tokens (464) 27.6 vs 28.9. Full grids lose with one: Qwen1.5-MoE 16
     // tokens (704) 41.0 vs 42.2, Mixtral 32 tokens 142.9 vs 147.7.
-    if (down_split(kDownRows) < kDownFillBlocks) {
+    // Past two residencies, also one where the last round of two-tile workgroups would be at
+    // most half full: the launch then drains on half-length workgroups. Measured, two vs one:
+    // DeepSeek-V2-Lite 48 tokens (1040 workgroups) 67.4 vs 63.3, 64 (1056) 68.9 vs 65.7, 128
+    // (1088) 72.6 vs 70.7; Qwen1.5-MoE 96 (1088) 70.7 vs 69.0, 128 (1088) 70.9 vs 70.4. Below
+    // two residencies the results were mixed (Qwen1.5-MoE 32 tokens, 912: 55.3 vs 56.4;
+    // DeepSeek-V2-Lite 16, 848: 52.2 vs 49.5), and there the rule keeps two.
+    const int64_t b2 = down_split(kDownRows);
+    const int64_t last = b2 % kDownFillBlocks;
+    if (b2 < kDownFillBlocks || (b2 > 2 * kDownFillBlocks && last > 0 && 2 * last <= kDownFillBlocks)) {
       p.down_rows = 1;
       down_split(1);
     }

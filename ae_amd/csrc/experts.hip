@@ -620,7 +620,7 @@ template <int DT>
 __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(CombineArgs c) {
   // thread g owns outputs [8g, 8g + 8): token g / (H/8); T*H/8 < 2^31 (one chunk of the call)
   const int per_t = c.H / kCombineRowOuts;
-  const int g = static_cast<int>(blockIdx.x) * kCombineRowThreads + static_cast<int>(threadIdx.x);
+  const int g = static_cast<int>(blockIdx.x * blockDim.x + threadIdx.x);
   if (g >= c.T * per_t) return;
   const int t = c.T * per_t < (1 << 23) ? div_small(g, per_t, 1.0f / static_cast<float>(per_t)) : g / per_t;
   const int h = (g - t * per_t) * kCombineRowOuts;
@@ -1102,12 +1102,15 @@ hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_t
 
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s) {
   if (c.rows) {
+    // One-wave workgroups until the grid holds a few workgroups per CU: at 128 tokens of
+    // hidden 2048 the 256-thread form has 128 workgroups, half the CUs.
     const int64_t outs = static_cast<int64_t>(c.T) * c.H / kCombineRowOuts;
-    const unsigned blocks = static_cast<unsigned>((outs + kCombineRowThreads - 1) / kCombineRowThreads);
+    const int threads = outs >= static_cast<int64_t>(kCombineRowThreads) * 1024 ? kCombineRowThreads : kWave;
+    const unsigned blocks = static_cast<unsigned>((outs + threads - 1) / threads);
     switch (dtype) {
-      case kF32: combine_rows_kernel<kF32><<<blocks, kCombineRowThreads, 0, s>>>(c); break;
-      case kF16: combine_rows_kernel<kF16><<<blocks, kCombineRowThreads, 0, s>>>(c); break;
-      default: combine_rows_kernel<kBF16><<<blocks, kCombineRowThreads, 0, s>>>(c); break;
+      case kF32: combine_rows_kernel<kF32><<<blocks, threads, 0, s>>>(c); break;
+      case kF16: combine_rows_kernel<kF16><<<blocks, threads, 0, s>>>(c); break;
+      default: combine_rows_kernel<kBF16><<<blocks, threads, 0, s>>>(c); break;
     }
     return hipGetLastError();
   }
