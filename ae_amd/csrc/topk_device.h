@@ -263,6 +263,139 @@ __device__ __forceinline__ void topk_batch(const void* logits, int T, int E, int
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Top-k softmax over blocks of consecutive experts (E <= 64): lane j of a group of G lanes
+// (G = 1, 2, 4 or 8, 8G >= E) holds experts 8j .. 8j+7 of its token, so a wave computes 64/G
+// tokens per pass and most of the work is lane-local. The softmax sum adds the lane's eight
+// values pairwise, ((x0+x1)+(x2+x3))+((x4+x5)+(x6+x7)), then over the group's lanes by the
+// butterfly with offsets 1, 2, 4: the same binary tree as the 64-lane butterfly of
+// group_topk_select (expert e on lane e, offsets 1..32), whose levels past 8G add exact
+// zeros, so probabilities, picks and weights equal group_topk_select's bit for bit. Each
+// selection round takes the lane's best value (strict > over ascending experts keeps the
+// lower index) and an arg-max over the group (ties to the lower index); NaN probabilities
+// rank at -1 and picked experts at -2, as in group_topk_select.
+// ---------------------------------------------------------------------------------------
+constexpr int kBlockExperts = 8;
+
+// Lanes per token of the block form: the fewest (a power of two) whose blocks cover E <= 64.
+__host__ __device__ constexpr int block_group_for(int E) {
+  return E <= 8 ? 1 : E <= 16 ? 2 : E <= 32 ? 4 : 8;
+}
+
+template <int G, typename Op>
+__device__ __forceinline__ float lane_group_reduce(float v, Op op) {
+  if constexpr (G >= 2) v = op(v, dpp<kDppXor1>(v));
+  if constexpr (G >= 4) v = op(v, dpp<kDppXor2>(v));
+  if constexpr (G >= 8) v = op(v, dpp<kDppHalfMirror>(v));
+  return v;
+}
+
+template <int G>
+__device__ __forceinline__ void lane_group_argmax(float& bp, int& be) {
+  if constexpr (G >= 2) argmax_step<kDppXor1>(bp, be);
+  if constexpr (G >= 4) argmax_step<kDppXor2>(bp, be);
+  if constexpr (G >= 8) argmax_step<kDppHalfMirror>(bp, be);
+}
+
+// Experts 8j .. 8j+7 of token t (clamped, in-bounds loads; experts past E read -inf, a token
+// past T reads zeros).
+template <int LDT, int G>
+__device__ __forceinline__ void load_logit_block(const void* logits, int t, int T, int E,
+                                                 float (&v)[kBlockExperts]) {
+  const int j = lane_id() % G;
+  const int64_t row = static_cast<int64_t>(t < T ? t : T - 1) * E;
+#pragma unroll
+  for (int i = 0; i < kBlockExperts; ++i) {
+    const int e = kBlockExperts * j + i;
+    const float x = load_as_f32<LDT>(logits, row + (e < E ? e : E - 1));
+    v[i] = e >= E ? -__builtin_inff() : (t < T ? x : 0.0f);
+  }
+}
+
+// The k picks of the lane's token, in pick order; lane j keeps picks j, j + G, ... in
+// w_out[r / G], id_out[r / G] (pick r), renormalised when asked.
+template <int G>
+__device__ __forceinline__ void block_topk_select(float (&v)[kBlockExperts], int E, int k, bool renorm,
+                                                  float (&w_out)[(kMaxTopK + G - 1) / G],
+                                                  int (&id_out)[(kMaxTopK + G - 1) / G]) {
+#pragma clang fp contract(off)
+  const int j = lane_id() % G;
+#pragma unroll
+  for (int s2 = 0; s2 < (kMaxTopK + G - 1) / G; ++s2) {
+    w_out[s2] = 0.0f;
+    id_out[s2] = -1;
+  }
+  float m = v[0];
+#pragma unroll
+  for (int i = 1; i < kBlockExperts; ++i) m = fmaxf(m, v[i]);
+  m = lane_group_reduce<G>(m, [](float a, float c) { return fmaxf(a, c); });
+  float ex[kBlockExperts];
+#pragma unroll
+  for (int i = 0; i < kBlockExperts; ++i)
+    ex[i] = kBlockExperts * j + i < E ? exp_nonpos(v[i] - m) : 0.0f;
+  float s = ((ex[0] + ex[1]) + (ex[2] + ex[3])) + ((ex[4] + ex[5]) + (ex[6] + ex[7]));
+  s = lane_group_reduce<G>(s, [](float a, float c) { return a + c; });
+  const float inv = 1.0f / s;
+  float q[kBlockExperts];
+#pragma unroll
+  for (int i = 0; i < kBlockExperts; ++i) {
+    const float pr = ex[i] * inv;
+    q[i] = (kBlockExperts * j + i < E && pr == pr) ? pr : -1.0f;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int r = 0; r < kMaxTopK; ++r) {
+    if (r >= k) break;
+    float bp = q[0];
+    int bi = 0;
+#pragma unroll
+    for (int i = 1; i < kBlockExperts; ++i)
+      if (q[i] > bp) { bp = q[i]; bi = i; }
+    int be = kBlockExperts * j + bi;
+    lane_group_argmax<G>(bp, be);
+    if (be / kBlockExperts == j) {
+#pragma unroll
+      for (int i = 0; i < kBlockExperts; ++i)
+        if (i == be % kBlockExperts) q[i] = -2.0f;
+    }
+    if (j == r % G) {
+      // the pick's probability: its rank value, or NaN where it ranked as -1
+      w_out[r / G] = bp >= 0.0f ? bp : __builtin_nanf("");
+      id_out[r / G] = be;
+    }
+    sum = (r == 0) ? bp : sum + bp;
+  }
+  if (renorm) {
+#pragma unroll
+    for (int s2 = 0; s2 < (kMaxTopK + G - 1) / G; ++s2) w_out[s2] = w_out[s2] / sum;
+  }
+}
+
+// NB consecutive passes of 64/G tokens (token t = first + b * stride for this lane's group):
+// every logit load is issued before any token is computed. fn(t, slot, w, id) is called for
+// every pick of token t < T.
+template <int LDT, int G, int NB, typename Fn>
+__device__ __forceinline__ void topk_block_batch(const void* logits, int T, int E, int k, bool renorm,
+                                                 int first, int stride, Fn&& fn) {
+  constexpr int kPer = (kMaxTopK + G - 1) / G;
+  float v[NB][kBlockExperts];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) load_logit_block<LDT, G>(logits, first + b * stride, T, E, v[b]);
+  const int j = lane_id() % G;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    float w[kPer];
+    int id[kPer];
+    block_topk_select<G>(v[b], E, k, renorm, w, id);
+    const int t = first + b * stride;
+    if (t < T) {
+#pragma unroll
+      for (int s = 0; s < kPer; ++s)
+        if (j + G * s < k) fn(t, j + G * s, w[s], id[s]);
+    }
+  }
+}
+
 struct AlignOutputs {
   // compact lists for the expert kernels (may be null)
   int32_t* hdr;         // [0] = number of work ranges, [1] = dropped-assignment flag
