@@ -626,11 +626,21 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
   const int h = (g - t * per_t) * kCombineRowOuts;
   const int64_t idx = static_cast<int64_t>(t) * c.H + h;
   const int64_t split_stride = static_cast<int64_t>(c.T) * c.k * c.H;
-  // The token's shared-expert partials and gate logit are loaded first, with everything else,
-  // so that the thread waits for one round of loads per split (not one per assignment).
+  // The token's gate logit and its shared-expert partials of the first two splits are loaded
+  // first, with the routed partials of the first split, so that the thread waits for one round
+  // of loads per routed split (not one per assignment, nor another for the shared expert's).
+  // Without a shared expert the same loads read a routed row (in bounds) and are unused.
   const bool shared = c.block && c.part_s != nullptr;
   const bool gated = shared && c.sgate != nullptr;
   const float zs = gated ? load_scalar(c.sgate, c.sgate_dtype, t) : 0.0f;
+  const int64_t sstride = static_cast<int64_t>(c.T) * c.H;
+  const float* ssrc = shared ? c.part_s + static_cast<int64_t>(t) * c.H + h
+                             : c.part + static_cast<int64_t>(t) * c.k * c.H + h;
+  const int64_t s1 = shared && c.splits_s > 1 ? sstride : 0;
+  const f32x4 ps0a = *reinterpret_cast<const f32x4*>(ssrc);
+  const f32x4 ps0b = *reinterpret_cast<const f32x4*>(ssrc + 4);
+  const f32x4 ps1a = *reinterpret_cast<const f32x4*>(ssrc + s1);
+  const f32x4 ps1b = *reinterpret_cast<const f32x4*>(ssrc + s1 + 4);
   const uint32_t vm = static_cast<uint32_t>(c.tmask[t]);
   f32x4 y0 = {0.f, 0.f, 0.f, 0.f}, y1 = {0.f, 0.f, 0.f, 0.f};
   // kCombineRowBatch assignments at a time: their weights and partials (from clamped j, in
@@ -687,12 +697,16 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
       }
     }
     if (shared) {
-      const int64_t sstride = static_cast<int64_t>(c.T) * c.H;
-      const float* src = c.part_s + static_cast<int64_t>(t) * c.H + h;
       f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < c.splits_s; ++sp) {
-        d0 += *reinterpret_cast<const f32x4*>(src + sp * sstride);
-        d1 += *reinterpret_cast<const f32x4*>(src + sp * sstride + 4);
+      d0 += ps0a;
+      d1 += ps0b;
+      if (c.splits_s > 1) {
+        d0 += ps1a;
+        d1 += ps1b;
+      }
+      for (int sp = 2; sp < c.splits_s; ++sp) {
+        d0 += *reinterpret_cast<const f32x4*>(ssrc + sp * sstride);
+        d1 += *reinterpret_cast<const f32x4*>(ssrc + sp * sstride + 4);
       }
       float gs = 1.0f;
       if (gated) gs = Elem<DT>::round(1.0f / (1.0f + __expf(-zs)));

@@ -94,12 +94,57 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
   });
   __syncthreads();
 
-  // wave 0: per-expert totals and per-wave prefixes, then exclusive scans over experts
-  // (each lane owns 4 consecutive experts), the per-wave start positions and the compact
-  // active-expert table. Every per-wave count is read at once (the array covers every wave
-  // and expert index; counts past the launched waves or past E are masked), and the start
-  // positions are written once.
-  if (wave == 0) {
+  // wave 0: per-expert totals and per-wave prefixes, then exclusive scans over experts (each
+  // lane owns one expert, or for E > 64 four consecutive ones), the per-wave start positions
+  // and the compact active-expert table. Every per-wave count is read at once (the array
+  // covers every wave and expert index; counts past the launched waves or past E are masked),
+  // and the start positions are written once.
+  if (wave == 0 && E <= kWave) {
+    // E <= 64: one expert per lane (lane e). The per-wave counts of expert e and its pool
+    // slot are read at once (consecutive lanes, consecutive words: no LDS bank conflicts);
+    // four scans over the lanes; expert e's start positions and work range records.
+    const int bm = out.bm > 0 ? out.bm : 1;
+    const int span = out.span > 0 ? out.span : 1;
+    const int e = lane;
+    const bool ve = e < E;
+    int cw[kRouteMaxWaves];
+#pragma unroll
+    for (int w = 0; w < kRouteMaxWaves; ++w) cw[w] = sh.cntw[w][e];
+    const int64_t sl = kCheckSlots ? sh.slot[e] : -1;
+    int c = 0;
+#pragma unroll
+    for (int w = 0; w < kRouteMaxWaves; ++w) {
+      const int v = (ve && w < nw) ? cw[w] : 0;
+      cw[w] = c;  // per-wave exclusive prefix, in wave order
+      c += v;
+    }
+    if (ve) sh.cnt[e] = c;
+    const int pd = div_small(c + bm - 1, bm, 1.0f / bm) * bm;
+    const int nrg = div_small(c + span - 1, span, 1.0f / span);
+    const int act = c > 0 ? 1 : 0;
+    const int ic = wave_incl_scan(c), ip = wave_incl_scan(pd), ia = wave_incl_scan(act),
+              ir = wave_incl_scan(nrg);
+    if (lane == kWave - 1) sh.nranges = ir;
+    const int bc = ic - c, bp = ip - pd;
+    // lane E (E < 64) holds the totals: experts past E count nothing
+    if (e <= E) { sh.off[e] = bc; sh.seg[e] = bp; }
+    if (E == kWave && lane == kWave - 1) { sh.off[E] = ic; sh.seg[E] = ip; }
+    if (ve) {
+#pragma unroll
+      for (int w = 0; w < kRouteMaxWaves; ++w)
+        if (w < nw) sh.cntw[w][e] = cw[w] + bc;
+      if (out.ranges && c > 0) {
+        RangeRec rec{};
+        rec.slot = sl;
+        rec.off = bc;
+        rec.cnt = c;
+        rec.key = ia - act;
+        rec.j0 = ir - nrg;
+        rec.nr = nrg;
+        for (int r = 0; r < nrg; ++r) out.ranges[rec.j0 + r] = rec;
+      }
+    }
+  } else if (wave == 0) {
     const int bm = out.bm > 0 ? out.bm : 1;
     const int span = out.span > 0 ? out.span : 1;
     int cw[4][kRouteMaxWaves];
