@@ -51,13 +51,15 @@ struct AlignShared {
   int64_t slot[kMaxExperts];              // pool slot per expert (-1: unmapped), route only
   int nranges;                            // work ranges over all experts
   int bad;                                // an assignment was dropped
+  uint32_t okbits[kMaxAssignments / 32 + 2];  // bit f: assignment f is routable (pass 1)
 };
 
 // Walks this wave's contiguous range of f in 64-wide chunks and calls fn(e, f, rank, count)
 // on every lane holding a routable assignment (e = its expert, rank = its position among the
 // chunk's assignments to e, count = their number). Assignments whose expert is unroutable
-// count as dropped.
-template <bool kCheckSlots, typename Fn>
+// count as dropped. kBits: also record which assignments are routable in sh.okbits (chunks
+// start at multiples of 64, so each chunk's ballot is two whole words).
+template <bool kCheckSlots, bool kBits = false, typename Fn>
 __device__ __forceinline__ void for_each_assignment(AlignShared& sh, int N, int E, Fn&& fn) {
   const int lane = lane_id();
   const int wave = threadIdx.x / kWave;
@@ -74,24 +76,34 @@ __device__ __forceinline__ void for_each_assignment(AlignShared& sh, int N, int 
       sh.bad = 1;
       e = -1;
     }
+    if constexpr (kBits) {
+      const uint64_t ok = ballot(e >= 0);
+      if (lane == 0) {
+        sh.okbits[base >> 5] = static_cast<uint32_t>(ok);
+        sh.okbits[(base >> 5) + 1] = static_cast<uint32_t>(ok >> 32);
+      }
+    }
     const uint64_t same = same_expert_lanes(e, e >= 0, nbits);
     if (e >= 0) fn(e, f, __popcll(same & lt_mask), __popcll(same));
   }
 }
 
 // Stable expert sort of the assignments in sh.ids. Precondition (caller): sh.cntw zeroed,
-// sh.ids (and sh.slot when kCheckSlots) written, and a barrier since.
+// sh.ids (and sh.slot when kCheckSlots) written, and a barrier since. With out.tmask, also the
+// per-token masks of routable assignments (k assignments per token).
 template <bool kCheckSlots>
-__device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& out) {
+__device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOutputs& out) {
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
   const int lane = lane_id();
   const int nw = blockDim.x / kWave;
 
   // pass 1: per-wave histograms (one writer per expert and chunk: the rank-0 lane)
-  for_each_assignment<kCheckSlots>(sh, N, E, [&](int e, int, int rank, int count) {
+  auto count_fn = [&](int e, int, int rank, int count) {
     if (rank == 0) sh.cntw[wave][e] += count;
-  });
+  };
+  if (out.tmask) for_each_assignment<kCheckSlots, true>(sh, N, E, count_fn);
+  else for_each_assignment<kCheckSlots>(sh, N, E, count_fn);
   __syncthreads();
 
   // wave 0: per-expert totals and per-wave prefixes, then exclusive scans over experts (each
@@ -212,6 +224,17 @@ __device__ void align_block(AlignShared& sh, int N, int E, const AlignOutputs& o
     if (out.hdr) { out.hdr[0] = sh.nranges; out.hdr[1] = sh.bad; }
     if (out.ntp) out.ntp[0] = sh.seg[E];
   }
+  if (out.tmask) {
+    // token t's bits t*k .. t*k+k-1 of the routable bitmap (k <= 16: at most two words; a
+    // second word past the written ones only supplies bits that are masked off)
+    const int T = N / k;
+    for (int t = tid; t < T; t += blockDim.x) {
+      const int bit = t * k;
+      const uint64_t v = static_cast<uint64_t>(sh.okbits[bit >> 5]) |
+                         (static_cast<uint64_t>(sh.okbits[(bit >> 5) + 1]) << 32);
+      out.tmask[t] = static_cast<int32_t>((v >> (bit & 31)) & ((1u << k) - 1u));
+    }
+  }
 
   // pass 2: stable scatter. Every lane reads its expert's running position before the
   // rank-0 lane advances it (one wave's LDS operations execute in program order).
@@ -264,7 +287,7 @@ __global__ __launch_bounds__(kRouteMaxThreads) void align_kernel(const int32_t* 
     if (threadIdx.x < kWave) sort_wave<false>(sh.ids, sh.slot, N, E, sw, out, AlignOutputs{});
     return;
   }
-  align_block<false>(sh, N, E, out);
+  align_block<false>(sh, N, E, 1, out);
 }
 
 // Routing for the expert kernels. With logits != null the top-k softmax runs first (results
@@ -311,8 +334,9 @@ __global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
   }
   if (threadIdx.x < E) sh.slot[threadIdx.x] = (my_slot >= 0 && my_slot < num_slots) ? my_slot : -1;
   __syncthreads();
-  if (out.tmask) {
-    // all of a token's ids, then all their slots, read at once (two LDS latencies per token)
+  if (out.tmask && E <= kWave && N <= kSortWaveMax) {
+    // the one-wave sort: all of a token's ids, then all their slots, read at once (two LDS
+    // latencies per token); align_block derives the masks from its first pass
     for (int t = threadIdx.x; t < T; t += blockDim.x) {
       int e[kMaxTopK];
 #pragma unroll
@@ -331,7 +355,7 @@ __global__ __launch_bounds__(kRouteMaxThreads) void route_kernel(
     if (threadIdx.x < kWave) sort_wave<true>(sh.ids, sh.slot, N, E, sw, out, AlignOutputs{});
     return;
   }
-  align_block<true>(sh, N, E, out);
+  align_block<true>(sh, N, E, k, out);
 }
 
 // Routing of a small batch by one wave (route_small_wave: T*k <= 64, E <= 64, T*G <= 256).
