@@ -105,6 +105,26 @@ struct WorkItem {
 // item at 4 waves), so the accumulation order of every output does not depend on W.
 // b: the work item's index in the launch (the workgroup index, or for a workgroup that walks
 // several items, the item it is on).
+// Item `local` of the nr * per_item items of one expert's nr token ranges -> (range r, weight
+// group g), numbered so that the nr ranges of weight group g are 8 items apart: workgroups are
+// dealt to the 8 XCDs round robin, so they run on one XCD, side by side, and share its L2 for
+// the rows they all read. Groups past the last multiple of 8 are numbered the same way with
+// their own count as the spacing.
+__device__ __forceinline__ void range_group(int local, int per_item, int nr, int& r, int& g) {
+  const int full = per_item / 8 * 8 * nr;
+  if (local < full) {
+    const int blk = local / (8 * nr);
+    const int in = local - blk * 8 * nr;
+    r = in / 8;
+    g = blk * 8 + (in - r * 8);
+  } else {
+    const int rem = per_item % 8;
+    const int in = local - full;
+    r = in / rem;
+    g = per_item / 8 * 8 + (in - r * rem);
+  }
+}
+
 template <typename S, int W = kExpertWaves>
 __device__ __forceinline__ bool work_item(const ExpertArgs& a, int b, int shared_blocks, int per_item,
                                           int rot_items, WorkItem& w, const int32_t* hdr,
@@ -112,16 +132,25 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int b, int shared
   const int64_t elem = static_cast<int64_t>(sizeof(S));
   const float rpi = 1.0f / static_cast<float>(per_item);  // grids hold fewer than 2^23 workgroups
   if (b < shared_blocks) {
-    const int v = div_small(b, per_item, rpi);
+    // The shared expert's token ranges all read its whole page: with several, they are numbered
+    // like a routed expert's ranges (range_group) and load with normal caching (nr > 1).
+    const int nr = a.sh.tok_groups > 1 ? a.sh.tok_groups : 1;
+    int v, g;
+    if (nr > 1) {
+      range_group(b, per_item, nr, v, g);
+    } else {
+      v = div_small(b, per_item, rpi);
+      g = b - v * per_item;
+    }
     const int span = a.rb.span;
     w.page = static_cast<const char*>(a.sh.page);
     w.page_bytes = 3 * static_cast<int64_t>(a.H) * a.sh.I * elem;
     w.I = a.sh.I;
     w.off = v * span;
     w.m = min(span, a.T - w.off);
-    w.tg = b - v * per_item;
-    w.rot = w.tg * W / kExpertWaves;
-    w.nr = 1;
+    w.tg = g;
+    w.rot = g * W / kExpertWaves;
+    w.nr = nr;
     w.shared = true;
     return true;
   }
@@ -137,26 +166,10 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int b, int shared
   const int j0 = uniform(rr.j0);
   const int nr = max(uniform(rr.nr), 1);
   const int64_t slot = uniform64(rr.slot);
-  // The expert's nr * per_item items, numbered so that the nr ranges of weight group g are 8
-  // items apart: workgroups are dealt to the 8 XCDs round robin, so they run on one XCD, side
-  // by side, and share its L2 for the rows they all read. Groups past the last multiple of 8
-  // are numbered the same way with their own count as the spacing.
+  // the expert's nr * per_item items (range_group)
   const int local = rb - j0 * per_item;
   int g = local, r = 0;
-  if (nr > 1) {
-    const int full = per_item / 8 * 8 * nr;
-    if (local < full) {
-      const int blk = local / (8 * nr);
-      const int in = local - blk * 8 * nr;
-      r = in / 8;
-      g = blk * 8 + (in - r * 8);
-    } else {
-      const int rem = per_item % 8;
-      const int in = local - full;
-      r = in / rem;
-      g = per_item / 8 * 8 + (in - r * rem);
-    }
-  }
+  if (nr > 1) range_group(local, per_item, nr, r, g);
   w.off = off + r * a.rb.span;
   w.m = min(a.rb.span, cnt - r * a.rb.span);
   w.page_bytes = a.page_elems * elem;
