@@ -365,7 +365,9 @@ struct BlockTerms {
 // tokens (512) 437.1 vs 435.3, but DeepSeek-V2-Lite 16 tokens (1024) 154.4 vs 154.3, Qwen1.5-MoE
 // 16 tokens (1024) 123.7 vs 125.0, DeepSeek-V2-Lite 32 tokens (2048) 181.7 vs 198.3. With ids
 // given (the sort alone) the layer call gains at every size: DeepSeek-V2-Lite 32 tokens 191.7
-// vs 188.8.
+// vs 188.8. The block top-k (eight experts per lane, one pass of the 4 waves for 32 tokens of
+// 64 experts) in every workgroup lost too: DeepSeek-V2-Lite 32 tokens 178.3 -> 180.0, Qwen1.5-MoE
+// 64 tokens 187.3 -> 191.6 (item walk) / 193.4 (none).
 constexpr int64_t kRouteInLaunchMax = 256;
 constexpr int64_t kRouteInLaunchTopkMax = 512;
 

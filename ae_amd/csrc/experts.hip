@@ -319,20 +319,19 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
       const int E = a.rt.E;
       const bool writer = writer_wg;
       const int64_t my_slot = tid < E ? a.e2s[tid] : -1;
+      auto keep = [&](int t, int slot, float wv, int id) {
+        const int f = t * a.k + slot;
+        if (writer) {
+          a.rt.w_out[f] = wv;
+          a.rt.ids_out[f] = id;
+        }
+        ids_l[f] = static_cast<int16_t>(id);
+      };
       if (a.rt.logits != nullptr) {
         constexpr int TPW = TopkGroup<RG, 1>::kTokens;
         const int stride = W * TPW;
-        for (int t0 = wave * TPW + lane / RG; t0 - lane / RG < a.T; t0 += stride * kTokBatch) {
-          topk_batch<DT, RG, 1>(a.rt.logits, a.T, E, a.k, a.rt.renorm != 0, t0, stride,
-                                [&](int t, int slot, float wv, int id) {
-            const int f = t * a.k + slot;
-            if (writer) {
-              a.rt.w_out[f] = wv;
-              a.rt.ids_out[f] = id;
-            }
-            ids_l[f] = static_cast<int16_t>(id);
-          });
-        }
+        for (int t0 = wave * TPW + lane / RG; t0 - lane / RG < a.T; t0 += stride * kTokBatch)
+          topk_batch<DT, RG, 1>(a.rt.logits, a.T, E, a.k, a.rt.renorm != 0, t0, stride, keep);
       } else {
         for (int f = tid; f < N; f += W * kWave) {
           const int x = a.rt.ids_in[f];

@@ -12,6 +12,7 @@ constexpr int kMaxExperts = 256;
 constexpr int kMaxExpertsPerLane = kMaxExperts / kWave;
 constexpr int kMaxAssignments = 16384;  // T * top_k
 constexpr int kMaxTopK = 16;
+constexpr int kBlockExperts = 8;        // experts per lane of the block top-k (topk_device.h)
 constexpr int kTokBatch = 1;            // wave-passes of tokens a wave computes together
 // Token passes of 64/G tokens (T * G <= 256) of the one-wave routing: each pass is a dependent
 // chain of group reductions, so beyond a few passes the multi-wave kernel is faster.

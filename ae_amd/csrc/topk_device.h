@@ -275,8 +275,6 @@ __device__ __forceinline__ void topk_batch(const void* logits, int T, int E, int
 // lower index) and an arg-max over the group (ties to the lower index); NaN probabilities
 // rank at -1 and picked experts at -2, as in group_topk_select.
 // ---------------------------------------------------------------------------------------
-constexpr int kBlockExperts = 8;
-
 // Lanes per token of the block form: the fewest (a power of two) whose blocks cover E <= 64.
 __host__ __device__ constexpr int block_group_for(int E) {
   return E <= 8 ? 1 : E <= 16 ? 2 : E <= 32 ? 4 : 8;
