@@ -312,6 +312,9 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     __shared__ RangeRec rr_l[kSortRangesMax];
     __shared__ int32_t sf_l[kSortWaveMax];
     __shared__ int32_t hdr_l[2];
+    __shared__ int32_t cnt_l[kWave];       // own-range form: routable assignments per expert
+    __shared__ int32_t wcnt_l[kExpertWaves];
+    __shared__ int32_t me_l;
     if (!in_shared) {
       const int lane = lane_id();
       const int tid = threadIdx.x;
@@ -319,6 +322,8 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
       const int E = a.rt.E;
       const bool writer = writer_wg;
       const int64_t my_slot = tid < E ? a.e2s[tid] : -1;
+      if (tid < kWave) cnt_l[tid] = 0;
+      if (tid == 0) me_l = -1;
       auto keep = [&](int t, int slot, float wv, int id) {
         const int f = t * a.k + slot;
         if (writer) {
@@ -350,20 +355,77 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
           a.rb.tmask[t] = static_cast<int32_t>(m);
         }
       }
-      if (wave == 0) {
-        AlignOutputs g{}, l{};
-        g.span = a.rb.span;
-        l.hdr = hdr_l;
-        l.ranges = rr_l;
-        l.sorted_f = sf_l;
-        if (writer) {
-          g.hdr = a.rb.hdr;
-          g.ranges = a.rb.ranges;
-          g.sorted_f = a.rb.sorted_f;
-          g.fpos = a.rb.fpos;
-          g.fslot = a.rb.fpos ? a.rb.fslot : nullptr;
+      if (P || writer) {
+        // the whole sort: the writer's records are the later kernels', and a walking workgroup
+        // takes several items
+        if (wave == 0) {
+          AlignOutputs g{}, l{};
+          g.span = a.rb.span;
+          l.hdr = hdr_l;
+          l.ranges = rr_l;
+          l.sorted_f = sf_l;
+          if (writer) {
+            g.hdr = a.rb.hdr;
+            g.ranges = a.rb.ranges;
+            g.sorted_f = a.rb.sorted_f;
+            g.fpos = a.rb.fpos;
+            g.fslot = a.rb.fpos ? a.rb.fslot : nullptr;
+          }
+          sort_wave<true>(ids_l, slot_l, N, E, sw, g, l);
         }
-        sort_wave<true>(ids_l, slot_l, N, E, sw, g, l);
+      } else {
+        // Own-range form: only the record of this workgroup's range j and its expert's sorted
+        // assignments -- the values sort_wave gives them (counts of routable assignments per
+        // expert, exclusive scans over the experts, the expert's assignments in ascending f).
+        for (int f = tid; f < N; f += W * kWave) {
+          const int e = ids_l[f];
+          if (e >= 0 && slot_l[e] >= 0) atomicAdd(&cnt_l[e], 1);
+        }
+        __syncthreads();
+        const int span = a.rb.span;
+        const int groups = (a.I / kRowTile + W - 1) / W;
+        const int j = (static_cast<int>(blockIdx.x) - a.sh.gateup_blocks) / groups;
+        if (wave == 0) {
+          const int c = lane < E ? cnt_l[lane] : 0;
+          const int nr = div_small(c + span - 1, span, 1.0f / static_cast<float>(span));
+          const int act = c > 0 ? 1 : 0;
+          const int ic = wave_incl_scan(c), ia = wave_incl_scan(act), ir = wave_incl_scan(nr);
+          if (c > 0 && j >= ir - nr && j < ir) {
+            RangeRec rec{};
+            rec.slot = slot_l[lane];
+            rec.off = ic - c;
+            rec.cnt = c;
+            rec.key = ia - act;
+            rec.j0 = ir - nr;
+            rec.nr = nr;
+            rr_l[j] = rec;  // j < the launch's range bound <= kSortRangesMax
+            me_l = lane;
+          }
+          if (lane == kWave - 1) hdr_l[0] = ir;
+        }
+        __syncthreads();
+        const int me = me_l;
+        if (me >= 0) {
+          const int off = rr_l[j].off;
+          const uint64_t below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+          int base = off;
+          for (int f0 = 0; f0 < N; f0 += W * kWave) {
+            const int f = f0 + tid;
+            const bool hit = f < N && ids_l[f] == me;
+            const uint64_t m = ballot(hit);
+            if (lane == 0) wcnt_l[wave] = __popcll(m);
+            __syncthreads();
+            int before = base, total = base;
+            for (int w = 0; w < W; ++w) {
+              const int n = wcnt_l[w];
+              if (w < wave) before += n;
+              total += n;
+            }
+            if (hit) sf_l[before + __popcll(m & below)] = f;
+            base = total;
+            __syncthreads();
+          }
+        }
       }
       __syncthreads();
       hdr = hdr_l;
