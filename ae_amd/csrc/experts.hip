@@ -472,7 +472,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     const int groups = (tiles + W - 1) / W;
     const int groups4 = (tiles + kExpertWaves - 1) / kExpertWaves;
     WorkItem it;
-    if (!work_item<typename Elem<DT>::S, W>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr, ranges))
+    if (!work_item<typename Elem<DT>::S, W, RG == 0>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr, ranges))
       continue;
     const int praw = it.tg * W + wave;
     const bool owner = praw < tiles;
@@ -560,7 +560,8 @@ __global__ __launch_bounds__(kExpertThreads, 2) void down_kernel(ExpertArgs a) {
   const int splits = in_shared ? a.sh.splits : a.splits;
   const int split_steps = in_shared ? a.sh.split_steps : a.split_steps;
   WorkItem it;
-  if (!work_item<typename Elem<DT>::S>(a, a.sh.down_blocks, groups * splits, it, a.rb.hdr, a.rb.ranges)) return;
+  if (!work_item<typename Elem<DT>::S, true>(a, a.sh.down_blocks, groups * splits, it, a.rb.hdr, a.rb.ranges))
+    return;
   const int sp = div_small(it.tg, groups, 1.0f / static_cast<float>(groups));
   const int tg = it.tg - sp * groups;
   const int rtraw = tg * kExpertWaves + wave;

@@ -50,6 +50,7 @@ struct AlignShared {
   int seg[kMaxExperts + 1];               // block-padded exclusive prefix
   int64_t slot[kMaxExperts];              // pool slot per expert (-1: unmapped), route only
   int nranges;                            // work ranges over all experts
+  int nactive;                            // experts with assignments
   int bad;                                // an assignment was dropped
   uint32_t okbits[kMaxAssignments / 32 + 2];  // bit f: assignment f is routable (pass 1)
 };
@@ -136,7 +137,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOut
     const int act = c > 0 ? 1 : 0;
     const int ic = wave_incl_scan(c), ip = wave_incl_scan(pd), ia = wave_incl_scan(act),
               ir = wave_incl_scan(nrg);
-    if (lane == kWave - 1) sh.nranges = ir;
+    if (lane == kWave - 1) { sh.nranges = ir; sh.nactive = ia; }
     const int bc = ic - c, bp = ip - pd;
     // lane E (E < 64) holds the totals: experts past E count nothing
     if (e <= E) { sh.off[e] = bc; sh.seg[e] = bp; }
@@ -191,7 +192,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOut
     }
     const int ic = wave_incl_scan(sc), ip = wave_incl_scan(sp), ia = wave_incl_scan(sa),
               ir = wave_incl_scan(sr);
-    if (lane == kWave - 1) sh.nranges = ir;
+    if (lane == kWave - 1) { sh.nranges = ir; sh.nactive = ia; }
     int bc = ic - sc, bp = ip - sp, ba = ia - sa, br = ir - sr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -221,7 +222,11 @@ __device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOut
   }
   __syncthreads();
   if (tid == 0) {
-    if (out.hdr) { out.hdr[0] = sh.nranges; out.hdr[1] = sh.bad; }
+    if (out.hdr) {
+      out.hdr[0] = sh.nranges;
+      out.hdr[1] = sh.bad;
+      out.hdr[kHdrSingleRanges] = sh.nranges == sh.nactive ? 1 : 0;
+    }
     if (out.ntp) out.ntp[0] = sh.seg[E];
   }
   if (out.tmask) {
@@ -553,6 +558,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_gate_kernel(NormGateArgs a)
       if (lane == 0) {
         a.rb.hdr[0] = __popcll(okm);
         a.rb.hdr[1] = bad ? 1 : 0;
+        a.rb.hdr[kHdrSingleRanges] = 1;
         a.rb.tmask[0] = static_cast<int32_t>(tm);
       }
     }

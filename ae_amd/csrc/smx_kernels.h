@@ -63,8 +63,11 @@ struct RangeRec {
   int32_t pad;
 };
 
+// hdr[kHdrSingleRanges] (global records only): 1 when every active expert is one work range.
+constexpr int kHdrSingleRanges = 2;
+
 struct RouteBuffers {
-  int32_t* hdr;         // [0] ranges, [1] dropped-assignment flag
+  int32_t* hdr;         // [0] ranges, [1] dropped-assignment flag, [2] one range per expert
   RangeRec* ranges;     // [max_ranges] in expert order, then range order
   int32_t* sorted_f;    // [T*k] flat assignment index f = t*k + j at each sorted position
   int32_t* tmask;       // [T] bit j set: assignment t*k+j contributes (routable expert and slot)

@@ -478,6 +478,7 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
   const int off = ic - ce, seg = ip - pad, ai = ia - act, br = ir - nr;
   const int seg_total = last_lane(ip);
   const int ranges_total = last_lane(ir);
+  const int active_total = last_lane(ia);
   const bool any_bad = ballot(bad) != 0;
   if (lane < E) {
     sc.cnt[lane] = ce;
@@ -500,7 +501,11 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
   }
   if (lane == 0) {
     sc.seg[E] = seg_total;
-    if (out.hdr) { out.hdr[0] = ranges_total; out.hdr[1] = any_bad ? 1 : 0; }
+    if (out.hdr) {
+      out.hdr[0] = ranges_total;
+      out.hdr[1] = any_bad ? 1 : 0;
+      out.hdr[kHdrSingleRanges] = ranges_total == active_total ? 1 : 0;
+    }
     if (out2.hdr) { out2.hdr[0] = ranges_total; out2.hdr[1] = any_bad ? 1 : 0; }
     if (out.ntp) out.ntp[0] = seg_total;
   }
@@ -675,7 +680,11 @@ __device__ __forceinline__ void route_small_wave(const void* logits, int T, int 
     }
   }
   if (lane == 0) {
-    if (a.hdr) { a.hdr[0] = nranges; a.hdr[1] = bad ? 1 : 0; }
+    if (a.hdr) {
+      a.hdr[0] = nranges;
+      a.hdr[1] = bad ? 1 : 0;
+      a.hdr[kHdrSingleRanges] = nranges == __popcll(first) ? 1 : 0;
+    }
     if (b.hdr) { b.hdr[0] = nranges; b.hdr[1] = bad ? 1 : 0; }
   }
 }

@@ -329,3 +329,34 @@ def test_fused_moe_custom_routing_function():
     y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
                                 w.float().cpu().numpy(), ids.int().cpu().numpy(), TORCH_TO_ORACLE[dtype])
     assert max_rel_err(f32_of(out), y_ref) <= TOL[dtype]
+
+
+# Work items in XCD order (every active expert one range, >= 32 ranges, >= 8 items per range):
+# shapes where the order applies, with and without a shared expert (whose leading workgroups
+# shift the routed ones off a multiple of 8), and one where the grid has no spare range (top-1,
+# 40 tokens over 64 experts) so the launch keeps the plain order.
+@pytest.mark.parametrize("T,E,k,Is", [(64, 64, 6, 0), (128, 64, 6, 0), (128, 60, 4, 1536),
+                                      (40, 64, 1, 0), (96, 48, 3, 512)])
+def test_many_single_range_experts(T, E, k, Is):
+    from ae_amd.layers import fused_moe_shared_forward
+    H, I = 512, 512
+    dtype = torch.bfloat16
+    x, logits = _inputs(T, H, E, dtype, seed=T * 3 + E + k)
+    pool, slots = make_pool(E, H, I, dtype, seed=E + Is)
+    if Is:
+        g = torch.Generator(device=DEV).manual_seed(T + Is)
+        page = (torch.randn(3 * Is * H, generator=g, device=DEV) * 0.02).to(dtype)
+        y, _, _ = fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page, None, 1.0,
+                                           inplace=False, return_routing=True)
+        torch.cuda.synchronize()
+        y_ref, _, _ = ref.fused_moe_shared_forward(
+            to_oracle(x), f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, False, "bf16",
+            shared_page=to_oracle(page), shared_gate_logits=None, routed_scaling_factor=1.0)
+    else:
+        with tiled_min_tokens(1 << 62):
+            y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                          return_routing=True)
+        torch.cuda.synchronize()
+        y_ref, w_ref, ids_ref = _oracle_forward(x, logits, pool, slots, k, True)
+        np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    parity(f32_of(y), y_ref, TOL[dtype], case=f"xcd order T={T} E={E} k={k} Is={Is}")
