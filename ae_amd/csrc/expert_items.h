@@ -125,7 +125,7 @@ __device__ __forceinline__ void range_group(int local, int per_item, int nr, int
   }
 }
 
-// XCD order of the routed items (kByXcd, global records): when every active expert is one range
+// XCD order of the routed items (kByXcd): when every active expert is one range
 // (hdr[kHdrSingleRanges]), at least kXcdMinRanges ranges and 8 items per range, the workgroups b
 // = x mod 8 (dealt to XCD x) run ranges x, x + 8, ... whole, and the ranges past the last
 // multiple of 8 item by item across the XCDs: an expert's token and activation rows are then
@@ -135,15 +135,42 @@ __device__ __forceinline__ void range_group(int local, int per_item, int nr, int
 // tokens, gate/up 280 -> 295 us), hence the range minimum.
 // Item q of XCD x (q = its index among the routed b = x mod 8) is range 8m + x, group g
 // (q = m * per_item + g) for q < (R/8) * per_item, else item (q - (R/8) * per_item) * 8 + x of
-// the remaining ranges. Every routed item below R * per_item is taken once when the grid holds
-// at least 8 routed workgroups past them: XCD x then has at least ceil(R * per_item / 8) routed
-// workgroups, and it needs at most that many. (Grids of one workgroup per item only.)
+// the remaining ranges. Every routed item below R * per_item is taken once when the launch's
+// items (`nitems`: its grid, or the item count of a grid walking items 8k apart) hold at least 8
+// routed items past them: XCD x then has at least ceil(R * per_item / 8) routed items, and it
+// needs at most that many.
 constexpr int kXcdMinRanges = 32;
+
+__device__ __forceinline__ bool xcd_order_applies(int single, int nranges, int per_item, int nitems,
+                                                  int shared_blocks) {
+  return single != 0 && nranges >= kXcdMinRanges && per_item >= 8 &&
+         nitems - shared_blocks - nranges * per_item >= 8;
+}
+
+// Routed item b -> (range j, weight group g) in XCD order (xcd_order_applies holds).
+__device__ __forceinline__ void xcd_order(int b, int shared_blocks, int per_item, int nranges, int& j,
+                                          int& g) {
+  const float rpi = 1.0f / static_cast<float>(per_item);
+  const int x = b & 7;
+  const int first = shared_blocks + (((x - shared_blocks) % 8) + 8) % 8;
+  const int q = (b - first) >> 3;
+  const int full = (nranges >> 3) * per_item;
+  if (q < full) {
+    const int m = div_small(q, per_item, rpi);
+    g = q - m * per_item;
+    j = 8 * m + x;
+  } else {
+    const int r = (q - full) * 8 + x;
+    const int m = div_small(r, per_item, rpi);
+    g = r - m * per_item;
+    j = (nranges & ~7) + m;
+  }
+}
 
 template <typename S, int W = kExpertWaves, bool kByXcd = false>
 __device__ __forceinline__ bool work_item(const ExpertArgs& a, int b, int shared_blocks, int per_item,
                                           int rot_items, WorkItem& w, const int32_t* hdr,
-                                          const RangeRec* ranges) {
+                                          const RangeRec* ranges, int nitems = 0) {
   const int64_t elem = static_cast<int64_t>(sizeof(S));
   const float rpi = 1.0f / static_cast<float>(per_item);  // grids hold fewer than 2^23 workgroups
   if (b < shared_blocks) {
@@ -177,23 +204,10 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int b, int shared
   bool by_xcd = false;
   int gx = 0;
   if constexpr (kByXcd) {
-    if (uniform(hdr[kHdrSingleRanges]) != 0 && nranges >= kXcdMinRanges && per_item >= 8 &&
-        static_cast<int>(gridDim.x) - shared_blocks - nranges * per_item >= 8) {
+    if (xcd_order_applies(uniform(hdr[kHdrSingleRanges]), nranges, per_item,
+                          nitems > 0 ? nitems : static_cast<int>(gridDim.x), shared_blocks)) {
       by_xcd = true;
-      const int x = b & 7;
-      const int first = shared_blocks + (((x - shared_blocks) % 8) + 8) % 8;
-      const int q = (b - first) >> 3;
-      const int full = (nranges >> 3) * per_item;
-      if (q < full) {
-        const int m = div_small(q, per_item, rpi);
-        gx = q - m * per_item;
-        j = 8 * m + x;
-      } else {
-        const int rr2 = (q - full) * 8 + x;
-        const int m = div_small(rr2, per_item, rpi);
-        gx = rr2 - m * per_item;
-        j = (nranges & ~7) + m;
-      }
+      xcd_order(b, shared_blocks, per_item, nranges, j, gx);
       if (j >= nranges) return false;
     }
   }

@@ -311,10 +311,10 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     __shared__ SortWaveLds sw;
     __shared__ RangeRec rr_l[kSortRangesMax];
     __shared__ int32_t sf_l[kSortWaveMax];
-    __shared__ int32_t hdr_l[2];
+    __shared__ int32_t hdr_l[4];
     __shared__ int32_t cnt_l[kWave];       // own-range form: routable assignments per expert
     __shared__ int32_t wcnt_l[kExpertWaves];
-    __shared__ int32_t me_l;
+    __shared__ int32_t me_l, j_l;
     if (!in_shared) {
       const int lane = lane_id();
       const int tid = threadIdx.x;
@@ -384,12 +384,12 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
         __syncthreads();
         const int span = a.rb.span;
         const int groups = (a.I / kRowTile + W - 1) / W;
-        const int j = (static_cast<int>(blockIdx.x) - a.sh.gateup_blocks) / groups;
         if (wave == 0) {
           const int c = lane < E ? cnt_l[lane] : 0;
           const int nr = div_small(c + span - 1, span, 1.0f / static_cast<float>(span));
           const int act = c > 0 ? 1 : 0;
           const int ic = wave_incl_scan(c), ia = wave_incl_scan(act), ir = wave_incl_scan(nr);
+          const int j = (static_cast<int>(blockIdx.x) - a.sh.gateup_blocks) / groups;
           if (c > 0 && j >= ir - nr && j < ir) {
             RangeRec rec{};
             rec.slot = slot_l[lane];
@@ -401,12 +401,16 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
             rr_l[j] = rec;  // j < the launch's range bound <= kSortRangesMax
             me_l = lane;
           }
-          if (lane == kWave - 1) hdr_l[0] = ir;
+          if (lane == kWave - 1) {
+            hdr_l[0] = ir;
+            hdr_l[kHdrSingleRanges] = ir == ia ? 1 : 0;
+            j_l = j;
+          }
         }
         __syncthreads();
         const int me = me_l;
         if (me >= 0) {
-          const int off = rr_l[j].off;
+          const int off = rr_l[j_l].off;
           const uint64_t below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
           int base = off;
           for (int f0 = 0; f0 < N; f0 += W * kWave) {
@@ -436,7 +440,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     __shared__ SmallRouteLds sc;
     __shared__ RangeRec rr_l[kSmallRangesMax];
     __shared__ int32_t sf_l[kWave];
-    __shared__ int32_t hdr_l[2];
+    __shared__ int32_t hdr_l[4];
     if (!in_shared) {
       if (wave == 0) {
         SmallRouteOut g, l;
@@ -472,7 +476,10 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     const int groups = (tiles + W - 1) / W;
     const int groups4 = (tiles + kExpertWaves - 1) / kExpertWaves;
     WorkItem it;
-    if (!work_item<typename Elem<DT>::S, W, RG == 0>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr, ranges))
+    // XCD order only with the routing kernel's records (inside the launch it measured slower:
+    // DeepSeek-V2-Lite 32 tokens 175.8 -> 177.0 us, Qwen1.5-MoE 32 tokens 162.4 -> 163.8)
+    if (!work_item<typename Elem<DT>::S, W, RG == 0>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr,
+                                                     ranges))
       continue;
     const int praw = it.tg * W + wave;
     const bool owner = praw < tiles;

@@ -506,7 +506,11 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
       out.hdr[1] = any_bad ? 1 : 0;
       out.hdr[kHdrSingleRanges] = ranges_total == active_total ? 1 : 0;
     }
-    if (out2.hdr) { out2.hdr[0] = ranges_total; out2.hdr[1] = any_bad ? 1 : 0; }
+    if (out2.hdr) {
+      out2.hdr[0] = ranges_total;
+      out2.hdr[1] = any_bad ? 1 : 0;
+      out2.hdr[kHdrSingleRanges] = ranges_total == active_total ? 1 : 0;
+    }
     if (out.ntp) out.ntp[0] = seg_total;
   }
   __builtin_amdgcn_wave_barrier();
@@ -685,7 +689,11 @@ __device__ __forceinline__ void route_small_wave(const void* logits, int T, int 
       a.hdr[1] = bad ? 1 : 0;
       a.hdr[kHdrSingleRanges] = nranges == __popcll(first) ? 1 : 0;
     }
-    if (b.hdr) { b.hdr[0] = nranges; b.hdr[1] = bad ? 1 : 0; }
+    if (b.hdr) {
+      b.hdr[0] = nranges;
+      b.hdr[1] = bad ? 1 : 0;
+      b.hdr[kHdrSingleRanges] = nranges == __popcll(first) ? 1 : 0;
+    }
   }
 }
 

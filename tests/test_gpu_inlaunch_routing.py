@@ -246,3 +246,30 @@ def test_repeated_caller_ids_more_ranges_than_experts():
     y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
                                 w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
     assert max_rel_err(f32_of(outs[True]), y_ref) <= TOL[torch.bfloat16]
+
+
+# Many one-range experts with at least 8 items per range (the routing kernels' records then
+# put the expert launches' items in XCD order; inside the gate/up launch the plain order stays):
+# the one-wave form (4 tokens of top-16), the multi-wave form from logits (8 tokens of top-6), its
+# caller-ids form through the top-k launch (16 tokens of top-6: the own-range routing of the
+# non-writer workgroups), and a grid that walks several items per workgroup (ffn 2048: 32 items
+# per range). Same bits as with the routing kernels, and the oracle.
+@pytest.mark.parametrize("T,H,I,E,k", [
+    (4, 256, 512, 64, 16),
+    (8, 256, 512, 64, 6),
+    (16, 256, 512, 64, 6),
+    (8, 256, 2048, 64, 6),
+])
+def test_in_launch_routing_many_experts(T, H, I, E, k):
+    dtype = torch.bfloat16
+    x, logits = _inputs(T, H, E, dtype, seed=T * 7 + I + k)
+    pool, slots = make_pool(E, H, I, dtype, seed=E + I + k)
+    outs = _both(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                           return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y, w, ids = outs[True]
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, TORCH_TO_ORACLE[dtype])
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
