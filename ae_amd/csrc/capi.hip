@@ -68,6 +68,16 @@ bool g_gateup_walk = true;
 // Qwen1.5-MoE 1 token (176) 31.2 / 30.3 / 30.5; Mixtral 1 token (448) 113.5 / 118.7 / 114.1.
 constexpr int64_t kChipCUs = 256;
 constexpr int64_t kGateupFillBlocks = 320;
+// 4-wave gate/up launches of at most two token tiles over rows of at most kGateupKSplitChunks
+// 256-byte chunks split each item's K walk between wave pairs (items of half the length: the
+// launch's last round drains in half the time), unless smx_set_gateup_waves fixes the workgroup
+// shape. Measured, us per layer, split / not (same box): DeepSeek-V2-Lite 16 tokens 149.4-149.8 /
+// 152.2-152.6 (gate/up 94.5-95.0 / 98.2-98.4), 32 tokens 175.8-176.4 / 176.5-176.6, 8 tokens
+// 121.9-122.2 / 122.6-123.5; Qwen1.5-MoE 16 and 32 tokens even. Mixtral rows (32 chunks): 8
+// tokens 321.2-322.0 / 326.7-327.1, but 16 tokens 375.7-376.5 / 364.7-365.7 and 32 tokens
+// 436.8-436.9 / 420.9-421.0 (its walking workgroups take twice the items), hence the chunk limit.
+constexpr bool kGateupKSplit = true;
+constexpr int64_t kGateupKSplitChunks = 16;
 
 // tiles: 16-row weight tiles of one routed expert; s_tiles: of the shared expert (0: none);
 // items: routed work items expected; s_groups: the shared expert's token ranges.
@@ -116,6 +126,7 @@ struct Plan {
   int split_steps = 0;
   int down_rows = kDownRows;  // W2 row tiles per down wave
   int gu_waves = kExpertWaves;  // waves per gate/up workgroup
+  bool gu_ks = false;           // gate/up K walk split between wave pairs (kGateupKSplit)
   size_t hdr = 0, ranges = 0, sorted_f = 0, w = 0, ids = 0;
   size_t tmask = 0, fpos = 0, fslot = 0;
   size_t act = 0, part = 0, total = 0;
@@ -288,6 +299,10 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     // every expert is one token range (T <= span) wherever fewer waves per workgroup apply
     if (T <= p.span)
       p.gu_waves = gateup_waves(I / kRowTile, Is / kRowTile, ex, (T + p.span - 1) / p.span, p.tok_tiles);
+    const int64_t hchunks = H * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+    p.gu_ks = kGateupKSplit && g_gateup_waves == 0 && p.gu_waves == kExpertWaves && p.tok_tiles <= 2 &&
+              hchunks % 2 == 0 && hchunks >= 4 && hchunks <= kGateupKSplitChunks;
+    const int gu_tiles = p.gu_ks ? 2 : p.gu_waves;  // weight tiles per gate/up workgroup
     if (Is > 0) {
       // its token ranges match the kernel's token-tile span
       const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
@@ -295,7 +310,7 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
       p.s_splits = static_cast<int>(ss);
       p.s_split_steps = static_cast<int>(schunks / ss * kUnroll);
       p.s_tok_groups = static_cast<int>((T + p.span - 1) / p.span);
-      p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + p.gu_waves - 1) / p.gu_waves));
+      p.s_gateup_blocks = static_cast<int>(p.s_tok_groups * ((Is / kRowTile + gu_tiles - 1) / gu_tiles));
       p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * p.down_rows) + kExpertWaves - 1) / kExpertWaves) * ss);
     }
   }
@@ -422,6 +437,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   a.split_steps = p.split_steps;
   a.down_rows = p.down_rows;
   a.gu_waves = p.gu_waves;
+  a.gu_ks = p.gu_ks ? 1 : 0;
   // the walk pays where every item's prologue would be the top-k from logits and the sort
   a.gu_items = g_gateup_walk && route_g > 0 && rt.logits != nullptr ? 1 : 0;
   a.f16out = dtype == kF32 && g_fp32_f16out ? 1 : 0;

@@ -24,9 +24,10 @@ __device__ __forceinline__ void wg_barrier() {
 // accumulation order over K is then a fixed rotation per workgroup (deterministic run to run).
 struct ChunkOrder {
   int n, rot;
+  int base = 0;  // first chunk of the walk (a K split walks chunks base .. base + n - 1)
   __device__ __forceinline__ int at(int c) const {
     const int p = c + rot;
-    return p >= n ? p - n : p;
+    return base + (p >= n ? p - n : p);
   }
 };
 

@@ -101,13 +101,13 @@ __device__ __forceinline__ void load_tokens(RawTokens<MT, W>& rb, const SharedTo
       rb.v[j][n] = __builtin_amdgcn_raw_buffer_load_b128(t.rsrc, t.off[j][n], cbase, 0);
 }
 
+// wv: the wave's index among the W waves that share the token stage.
 template <int MT, int W>
-__device__ __forceinline__ void store_tokens(const RawTokens<MT, W>& rb, u32x4* bt) {
+__device__ __forceinline__ void store_tokens(const RawTokens<MT, W>& rb, u32x4* bt, int wv) {
   const int lane = lane_id();
-  const int wave = wave_id();
 #pragma unroll
   for (int n = 0; n < 4 / W; ++n) {
-    u32x4* wr = bt + kPitch * (4 * (wave + W * n) + (lane >> 4)) + (lane & 15);
+    u32x4* wr = bt + kPitch * (4 * (wv + W * n) + (lane >> 4)) + (lane & 15);
 #pragma unroll
     for (int j = 0; j < MT; ++j) wr[j * kTileSlots] = rb.v[j][n];
   }
@@ -127,7 +127,7 @@ __device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT, W>& tne
                                         RawTokens<MT, W>& tfree, u32x4* lds, const u32x4* bt,
                                         u32x4* bt_next, const WeightStream& w,
                                         const SharedTokens<MT, W>& t, int issue_chunk,
-                                        f32x4 (&acc)[R][MT]) {
+                                        f32x4 (&acc)[R][MT], int wv) {
   const int lane = lane_id();
   u32x4* wr = lds + kPitch * (lane >> 4) + (lane & 15);
 #pragma unroll
@@ -157,7 +157,7 @@ __device__ __forceinline__ void wg_step(Raw<R>& cur, const RawTokens<MT, W>& tne
     }
   }
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (kNext) store_tokens(tnext, bt_next);
+  if constexpr (kNext) store_tokens(tnext, bt_next, wv);
   wg_barrier();
 }
 
@@ -176,30 +176,30 @@ __device__ __forceinline__ void issue_weights(Raw<R>& a, Raw<R>& b, const Weight
 template <int CP, int DT, int R, int MT, int W>
 __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTokens<MT, W>& t,
                                           const ChunkOrder& ord, u32x4* lds, u32x4* bsh,
-                                          f32x4 (&acc)[R][MT], Raw<R>& a, Raw<R>& b) {
+                                          f32x4 (&acc)[R][MT], Raw<R>& a, Raw<R>& b, int wv) {
   RawTokens<MT, W> t0, t1;
   u32x4* b0 = bsh;
   u32x4* b1 = bsh + MT * kTileSlots;
   const int nchunks = ord.n;
   load_tokens(t0, t, ord.at(0));
   if (nchunks > 1) load_tokens(t1, t, ord.at(1));
-  store_tokens(t0, b0);
+  store_tokens(t0, b0, wv);
   wg_barrier();
   int c = 0;
   for (; c + 3 < nchunks; c += 2) {
-    wg_step<CP, DT, R, MT, W, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
-    wg_step<CP, DT, R, MT, W, true, true>(b, t0, t1, lds, b1, b0, w, t, ord.at(c + 3), acc);
+    wg_step<CP, DT, R, MT, W, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc, wv);
+    wg_step<CP, DT, R, MT, W, true, true>(b, t0, t1, lds, b1, b0, w, t, ord.at(c + 3), acc, wv);
   }
   const int rem = nchunks - c;  // 1, 2 or 3 chunks left
   if (rem == 3) {
-    wg_step<CP, DT, R, MT, W, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc);
-    wg_step<CP, DT, R, MT, W, false, true>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
-    wg_step<CP, DT, R, MT, W, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, true, true>(a, t1, t0, lds, b0, b1, w, t, ord.at(c + 2), acc, wv);
+    wg_step<CP, DT, R, MT, W, false, true>(b, t0, t1, lds, b1, b0, w, t, 0, acc, wv);
+    wg_step<CP, DT, R, MT, W, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc, wv);
   } else if (rem == 2) {
-    wg_step<CP, DT, R, MT, W, false, true>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
-    wg_step<CP, DT, R, MT, W, false, false>(b, t0, t1, lds, b1, b0, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, false, true>(a, t1, t0, lds, b0, b1, w, t, 0, acc, wv);
+    wg_step<CP, DT, R, MT, W, false, false>(b, t0, t1, lds, b1, b0, w, t, 0, acc, wv);
   } else {
-    wg_step<CP, DT, R, MT, W, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc);
+    wg_step<CP, DT, R, MT, W, false, false>(a, t1, t0, lds, b0, b1, w, t, 0, acc, wv);
   }
 }
 
@@ -207,13 +207,22 @@ __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTok
 // weight-row tile p (gate rows [16p, 16p+16) and the matching up rows); `owner` is false for
 // a wave past the expert's last tile (it streams tile p again and stores nothing).
 // `sorted`: the routing's sorted flat assignments (global memory, or the workgroup's LDS copy).
-template <int CP, int DT, int MT, int W>
+// KS (4-wave workgroups): the K walk is split between wave pairs -- waves 0, 1 own tiles 2tg,
+// 2tg + 1 over the first half of the chunks, waves 2, 3 the same tiles over the second half,
+// each half with its own token stage -- and the second half's sums reach the first through LDS
+// before the epilogue: items of half the length, so a launch's last round of workgroups drains
+// in half the time. bsh then holds two stages.
+template <int CP, int DT, int MT, int W, bool KS = false>
 __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkItem& it, int p,
                                               bool owner, u32x4* lds, u32x4* bsh,
                                               const int32_t* sorted) {
   using S = typename Elem<DT>::S;
+  static_assert(!KS || W == kExpertWaves, "the K split pairs the waves of a 4-wave workgroup");
+  constexpr int WT = KS ? 2 : W;  // waves sharing one token stage
   const int lane = lane_id();
   const int wave = wave_id();
+  const int h = KS ? wave >> 1 : 0;     // K half
+  const int wv = KS ? wave & 1 : wave;  // index among the waves of the token stage
   const int r = lane & 15, g = lane >> 4;
   const int H = a.H, I = it.I, off = it.off, m = it.m;
   const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
@@ -223,21 +232,24 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   ws.tile_stride = static_cast<uint32_t>(I * row_bytes);
   ws.row4 = static_cast<uint32_t>(4 * row_bytes);
   ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
-  const ChunkOrder ord = rotated_order(static_cast<int>(row_bytes / (kStepBytes * kUnroll)), it.rot);
+  const int nch = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
+  ChunkOrder ord = rotated_order(KS ? nch / 2 : nch, it.rot);
+  ord.base = h * ord.n;
+  u32x4* stage = bsh + h * 2 * MT * kTileSlots;
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   const int f16out = it.shared ? 0 : a.f16out;
   const float rk = 1.0f / static_cast<float>(a.k);  // flat assignment f -> token f / k
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<2> wa, wb;
     issue_weights<CP>(wa, wb, ws, ord);
-    SharedTokens<MT, W> tb;
+    SharedTokens<MT, WT> tb;
     tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
     tb.base = 0;
 #pragma unroll
     for (int j = 0; j < MT; ++j)
 #pragma unroll
-      for (int n = 0; n < 4 / W; ++n) {
-        const int q = min(q0 + j * kTokTile + 4 * (wave + W * n) + (lane >> 4), m - 1);
+      for (int n = 0; n < 4 / WT; ++n) {
+        const int q = min(q0 + j * kTokTile + 4 * (wv + WT * n) + (lane >> 4), m - 1);
         const int tok = it.shared ? off + q : div_small(sorted[off + q], a.k, rk);
         tb.off[j][n] = static_cast<uint32_t>(tok * row_bytes + (lane & 15) * 16);
       }
@@ -246,11 +258,31 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
     for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<CP, DT, 2, MT, W>(ws, tb, ord, lds, bsh, acc, wa, wb);
+    stream_wg<CP, DT, 2, MT, WT>(ws, tb, ord, lds, stage, acc, wa, wb, wv);
+    if constexpr (KS) {
+      // the second half's sums into the first half's waves, through the wave tiles (wave w + 2
+      // is wave w's partner; its tile is 2 * kTileSlots slots per wave further on)
+      f32x4* red = reinterpret_cast<f32x4*>(lds);
+      if (h == 1) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) red[(i * MT + mt) * kWave + lane] = acc[i][mt];
+      }
+      wg_barrier();
+      if (h == 0) {
+        const f32x4* pr = reinterpret_cast<const f32x4*>(lds + 4 * kTileSlots);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[i][mt] = acc[i][mt] + pr[(i * MT + mt) * kWave + lane];
+      }
+      wg_barrier();  // the tiles are free for the next pass
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
-      if (owner && q < m) {
+      if (owner && h == 0 && q < m) {
         float o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -269,14 +301,14 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
 // wave of a workgroup runs the same chunks and barriers. The token tiles per pass follow
 // the item's token count (up to MT): an expert with few tokens streams its weights with
 // one tile of 16 tokens.
-template <int CP, int DT, int MT, int W>
+template <int CP, int DT, int MT, int W, bool KS = false>
 __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem& it, int p,
                                             bool owner, u32x4* lds, u32x4* bsh,
                                             const int32_t* sorted) {
-  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1, W>(a, it, p, owner, lds, bsh, sorted);
-  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1), W>(a, it, p, owner, lds, bsh, sorted);
-  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1), W>(a, it, p, owner, lds, bsh, sorted);
-  else gateup_passes<CP, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
+  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1, W, KS>(a, it, p, owner, lds, bsh, sorted);
+  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1), W, KS>(a, it, p, owner, lds, bsh, sorted);
+  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1), W, KS>(a, it, p, owner, lds, bsh, sorted);
+  else gateup_passes<CP, DT, MT, W, KS>(a, it, p, owner, lds, bsh, sorted);
 }
 
 // kMulti: the launch may hold experts split into several token ranges (T > span). Their
@@ -296,8 +328,12 @@ __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem&
 // RG > 0) is done once per workgroup, at the start, and every later item starts with its weight
 // loads instead of a routing prologue under load. Every such workgroup routes; the first writes
 // the records.
-template <bool kMulti, int DT, int MT, int RG, bool RM = false, int W = kExpertWaves, bool P = false>
+// KS: the K walk of every item is split between wave pairs (gateup_passes): a workgroup covers
+// TW = 2 weight tiles instead of W.
+template <bool kMulti, int DT, int MT, int RG, bool RM = false, int W = kExpertWaves, bool P = false,
+          bool KS = false>
 __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
+  constexpr int TW = KS ? 2 : W;  // weight tiles per workgroup
   const int wave = wave_id();
   // routing: whether this workgroup has a routed item, and whether it writes the records
   const bool in_shared = P ? false : static_cast<int>(blockIdx.x) < a.sh.gateup_blocks;
@@ -383,7 +419,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
         }
         __syncthreads();
         const int span = a.rb.span;
-        const int groups = (a.I / kRowTile + W - 1) / W;
+        const int groups = (a.I / kRowTile + TW - 1) / TW;
         if (wave == 0) {
           const int c = lane < E ? cnt_l[lane] : 0;
           const int nr = div_small(c + span - 1, span, 1.0f / static_cast<float>(span));
@@ -467,25 +503,25 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     }
   }
   __shared__ u32x4 lds_all[W][2 * kTileSlots];
-  __shared__ u32x4 bsh[2 * MT * kTileSlots];
+  __shared__ u32x4 bsh[(KS ? 4 : 2) * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
   const int nitems = P ? a.gu_items : static_cast<int>(blockIdx.x) + 1;
   for (int b = blockIdx.x; b < nitems; b += gridDim.x) {
     const int Iw = b < a.sh.gateup_blocks ? a.sh.I : a.I;
     const int tiles = Iw / kRowTile;
-    const int groups = (tiles + W - 1) / W;
+    const int groups = (tiles + TW - 1) / TW;
     const int groups4 = (tiles + kExpertWaves - 1) / kExpertWaves;
     WorkItem it;
     // XCD order only with the routing kernel's records (inside the launch it measured slower:
     // DeepSeek-V2-Lite 32 tokens 175.8 -> 177.0 us, Qwen1.5-MoE 32 tokens 162.4 -> 163.8)
-    if (!work_item<typename Elem<DT>::S, W, RG == 0>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr,
+    if (!work_item<typename Elem<DT>::S, TW, RG == 0>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr,
                                                      ranges))
       continue;
-    const int praw = it.tg * W + wave;
+    const int praw = it.tg * TW + (KS ? wave & 1 : wave);
     const bool owner = praw < tiles;
     const int p = owner ? praw : tiles - 1;
-    if (kMulti && it.nr > 1) gateup_item<0, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
-    else gateup_item<kNonTemporal, DT, MT, W>(a, it, p, owner, lds, bsh, sorted);
+    if (kMulti && it.nr > 1) gateup_item<0, DT, MT, W, KS>(a, it, p, owner, lds, bsh, sorted);
+    else gateup_item<kNonTemporal, DT, MT, W, KS>(a, it, p, owner, lds, bsh, sorted);
   }
 }
 
@@ -528,7 +564,7 @@ __device__ __forceinline__ void down_passes(const ExpertArgs& a, const WorkItem&
     for (int i = 0; i < R; ++i)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) acc[i][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    stream_wg<CP, DT, R, MT, kExpertWaves>(ws, tb, ord, lds, bsh, acc, wa, wb);
+    stream_wg<CP, DT, R, MT, kExpertWaves>(ws, tb, ord, lds, bsh, acc, wa, wb, wave);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int q = q0 + mt * kTokTile + r;
@@ -1065,9 +1101,11 @@ static int resident_slots() {
 // workgroup stays on one XCD's items), when such a G keeps at least 7/8 of the slots busy.
 template <bool kMulti, int DT, int MT, int RG, bool RM>
 static void launch_gateup_w(const ExpertArgs& a, int max_ranges, hipStream_t s) {
-  auto go = [&](auto wc) {
+  auto go = [&](auto wc, auto ksc) {
     constexpr int W = decltype(wc)::value;
-    const int64_t groups = (a.I / kRowTile + W - 1) / W;
+    constexpr bool KS = decltype(ksc)::value;
+    constexpr int TW = KS ? 2 : W;
+    const int64_t groups = (a.I / kRowTile + TW - 1) / TW;
     const int64_t items = a.sh.gateup_blocks + max_ranges * groups;
     const int slots = resident_slots();
     if constexpr (W == kExpertWaves) {
@@ -1077,17 +1115,21 @@ static void launch_gateup_w(const ExpertArgs& a, int max_ranges, hipStream_t s) 
       if (a.gu_items > 0 && items > slots && 8 * g >= 7 * static_cast<int64_t>(slots)) {
         ExpertArgs b = a;
         b.gu_items = static_cast<int>(items);
-        gateup_kernel<kMulti, DT, MT, RG, RM, W, true><<<static_cast<unsigned>(g), W * kWave, 0, s>>>(b);
+        gateup_kernel<kMulti, DT, MT, RG, RM, W, true, KS><<<static_cast<unsigned>(g), W * kWave, 0, s>>>(b);
         return;
       }
     }
-    gateup_kernel<kMulti, DT, MT, RG, RM, W><<<static_cast<unsigned>(items), W * kWave, 0, s>>>(a);
+    gateup_kernel<kMulti, DT, MT, RG, RM, W, false, KS><<<static_cast<unsigned>(items), W * kWave, 0, s>>>(a);
   };
+  using No = std::false_type;
   if constexpr (!kMulti && MT <= 2) {
-    if (a.gu_waves == 1) return go(std::integral_constant<int, 1>{});
-    if (a.gu_waves == 2) return go(std::integral_constant<int, 2>{});
+    if (a.gu_waves == 1) return go(std::integral_constant<int, 1>{}, No{});
+    if (a.gu_waves == 2) return go(std::integral_constant<int, 2>{}, No{});
   }
-  go(std::integral_constant<int, kExpertWaves>{});
+  if constexpr (MT <= 2) {
+    if (a.gu_ks) return go(std::integral_constant<int, kExpertWaves>{}, std::true_type{});
+  }
+  go(std::integral_constant<int, kExpertWaves>{}, No{});
 }
 
 template <bool kMulti, int DT, int MT>

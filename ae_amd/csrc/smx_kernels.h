@@ -123,6 +123,8 @@ struct ExpertArgs {
                         // the launch's grid follow it
   int gu_items;         // host: nonzero lets a gate/up grid larger than one residency of the
                         // chip run as workgroups that walk several items; kernel: the item count
+  int gu_ks;            // 4-wave gate/up workgroups split each item's K walk between wave pairs
+                        // (2 weight tiles per workgroup; sh.gateup_blocks and the grid follow it)
   InRoute rt;           // used by the gate/up launch with routing inside (route_g > 0)
   SharedArgs sh;
 };

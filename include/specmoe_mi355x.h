@@ -335,9 +335,12 @@ int smx_routing_in_gateup(void);
  * the same -- one wave per 16 intermediate rows of an expert; only the grouping of waves into
  * workgroups, and with it the grid, changes), or 0 (the default rule): 4, unless that grid
  * holds more workgroups than the chip's 256 CUs but fewer than 320 (some CUs would run two
- * while most run one), then 2.
+ * while most run one), then 2; with 4, for batches of at most 32 tokens over hidden rows of at
+ * most 4 KB, the default also splits each item's K walk between wave pairs (two weight tiles per
+ * workgroup, the halves' fp32 sums added once before the SwiGLU: a different, fixed summation
+ * order).
  * Applies to batches of at most 32 tokens; larger ones always use 4. Outputs are identical
- * for every setting (same per-wave K walk and rounding). Process-wide, like
+ * for every setting 1, 2 and 4 (same per-wave K walk and rounding). Process-wide, like
  * smx_set_tiled_min_tokens. Part of the expert-kernel configuration that replaces the
  * reference's per-call Triton tile choice (specmoe/layers/fused_moe_kernel.py:293-306).
  */

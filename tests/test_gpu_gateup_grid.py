@@ -1,7 +1,10 @@
 """Gate/up grid shapes: waves per workgroup (4, 2, 1) and workgroups walking several items. The
-grid changes, the per-wave work and K walk do not, so every setting gives the same bits --
+grid changes, the per-wave work and K walk do not, so every forced setting gives the same bits --
 routing from logits inside the gate/up launch or from the routing kernels, caller ids,
-shared-expert blocks -- and matches the oracle, through the C ABI."""
+shared-expert blocks -- and matches the oracle, through the C ABI. The default rule may also
+split each item's K walk between wave pairs (rows of at most 16 chunks, at most 32 tokens): a
+different fixed summation order, so the default run keeps the routing bits and matches the
+oracle, and repeats its own bits."""
 import numpy as np
 import pytest
 import torch
@@ -31,9 +34,19 @@ def _each_waves(fn):
     return outs
 
 
-def _assert_same(outs):
+def _assert_same(outs, fn=None):
+    """Forced settings: the same bits. The default: the same routing bits (the trailing
+    outputs), and with `fn` its own bits again on a second call."""
     base = outs[4]
+    if fn is not None:
+        again = fn()
+        for a, b in zip(outs[None], again):
+            assert torch.equal(a, b), "default gate/up rule not deterministic"
     for w, o in outs.items():
+        if w is None:
+            for a, b in zip(base[1:], o[1:]):
+                assert torch.equal(a, b), "default gate/up rule changed the routing"
+            continue
         for a, b in zip(base, o):
             assert torch.equal(a, b), f"gate/up waves {w} differ from 4"
 
@@ -53,15 +66,17 @@ def test_fused_forward_same_bits_every_waves(dtype, in_launch, T, H, I, E, k, P)
     if P > E:
         slots[1] = P + 5  # an expert outside the pool: its assignments are dropped
     with routing_in_gateup(in_launch):
-        outs = _each_waves(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True,
-                                                     inplace=False, return_routing=True))
-    _assert_same(outs)
+        call = lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True,  # noqa: E731
+                                         inplace=False, return_routing=True)
+        outs = _each_waves(call)
+        _assert_same(outs, call)
     y, w, ids = outs[1]
     y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
                                                   slots.cpu().numpy(), k, True, TORCH_TO_ORACLE[dtype])
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
     parity(f32_of(y), y_ref, TOL[dtype], case=f"gate/up waves 1 T={T} I={I} E={E}")
+    parity(f32_of(outs[None][0]), y_ref, TOL[dtype], case=f"gate/up default T={T} I={I} E={E}")
 
 
 @pytest.mark.parametrize("T", [1, 2, 5])
@@ -75,16 +90,18 @@ def test_shared_block_same_bits_every_waves(T):
     pool, slots = make_pool(E, H, I, dtype, seed=41)
     g = torch.Generator(device=DEV).manual_seed(42)
     page = (torch.randn(3 * Is * H, generator=g, device=DEV) * 0.02).to(dtype)
-    outs = _each_waves(lambda: fused_moe_shared_forward(
+    call = lambda: fused_moe_shared_forward(  # noqa: E731
         x.clone(), logits, pool, slots, k, False, page, None, 2.5, inplace=False,
-        return_routing=True))
-    _assert_same(outs)
+        return_routing=True)
+    outs = _each_waves(call)
+    _assert_same(outs, call)
     y = outs[1][0]
     y_ref, _, _ = ref.fused_moe_shared_forward(
         to_oracle(x), f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, False,
         TORCH_TO_ORACLE[dtype], shared_page=to_oracle(page), shared_gate_logits=None,
         routed_scaling_factor=2.5)
     parity(f32_of(y), y_ref, TOL[dtype], case=f"shared block gate/up waves 1 T={T}")
+    parity(f32_of(outs[None][0]), y_ref, TOL[dtype], case=f"shared block gate/up default T={T}")
 
 
 def test_caller_ids_same_bits_every_waves():
@@ -102,6 +119,7 @@ def test_caller_ids_same_bits_every_waves():
     y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
                                 w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
     parity(f32_of(outs[1][0]), y_ref, TOL[dtype], case="caller ids gate/up waves 1")
+    parity(f32_of(outs[None][0]), y_ref, TOL[dtype], case="caller ids gate/up default")
 
 
 def _each_walk(fn):
@@ -155,3 +173,30 @@ def test_item_walk_shared_block_same_bits():
         TORCH_TO_ORACLE[dtype], shared_page=to_oracle(page), shared_gate_logits=None,
         routed_scaling_factor=1.0)
     parity(f32_of(outs[True][0]), y_ref, TOL[dtype], case="item walk shared block T=32")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("in_launch", [True, False])
+@pytest.mark.parametrize("T", [8, 16, 32])
+def test_gateup_k_split_shared_block(dtype, in_launch, T):
+    """The default rule's K split (wave pairs over the two halves of each item's K walk, summed
+    through LDS) on a DeepSeek-V2-Lite-like block whose rows it applies to (H 1024: 8 chunks in
+    bf16, 16 in fp32), against the oracle; bit-stable run to run; within tolerance of the forced
+    4-wave shape (other summation order)."""
+    H, I, E, k, Is = 1024, 256, 64, 6, 512
+    x, logits = _inputs(T, H, E, dtype, seed=300 + T)
+    pool, slots = make_pool(E, H, I, dtype, seed=301)
+    g = torch.Generator(device=DEV).manual_seed(302)
+    page = (torch.randn(3 * Is * H, generator=g, device=DEV) * 0.02).to(dtype)
+    call = lambda: fused_moe_shared_forward(  # noqa: E731
+        x.clone(), logits, pool, slots, k, False, page, None, 2.5, inplace=False,
+        return_routing=True)
+    with routing_in_gateup(in_launch):
+        outs = _each_waves(call)
+        _assert_same(outs, call)
+    y_ref, _, _ = ref.fused_moe_shared_forward(
+        to_oracle(x), f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, False,
+        TORCH_TO_ORACLE[dtype], shared_page=to_oracle(page), shared_gate_logits=None,
+        routed_scaling_factor=2.5)
+    parity(f32_of(outs[None][0]), y_ref, TOL[dtype], case=f"K split T={T} {dtype}")
+    parity(f32_of(outs[4][0]), y_ref, TOL[dtype], case=f"forced 4 waves T={T} {dtype}")
