@@ -76,8 +76,12 @@ constexpr int64_t kGateupFillBlocks = 320;
 // 121.9-122.2 / 122.6-123.5; Qwen1.5-MoE 16 and 32 tokens even. Mixtral rows (32 chunks): 8
 // tokens 321.2-322.0 / 326.7-327.1, but 16 tokens 375.7-376.5 / 364.7-365.7 and 32 tokens
 // 436.8-436.9 / 420.9-421.0 (its walking workgroups take twice the items), hence the chunk limit.
+// A grid of about one residency has no last round to shorten, and only the split's costs (two
+// token stages, the LDS sum) remain: DeepSeek-V2-Lite 1 token (176 4-wave workgroups) 31.2 /
+// 29.8, 4 tokens (~506) 73.4-74.2 / 72.7-73.2; hence the grid minimum (1.25 residencies).
 constexpr bool kGateupKSplit = true;
 constexpr int64_t kGateupKSplitChunks = 16;
+constexpr int64_t kGateupKSplitMinBlocks = 640;
 
 // tiles: 16-row weight tiles of one routed expert; s_tiles: of the shared expert (0: none);
 // items: routed work items expected; s_groups: the shared expert's token ranges.
@@ -300,8 +304,11 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     if (T <= p.span)
       p.gu_waves = gateup_waves(I / kRowTile, Is / kRowTile, ex, (T + p.span - 1) / p.span, p.tok_tiles);
     const int64_t hchunks = H * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+    const int64_t blocks4 = ex * ((I / kRowTile + kExpertWaves - 1) / kExpertWaves) +
+                            (Is > 0 ? (T + p.span - 1) / p.span * ((Is / kRowTile + kExpertWaves - 1) / kExpertWaves) : 0);
     p.gu_ks = kGateupKSplit && g_gateup_waves == 0 && p.gu_waves == kExpertWaves && p.tok_tiles <= 2 &&
-              hchunks % 2 == 0 && hchunks >= 4 && hchunks <= kGateupKSplitChunks;
+              hchunks % 2 == 0 && hchunks >= 4 && hchunks <= kGateupKSplitChunks &&
+              blocks4 >= kGateupKSplitMinBlocks;
     const int gu_tiles = p.gu_ks ? 2 : p.gu_waves;  // weight tiles per gate/up workgroup
     if (Is > 0) {
       // its token ranges match the kernel's token-tile span

@@ -180,10 +180,10 @@ def test_item_walk_shared_block_same_bits():
 @pytest.mark.parametrize("T", [8, 16, 32])
 def test_gateup_k_split_shared_block(dtype, in_launch, T):
     """The default rule's K split (wave pairs over the two halves of each item's K walk, summed
-    through LDS) on a DeepSeek-V2-Lite-like block whose rows it applies to (H 1024: 8 chunks in
-    bf16, 16 in fp32), against the oracle; bit-stable run to run; within tolerance of the forced
-    4-wave shape (other summation order)."""
-    H, I, E, k, Is = 1024, 256, 64, 6, 512
+    through LDS) on a DeepSeek-V2-Lite-like block it applies to (rows of H 512: 4 chunks in bf16,
+    8 in fp32; ffn 1408 and a shared ffn of 2816 give grids of 800+ 4-wave workgroups), against
+    the oracle; bit-stable run to run; the forced 4-wave shape (unsplit) against the oracle too."""
+    H, I, E, k, Is = 512, 1408, 64, 6, 2816
     x, logits = _inputs(T, H, E, dtype, seed=300 + T)
     pool, slots = make_pool(E, H, I, dtype, seed=301)
     g = torch.Generator(device=DEV).manual_seed(302)
@@ -200,3 +200,6 @@ def test_gateup_k_split_shared_block(dtype, in_launch, T):
         routed_scaling_factor=2.5)
     parity(f32_of(outs[None][0]), y_ref, TOL[dtype], case=f"K split T={T} {dtype}")
     parity(f32_of(outs[4][0]), y_ref, TOL[dtype], case=f"forced 4 waves T={T} {dtype}")
+    if dtype == torch.float32:
+        # the split ran: fp32 outputs of another summation order differ in low bits somewhere
+        assert not torch.equal(outs[None][0], outs[4][0])
