@@ -125,8 +125,10 @@ def routing_in_gateup(on: bool) -> Iterator[None]:
 def set_gateup_waves(waves: Optional[int]) -> Optional[int]:
     """Set the waves per workgroup of the weight-streaming gate/up kernel (4, 2 or 1; None: the
     library's rule, which uses 2 -- twice the workgroups -- when a 4-wave grid would put two
-    workgroups on some CUs and one on most). Outputs do not depend on it. Returns the previous
-    setting (None for the rule). Process-wide."""
+    workgroups on some CUs and one on most, and for many-expert blocks of hidden rows up to 4 KB
+    with grids of 1.25+ residencies splits each item's K walk between wave pairs). Outputs do
+    not depend on the forced settings 4, 2 and 1; the rule's K split sums in another fixed order.
+    Returns the previous setting (None for the rule). Process-wide."""
     prev = int(_lib.lib().smx_gateup_waves())
     _lib.call("smx_set_gateup_waves", 0 if waves is None else int(waves))
     return None if prev == 0 else prev
