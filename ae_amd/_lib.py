@@ -79,6 +79,8 @@ SIGNATURES = [
     ("smx_gateup_waves", _i32, []),
     ("smx_set_gateup_item_walk", ctypes.c_int, [_i32]),
     ("smx_gateup_item_walk", _i32, []),
+    ("smx_moe_plan_info", ctypes.c_int,
+     [_i64, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.POINTER(_i64), _i32]),
     ("smx_set_profile_events", ctypes.c_int, [ctypes.POINTER(_c_void_p), _i32]),
     ("smx_stream_read", ctypes.c_int, [_c_void_p, _sz, _sz, _c_void_p, _c_void_p]),
 ]
@@ -119,6 +121,24 @@ def lib() -> ctypes.CDLL:
                 fn.argtypes = argtypes
             _lib = handle
     return _lib
+
+
+# Fields of smx_moe_plan_info, in the order of enum smx_plan_field.
+PLAN_FIELDS = ("tiled", "fused_down", "span", "max_ranges", "tok_tiles", "splits", "split_steps",
+               "down_rows", "gateup_waves", "gateup_ksplit", "shared_splits",
+               "shared_split_steps", "shared_tok_groups", "shared_gateup_blocks",
+               "shared_down_blocks", "tile_gateup_grid", "tile_down_grid", "chunk_tokens",
+               "workspace_bytes")
+
+
+def plan_info(T: int, H: int, I: int, E: int, top_k: int, dtype: int, shared_I: int = 0) -> dict:
+    """The launch plan of a MoE call of these sizes under the current settings (host only)."""
+    out = (ctypes.c_int64 * len(PLAN_FIELDS))()
+    n = lib().smx_moe_plan_info(T, H, I, E, top_k, shared_I, dtype, out, len(PLAN_FIELDS))
+    if n >= 1000:
+        check("smx_moe_plan_info", n)
+    assert n == len(PLAN_FIELDS), f"library reports {n} plan fields, binding knows {len(PLAN_FIELDS)}"
+    return dict(zip(PLAN_FIELDS, (int(v) for v in out)))
 
 
 def check(fn: str, code: int) -> None:

@@ -1,6 +1,7 @@
 """Build recipe for libspecmoe_mi355x.so (gfx950) -- compiles in-tree, no JIT cache.
 
     python -m ae_amd.build          # or: from ae_amd.build import build_library
+    python -m ae_amd.build --changed   # recompile only sources newer than their objects
 
 Each HIP source is compiled to an object under ae_amd/_build/ (in parallel), then linked
 into ae_amd/libspecmoe_mi355x.so. hipcc cross-compiles, so this runs without a GPU.
@@ -49,11 +50,30 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build_library(verbose: bool = False) -> str:
-    """Compile all sources and link the shared library; returns its path."""
+def _stale(src: str) -> bool:
+    """The object of src is missing or older than src or any header in csrc/ or include/."""
+    obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
+    if not os.path.exists(obj):
+        return True
+    deps = [os.path.join(CSRC, src)]
+    deps += [os.path.join(CSRC, h) for h in os.listdir(CSRC) if h.endswith(".h")]
+    inc = os.path.join(os.path.dirname(PKG_DIR), "include")
+    deps += [os.path.join(inc, h) for h in os.listdir(inc) if h.endswith(".h")]
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def build_library(verbose: bool = False, changed_only: bool = False) -> str:
+    """Compile the sources (all of them, or with changed_only those whose objects are stale)
+    and link the shared library; returns its path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    with concurrent.futures.ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+    todo = [s for s in SOURCES if _stale(s)] if changed_only else list(SOURCES)
+    if todo:
+        with concurrent.futures.ThreadPoolExecutor(max_workers=len(todo)) as ex:
+            list(ex.map(_compile, todo))
+    if verbose and changed_only:
+        print(f"compiled {todo}")
+    objs = [os.path.join(BUILD_DIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
     tmp = LIB_PATH + ".tmp"
     cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -66,5 +86,5 @@ def build_library(verbose: bool = False) -> str:
 
 
 if __name__ == "__main__":
-    build_library(verbose=True)
+    build_library(verbose=True, changed_only="--changed" in sys.argv[1:])
     sys.exit(0)

@@ -21,7 +21,7 @@ namespace {
 
 using namespace smx;
 
-constexpr int kVersion = 1 * 10000 + 0 * 100 + 0;
+constexpr int kVersion = 1 * 10000 + 1 * 100 + 0;
 constexpr size_t kAlign = 256;
 // Down-projection waves to aim for: K is split into the fewest parts that give this many
 // (two per SIMD). Fewer, longer splits stream better (Mixtral T=32: 4 splits 148 us, 2 splits
@@ -519,7 +519,10 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   return SMX_OK;
 }
 
-// Per-device address of `scratch`, looked up with that device current on its first use.
+// Per-device address of `scratch`, looked up with that device current on its first use and
+// kept for the life of the process. A hipDeviceReset (or an unload of the library's code
+// object) while the library stays loaded would leave a stale address here: the no-allocation
+// entry point does not support device resets (its header says so).
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
@@ -593,6 +596,41 @@ int smx_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E, 
   return static_cast<int>(launch_align(topk_ids, static_cast<int>(numel), static_cast<int>(E),
                                        static_cast<int>(block_size), sorted_ids, expert_ids,
                                        num_tokens_post_pad, static_cast<hipStream_t>(stream)));
+}
+
+int smx_moe_plan_info(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k, int64_t shared_I,
+                      int dtype, int64_t* out, int n) {
+  if (n < 0 || (n > 0 && !out)) return SMX_ERR_INVALID_ARG;
+  int rc = check_shape(T, H, I, E, top_k, dtype);
+  if (rc != SMX_OK) return rc;
+  rc = check_shared(T, H, shared_I, dtype);
+  if (rc != SMX_OK) return rc;
+  const int64_t tc = chunk_tokens(T, H, I, top_k, shared_I, dtype);
+  const Plan p = make_plan(std::min(T, tc), H, I, E, top_k, dtype, shared_I);
+  int64_t v[SMX_PLAN_FIELDS] = {};
+  v[SMX_PLAN_TILED] = p.tiled;
+  v[SMX_PLAN_FUSED_DOWN] = p.rows;
+  v[SMX_PLAN_SPAN] = p.span;
+  v[SMX_PLAN_MAX_RANGES] = p.max_ranges;
+  v[SMX_PLAN_TOK_TILES] = p.tok_tiles;
+  v[SMX_PLAN_SPLITS] = p.splits;
+  v[SMX_PLAN_SPLIT_STEPS] = p.split_steps;
+  v[SMX_PLAN_DOWN_ROWS] = p.down_rows;
+  v[SMX_PLAN_GATEUP_WAVES] = p.gu_waves;
+  v[SMX_PLAN_GATEUP_KSPLIT] = p.gu_ks;
+  v[SMX_PLAN_SHARED_SPLITS] = p.Is > 0 ? p.s_splits : 0;
+  v[SMX_PLAN_SHARED_SPLIT_STEPS] = p.Is > 0 ? p.s_split_steps : 0;
+  v[SMX_PLAN_SHARED_TOK_GROUPS] = p.s_tok_groups;
+  v[SMX_PLAN_SHARED_GATEUP_BLOCKS] = p.s_gateup_blocks;
+  v[SMX_PLAN_SHARED_DOWN_BLOCKS] = p.s_down_blocks;
+  if (p.tiled) {
+    v[SMX_PLAN_TILE_GATEUP_GRID] = tile_grid_blocks(0, H, I, p.s_gateup_blocks, p.max_ranges, 1);
+    v[SMX_PLAN_TILE_DOWN_GRID] = tile_grid_blocks(1, H, I, p.s_down_blocks, p.max_ranges, p.splits);
+  }
+  v[SMX_PLAN_CHUNK_TOKENS] = tc;
+  v[SMX_PLAN_WORKSPACE_BYTES] = static_cast<int64_t>(workspace_for(T, H, I, E, top_k, dtype, shared_I, false));
+  for (int i = 0; i < n && i < SMX_PLAN_FIELDS; ++i) out[i] = v[i];
+  return SMX_PLAN_FIELDS;
 }
 
 size_t smx_moe_workspace_size(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k, int dtype) {

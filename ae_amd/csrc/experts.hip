@@ -19,6 +19,7 @@
 // (specmoe/layers/fused_moe_kernel.py:319-349): C1 rounded to the activation dtype (:203),
 // silu_and_mul (:337), the down GEMM scaled by the routing weight before rounding (:197-203),
 // and the fp32 top-k sum rounded once (:344-347).
+#include <atomic>
 #include <type_traits>
 
 #include "expert_items.h"
@@ -1081,16 +1082,21 @@ hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s) {
 }
 
 // Resident 4-wave expert workgroups of the current device: two per CU (their launch bounds).
+// The per-device cache is read and written by concurrent callers: relaxed atomics suffice (every
+// writer stores the same value, and a reader that sees 0 queries the device itself).
 static int resident_slots() {
-  static int cached[64] = {};
+  static std::atomic<int> cached[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 512;
-  if (dev < 64 && cached[dev] > 0) return cached[dev];
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
     cus = 256;
   const int slots = 2 * cus;
-  if (dev < 64) cached[dev] = slots;
+  if (dev < 64) cached[dev].store(slots, std::memory_order_relaxed);
   return slots;
 }
 

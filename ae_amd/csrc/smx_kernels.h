@@ -223,6 +223,9 @@ hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok
 hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
                        hipStream_t s);
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s);
+// Workgroups of a tiled launch (stage 0: gate/up, 1: down): the shared expert's leading
+// workgroups, then every work range's weight groups (down: times the K splits).
+int64_t tile_grid_blocks(int stage, int64_t H, int64_t I, int shared_blocks, int max_ranges, int splits);
 hipError_t launch_tile_gateup(int dtype, const ExpertArgs& a, int max_ranges, hipStream_t s);
 hipError_t launch_tile_down(int dtype, const ExpertArgs& a, int max_ranges, hipStream_t s);
 

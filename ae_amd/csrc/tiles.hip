@@ -172,10 +172,19 @@ struct TWalk {
   int rb0, rb1;  // per lane: LDS slot of its A and B fragments, k-group 0 / 1, tile 0
 };
 
+// Vector-memory operations a wave issues after its token DMA of a step, until the wait that
+// must see that DMA landed: the same step's weights, then the next step's DMA and weights. The
+// waits below count on this issue order (the hardware retires a wave's vector-memory loads in
+// order), so every DMA group and weight group is fenced from the compiler's scheduler by a
+// sched_barrier: without them the compiler issued the prologue's first weight loads ahead of
+// its DMA, and the prologue's wait then left the first DMA in flight at the barrier -- other
+// waves read that quarter of the first stage before it landed (stale LDS, NaN on occasion).
+constexpr int kVmAfterDma = 2 * kTATiles * 2 + kTBLoads;  // 8 + 4 + 8
+
 // One step of the 16-bit walk, for step c: its token rows are in stage `cur` and its weights in
 // the wave's tile. Step c+2's token rows go out by DMA into `dma_dst` (the stage step c-1 read)
-// and its weights into `issue_to`; after the MFMAs, step c+1's weights (`next`, loaded two steps
-// back) are written to the tile, the wave waits until step c+1's DMA has landed -- loads
+// and then its weights into `issue_to`; after the MFMAs, step c+1's weights (`next`, loaded two
+// steps back) are written to the tile, the wave waits until step c+1's DMA has landed -- loads
 // issued after it: step c+1's weights (8), step c+2's DMA (4) and weights (8) -- and the
 // workgroup meets at the barrier.
 template <int CP, int DT>
@@ -183,13 +192,14 @@ __device__ __forceinline__ void dma_step(WRegs& issue_to, const WRegs& next, WRe
                                          const u32x4* cur, u32x4* dma_dst, u32x4* wtile,
                                          const TWalk& wk, int issue, f32x4 (&acc)[kTATiles][kTBTiles]) {
   dma_t(wk.t, dma_dst, issue);
+  __builtin_amdgcn_sched_barrier(0);
   load_w<CP>(issue_to, wk.w, issue);
   __builtin_amdgcn_sched_barrier(0);
   read_frags(frag, wtile, wk.rb0, wk.rb1);
   mma_step<DT>(frag, cur, wk.rb0, wk.rb1, acc);
   __builtin_amdgcn_sched_barrier(0);
   store_w(next, wtile, wk.wa);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTATiles * 2 + kTBLoads));
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(kVmAfterDma));
   bare_barrier();
 }
 
@@ -206,12 +216,18 @@ __device__ __forceinline__ void tile_walk(const TWalk& wk, int n, u32x4* st0, u3
                                           u32x4* st2, u32x4* wtile,
                                           f32x4 (&acc)[kTATiles][kTBTiles]) {
   WRegs r0, r1, frag;
+  // issue order: step 0's DMA, its weights, step 1's DMA, its weights (kVmAfterDma after the
+  // first DMA), so that the wait before the barrier sees step 0's token rows in LDS
   dma_t(wk.t, st0, 0);
-  dma_t(wk.t, st1, min(1, n - 1));
+  __builtin_amdgcn_sched_barrier(0);
   load_w<CP>(r0, wk.w, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  dma_t(wk.t, st1, min(1, n - 1));
+  __builtin_amdgcn_sched_barrier(0);
   load_w<CP>(r1, wk.w, min(1, n - 1));
+  __builtin_amdgcn_sched_barrier(0);
   store_w(r0, wtile, wk.wa);
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTATiles * 2 + kTBLoads));  // step 0's DMA
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(kVmAfterDma));  // step 0's DMA
   bare_barrier();
   for (int c = 0;; c += 6) {
     const int l = n - 1;
@@ -253,6 +269,15 @@ __device__ __forceinline__ void tile_walk_1(const TWalk& wk, int n, u32x4* s0, u
     store_w(raw, wtile, wk.wa);
     wg_barrier();
   }
+}
+
+// The 16-bit walk ends with reloads of its last step still in flight, DMAs into its LDS stages
+// among them. The wave waits for them before it ends (after its output stores, so the wait
+// costs nothing the end of the program would not), so that no DMA of this workgroup can land
+// in LDS that a later workgroup on the CU has been given.
+template <int DT>
+__device__ __forceinline__ void drain_walk() {
+  if constexpr (DT != kF32) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 }
 
 template <int CP, int DT>
@@ -371,6 +396,7 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_gateup_kernel(ExpertAr
       store4<DT>(act, static_cast<int64_t>(it.off + q) * I + ct[i] * kRowTile + 4 * g, o[0], o[1], o[2], o[3]);
     }
   }
+  drain_walk<DT>();
 }
 
 template <int DT>
@@ -436,6 +462,13 @@ __global__ __launch_bounds__(kExpertThreads, 2) void tile_down_kernel(ExpertArgs
     for (int i = 0; i < kTATiles; ++i)
       if (own[i]) *reinterpret_cast<f32x4*>(dst + ht[i] * kRowTile + 4 * g) = acc[i][bt];
   }
+  drain_walk<DT>();
+}
+
+int64_t tile_grid_blocks(int stage, int64_t H, int64_t I, int shared_blocks, int max_ranges, int splits) {
+  const int64_t groups = stage == 0 ? (I + kTileGateCols - 1) / kTileGateCols
+                                    : (H + kTileDownRows - 1) / kTileDownRows * splits;
+  return shared_blocks + max_ranges * groups;
 }
 
 template <int DT>
@@ -450,12 +483,10 @@ static hipError_t tile_launch(int stage, const ExpertArgs& a, int max_ranges, hi
     if (odd) return hipErrorInvalidValue;
   }
   if (stage == 0) {
-    const int64_t groups = (a.I + kTileGateCols - 1) / kTileGateCols;
-    const int64_t blocks = a.sh.gateup_blocks + max_ranges * groups;
+    const int64_t blocks = tile_grid_blocks(0, a.H, a.I, a.sh.gateup_blocks, max_ranges, 1);
     tile_gateup_kernel<DT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   } else {
-    const int64_t groups = (a.H + kTileDownRows - 1) / kTileDownRows;
-    const int64_t blocks = a.sh.down_blocks + max_ranges * groups * a.splits;
+    const int64_t blocks = tile_grid_blocks(1, a.H, a.I, a.sh.down_blocks, max_ranges, a.splits);
     tile_down_kernel<DT><<<static_cast<unsigned>(blocks), kExpertThreads, 0, s>>>(a);
   }
   return hipGetLastError();

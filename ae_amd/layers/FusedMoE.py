@@ -4,11 +4,17 @@ Same constructor arguments, the same ``ws`` parameter protocol (master weights
 ``[E, 3*I_p*H]`` on the host, the GPU pool attached by the engine as ``ws.gpu_cache``), the
 same weight_loader page packing, and the same
 ``forward(hidden_states, router_logits, expert_cache_indices)``; the computation runs in
-libspecmoe_mi355x.so. Unsupported options raise NotImplementedError instead of silently
-computing something else.
+libspecmoe_mi355x.so. Routing options that would select different experts than the plain
+top-k (grouped top-k over several groups, a correction bias) raise NotImplementedError
+instead of silently computing something else. The options the reference's forward_cuda
+accepts and ignores -- ``activation``, ``apply_router_weight_on_input``, ``inplace`` and
+``no_combine`` (specmoe/layers/FusedMoE.py:155-196 always runs SiLU, weights after the down
+projection, combines and writes in place) -- are accepted and ignored the same way, with a
+one-time warning for a non-default value.
 """
 from __future__ import annotations
 
+import warnings
 from enum import Enum
 from typing import Callable, List, Optional, Tuple
 
@@ -31,6 +37,23 @@ def set_weight_attrs(weight: torch.Tensor, weight_attrs: Optional[dict]) -> None
         return
     for key, value in weight_attrs.items():
         setattr(weight, key, value)
+
+
+# Options forward_cuda ignores, as the reference's does, and their default values.
+_IGNORED_DEFAULTS = {"activation": "silu", "apply_router_weight_on_input": False,
+                     "inplace": True, "no_combine": False}
+_warned: set = set()
+
+
+def warn_ignored_options(**values) -> None:
+    """Warn once per (option, value) when an option the reference ignores is not its
+    default: the result is the SiLU, combined, in-place output regardless."""
+    for name, value in values.items():
+        if value != _IGNORED_DEFAULTS[name] and (name, repr(value)) not in _warned:
+            _warned.add((name, repr(value)))
+            warnings.warn(f"FusedMoE: {name}={value!r} is ignored, as in the reference's "
+                          "forward_cuda (SiLU, routing weights after the down projection, "
+                          "combined, in place)", RuntimeWarning, stacklevel=3)
 
 
 class FusedMoeWeightScaleSupported(Enum):
@@ -89,12 +112,9 @@ class UnquantizedFusedMoEMethod:
         pool ``layer.ws.gpu_cache`` -- here one library call."""
         check_routing_options(use_grouped_topk, topk_group, num_expert_group,
                               custom_routing_function, correction_bias, routed_scaling_factor)
-        if activation != "silu":
-            raise NotImplementedError(f"activation={activation!r} (only silu)")
-        if apply_router_weight_on_input:
-            raise NotImplementedError("apply_router_weight_on_input")
-        if no_combine:
-            raise NotImplementedError("no_combine")
+        warn_ignored_options(activation=activation,
+                             apply_router_weight_on_input=apply_router_weight_on_input,
+                             inplace=inplace, no_combine=no_combine)
         pool = getattr(layer.ws, "gpu_cache", None)
         if pool is None:
             raise RuntimeError("no expert pool attached: set ws.gpu_cache before forward")

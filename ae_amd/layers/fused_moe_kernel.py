@@ -163,6 +163,27 @@ def gateup_item_walk(on: bool) -> Iterator[None]:
         set_gateup_item_walk(prev)
 
 
+def _caller_buffers(hidden_states: torch.Tensor, inplace: bool, out: Optional[torch.Tensor],
+                    ws: Optional[torch.Tensor], nbytes: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The output and workspace of a call: the caller's when given (checked), else the input
+    itself (inplace) or a new tensor, and a workspace from the caching allocator."""
+    if out is None:
+        out = hidden_states if inplace else torch.empty_like(hidden_states)
+    else:
+        assert not inplace, "out= and inplace=True both name the output"
+        assert out.shape == hidden_states.shape and out.dtype == hidden_states.dtype, \
+            "out must match hidden_states in shape and dtype"
+        assert out.is_contiguous() and out.device == hidden_states.device, \
+            "out must be contiguous and on the device of hidden_states"
+    if ws is None:
+        ws = workspace(nbytes, hidden_states.device)
+    else:
+        assert ws.dtype == torch.uint8 and ws.is_contiguous() and ws.device == hidden_states.device, \
+            "workspace must be a contiguous uint8 tensor on the device of hidden_states"
+        assert ws.numel() >= nbytes, f"workspace holds {ws.numel()} bytes, the call needs {nbytes}"
+    return out, ws
+
+
 def _pool_geometry(hidden_states: torch.Tensor, w1: torch.Tensor) -> Tuple[int, int]:
     H = hidden_states.shape[1]
     _, page_size = w1.shape
@@ -229,12 +250,17 @@ def fused_moe_forward(
     renormalize: bool,
     inplace: bool = True,
     return_routing: bool = False,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
 ):
     """Routing (select_experts) and stack_fused_moe in one library call.
 
     Reference: the body of UnquantizedFusedMoEMethod.forward_cuda,
     specmoe/layers/FusedMoE.py:155-196 (select_experts at :174, stack_fused_moe at :187,
     inplace=True). With ``return_routing`` also returns ``(topk_weights, topk_ids)``.
+    ``out`` (with ``inplace=False``) receives the result; ``workspace`` is a caller-owned uint8
+    scratch of at least ``smx_moe_workspace_size`` bytes (default: one from torch's caching
+    allocator). Neither needs any initial contents: the call writes every byte it reads.
     """
     assert hidden_states.shape[0] == router_logits.shape[0], "Number of tokens mismatch"
     assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
@@ -245,13 +271,12 @@ def fused_moe_forward(
     H, I = _pool_geometry(hidden_states, w1)
     T, E = router_logits.shape
     logits = router_logits.contiguous()
-    out = hidden_states if inplace else torch.empty_like(hidden_states)
     slots = _as_index(indicies, torch.int64)
     dt = dtype_code(hidden_states.dtype)
     nbytes = _lib.lib().smx_moe_workspace_size(T, H, I, E, top_k, dt)
     if nbytes == 0 and T > 0:
         raise ValueError(f"unsupported MoE shape T={T} H={H} I={I} E={E} top_k={top_k}")
-    ws = workspace(nbytes, hidden_states.device)
+    out, ws = _caller_buffers(hidden_states, inplace, out, workspace, nbytes)
     w = ids = None
     if return_routing:
         w = torch.empty((T, top_k), dtype=torch.float32, device=hidden_states.device)
@@ -277,6 +302,8 @@ def fused_moe_shared_forward(
     routed_scaling_factor: float = 1.0,
     inplace: bool = True,
     return_routing: bool = False,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
 ):
     """A MoE block with an always-active shared expert, in one library call.
 
@@ -286,7 +313,8 @@ def fused_moe_shared_forward(
     ``sigmoid(shared_gate_logits)`` (``[T]`` or ``[T,1]``) or 1. The reference has no shared
     expert; this is the block of Qwen1.5-MoE (gated shared expert) and DeepSeek-V2 (ungated,
     ``n_shared * I`` columns, scaled routed output) over the routed path of
-    specmoe/layers/FusedMoE.py:155-196.
+    specmoe/layers/FusedMoE.py:155-196. ``out`` and ``workspace`` as in
+    :func:`fused_moe_forward` (the workspace size is ``smx_moe_shared_workspace_size``).
     """
     assert hidden_states.shape[0] == router_logits.shape[0], "Number of tokens mismatch"
     assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
@@ -310,14 +338,13 @@ def fused_moe_shared_forward(
             "shared-expert gate logits and router logits dtypes differ"
         sgate = shared_gate_logits.contiguous()
     logits = router_logits.contiguous()
-    out = hidden_states if inplace else torch.empty_like(hidden_states)
     slots = _as_index(indicies, torch.int64)
     dt = dtype_code(hidden_states.dtype)
     nbytes = _lib.lib().smx_moe_shared_workspace_size(T, H, I, E, top_k, Is, dt)
     if nbytes == 0 and T > 0:
         raise ValueError(f"unsupported MoE shape T={T} H={H} I={I} E={E} top_k={top_k} "
                          f"shared I={Is}")
-    ws = workspace(nbytes, hidden_states.device)
+    out, ws = _caller_buffers(hidden_states, inplace, out, workspace, nbytes)
     w = ids = None
     if return_routing:
         w = torch.empty((T, top_k), dtype=torch.float32, device=hidden_states.device)

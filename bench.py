@@ -26,7 +26,10 @@ the numpy oracle on the same inputs (ids, weight bits, both output error metrics
 baseline: a torch-CPU restatement of the same layer (GEMMs on MKL, weights converted to fp32
 once, outside the timing) on the host cores, median of >= 20 calls after 3 warm-up calls. The
 default Mixtral run also times 8, 16, 48 and 64 tokens (the rest of the metric's 8-64 range)
-with the same event-timed loop and reports them under "sweep".
+with the same event-timed loop and reports them under "sweep", and under "workloads" the other
+configurations of the benchmark's definition: c1 (fp32, with its gate/up roofline and CPU
+baseline), Mixtral at 1 and 4 tokens (unbiased gate), Qwen1.5-MoE at 64 tokens, and the
+26-layer DeepSeek-V2-Lite stack at 1, 32 and 128 tokens (parity: its first layer).
 
     python bench.py [--steps K] [--warmup W] [--tokens T] [--no-cpu] [--no-parity]
     python bench.py --workload c1
@@ -63,6 +66,18 @@ WORKLOADS = {
 }
 # The rest of the headline metric's 8-64 token range, timed beside the default Mixtral run.
 HEADLINE_SWEEP = (8, 16, 48, 64)
+# The other configurations of the benchmark's definition, timed beside the default run (the
+# same event-timed loop and weight rotation) under "workloads": name -> (workload, tokens,
+# layers, overrides of the workload's settings, CPU baseline).
+EXTRA_WORKLOADS = {
+    "c1_fp32_t32": ("c1", 32, 1, {}, True),
+    "c2_mixtral_t1": ("mixtral", 1, 1, {"zipf": 0.0}, False),
+    "c2_mixtral_t4": ("mixtral", 4, 1, {"zipf": 0.0}, False),
+    "c4_qwen15_t64": ("qwen15", 64, 1, {}, False),
+    "c5_dsv2lite_26layers_t1": ("dsv2lite", 1, 26, {}, False),
+    "c5_dsv2lite_26layers_t32": ("dsv2lite", 32, 26, {}, False),
+    "c5_dsv2lite_26layers_t128": ("dsv2lite", 128, 26, {}, False),
+}
 DTYPES = {"bf16": (torch.bfloat16, 2, 2), "fp32": (torch.float32, 4, 0)}  # torch dtype, bytes, SMX code
 
 
@@ -96,6 +111,9 @@ def parse():
     ap.add_argument("--no-parity", action="store_true", help="skip the parity check against the oracle")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the 8/16/48/64-token lines of the default Mixtral run")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the other configurations (C1, C2 at 1 and 4 tokens, Qwen1.5-MoE, "
+                         "the DeepSeek-V2-Lite stack) timed beside the default Mixtral run")
     ap.add_argument("--cpu-runs", type=int, default=20,
                     help="CPU baseline: timed layer calls (after 3 warm-up calls); the median is reported")
     ap.add_argument("--h2d", action="store_true",
@@ -544,13 +562,73 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
                 "us_per_launch": round(stage_us[1], 2),
             }
     oracle_out = None
-    parity = not args.no_parity and len(layers) == 1 and not args.layer
-    if parity or not args.no_cpu:
+    # a stack's parity is its first layer's call (every layer runs the same kernels)
+    parity = not args.no_parity and not args.layer
+    cpu = not args.no_cpu and len(layers) == 1
+    if parity or cpu:
         host = _host_inputs(args, wl, x, logits, sgate, layers[0], slots)
         if parity:
             out["parity"], oracle_out = parity_check(args, host, y_first, w_first, ids_np)
-        if not args.no_cpu:
+            if len(layers) > 1:
+                out["parity"]["scope"] = "the first layer's call of the stack"
+        if cpu:
             out["cpu_baseline"] = cpu_baseline(args, host, layer_bytes, T, oracle_out)
+    return out
+
+
+def run_workloads(args, dev, L, mixtral_layers):
+    """The other configurations of the benchmark's definition, one compact entry each: us per
+    step, algorithmic GB/s and HBM fraction from the same event-timed loop as the headline,
+    the per-kernel stages and gate/up roofline of single layers, parity against the oracle
+    (a stack: its first layer) and, for the reference's CPU-runnable configuration, the CPU
+    baseline. Weights of each workload are freed before the next one is built."""
+    keep = ("us_per_step", "layer_hbm_frac", "algorithmic_bytes", "stage_us", "roofline",
+            "parity", "cpu_baseline")
+    out = {}
+    built = {}
+    for name, (wname, T, nlayers, over, cpu) in EXTRA_WORKLOADS.items():
+        wl = WORKLOADS[wname]
+        a = argparse.Namespace(**vars(args))
+        a.workload = wname
+        for key in ("hidden", "ffn", "experts", "topk"):
+            setattr(a, key, wl[key])
+        a.dtype = wl.get("dtype", "bf16")
+        a.layers = nlayers
+        a.no_cpu = not cpu
+        a.no_parity = False
+        for key, v in over.items():
+            setattr(a, key, v)
+        if wname == "mixtral":
+            layers = mixtral_layers
+        else:
+            key = (wname, nlayers)
+            if key not in built:
+                built.clear()  # free the previous workload's weights first
+                torch.cuda.empty_cache()
+                es = DTYPES[a.dtype][1]
+                page_bytes = 3 * a.hidden * a.ffn * es
+                pool_bytes = a.experts * page_bytes + 3 * a.hidden * wl["shared_ffn"] * es
+                copies = max(2, -(-(1 << 30) // pool_bytes)) if nlayers == 1 else 1
+                g = torch.Generator(device=dev).manual_seed(0)
+                built[key] = [Layer(g, dev, a.hidden, a.ffn, a.experts, wl["shared_ffn"], copies,
+                                    DTYPES[a.dtype][0]) for _ in range(nlayers)]
+            layers = built[key]
+        r = run_tokens(a, wl, T, layers, L, dev)
+        entry = {"workload": r["config"]["workload"], "dtype": r["dtype"],
+                 "gbs": r["value"], "ms_per_step": r["ms_per_step"],
+                 "active_experts": r["config"]["active_experts"],
+                 "expert_kernels": r["config"]["expert_kernels"],
+                 "down_combine": r["config"]["down_combine"],
+                 "routing": r["config"]["routing"]}
+        entry.update({k: r[k] for k in keep if r.get(k) is not None})
+        if entry.get("parity"):
+            p = entry["parity"]
+            entry["parity"] = {k: p[k] for k in ("ids_equal", "weight_bits_equal", "max_rel_err",
+                                                 "elem_rel_err_p99", "tol_max_rel_err", "pass",
+                                                 "scope") if k in p}
+        out[name] = entry
+    built.clear()
+    torch.cuda.empty_cache()
     return out
 
 
@@ -613,6 +691,8 @@ def main():
         if headline_sweep:
             out["sweep"] = {str(t): run_tokens(args, wl, t, layers, L, dev, light=True)
                             for t in HEADLINE_SWEEP}
+            if not args.no_workloads:
+                out["workloads"] = run_workloads(args, dev, L, layers)
         print(json.dumps(out), flush=True)
 
 

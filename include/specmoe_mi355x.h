@@ -140,7 +140,9 @@ int smx_fused_moe_forward(const void* hidden, void* out, int dtype, int64_t T, i
  * Every call on one GPU shares that GPU's scratch and leaves its intermediates there: calls
  * that overlap on one GPU (two streams, or two threads without ordering) race. Nothing in the
  * scratch has to start at zero. Arguments and results otherwise as smx_fused_moe_forward, on the
- * device current at the call.
+ * device current at the call. The scratch's device address is looked up once per device, on
+ * the first call there, and kept: resetting a device (hipDeviceReset) while the library is
+ * loaded is not supported by this entry point.
  */
 #define SMX_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int smx_fused_moe_forward_noalloc(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
@@ -359,6 +361,42 @@ int smx_gateup_waves(void);
  */
 int smx_set_gateup_item_walk(int on);
 int smx_gateup_item_walk(void);
+
+/*
+ * The launch plan a MoE call of these sizes takes under the current settings, on the host
+ * only (no device work; usable without a GPU). Fills out[i] for i < min(n, SMX_PLAN_FIELDS)
+ * in the order of enum smx_plan_field and returns SMX_PLAN_FIELDS, or an SMX_ERR_* code for
+ * sizes the MoE entry points reject. A call of more tokens than one pass holds
+ * (SMX_PLAN_CHUNK_TOKENS) runs its passes with the plan of their own sizes: this describes the
+ * first. shared_I = 0: no shared expert.
+ * No counterpart in the reference's operator API; it describes what replaces the reference's
+ * per-call kernel configuration rule and grid (specmoe/layers/fused_moe_kernel.py:222-223,
+ * 293-306), for tests and for the solver's performance model.
+ */
+enum smx_plan_field {
+  SMX_PLAN_TILED = 0,           /* 1: tiled MFMA expert kernels; 0: weight-streaming kernels */
+  SMX_PLAN_FUSED_DOWN,          /* 1: down projection fused with the combine (few tokens) */
+  SMX_PLAN_SPAN,                /* sorted positions per work range */
+  SMX_PLAN_MAX_RANGES,          /* work ranges the grids are sized for */
+  SMX_PLAN_TOK_TILES,           /* 16-token tiles per range (streaming kernels) */
+  SMX_PLAN_SPLITS,              /* K splits of the routed down projection */
+  SMX_PLAN_SPLIT_STEPS,         /* 64-byte steps per down split */
+  SMX_PLAN_DOWN_ROWS,           /* 16-row W2 tiles per down wave (streaming kernels) */
+  SMX_PLAN_GATEUP_WAVES,        /* waves per gate/up workgroup (streaming kernels) */
+  SMX_PLAN_GATEUP_KSPLIT,       /* 1: each gate/up item's K walk split between wave pairs */
+  SMX_PLAN_SHARED_SPLITS,       /* K splits of the shared expert's down projection */
+  SMX_PLAN_SHARED_SPLIT_STEPS,  /* 64-byte steps per shared down split */
+  SMX_PLAN_SHARED_TOK_GROUPS,   /* token ranges of the shared expert */
+  SMX_PLAN_SHARED_GATEUP_BLOCKS,/* leading gate/up workgroups running the shared expert */
+  SMX_PLAN_SHARED_DOWN_BLOCKS,  /* leading down workgroups running the shared expert */
+  SMX_PLAN_TILE_GATEUP_GRID,    /* tiled path: gate/up workgroups launched (0 otherwise) */
+  SMX_PLAN_TILE_DOWN_GRID,      /* tiled path: down workgroups launched (0 otherwise) */
+  SMX_PLAN_CHUNK_TOKENS,        /* tokens per pass */
+  SMX_PLAN_WORKSPACE_BYTES,     /* workspace of the whole call */
+  SMX_PLAN_FIELDS
+};
+int smx_moe_plan_info(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
+                      int64_t shared_I, int dtype, int64_t* out, int n);
 
 /*
  * Measurement hook. With `events` = 5 hipEvent_t handles, every following MoE call records

@@ -44,10 +44,21 @@ def elem_rel_err(y: np.ndarray, want: np.ndarray) -> np.ndarray:
     return np.abs(y.astype(np.float64) - want) / np.maximum(np.abs(want), floor)
 
 
-def parity(y: np.ndarray, want: np.ndarray, tol: float, case: str = "", **extra) -> dict:
-    """Both output metrics of one comparison. Asserts max |y - ref| / max |ref| <= tol and a
-    median elementwise relative error <= tol, and records the figures: with SMX_PARITY_LOG set,
-    one JSON line per comparison is appended to that file."""
+# The 99th percentile of the elementwise relative error may reach this multiple of the
+# output tolerance: outputs near the floor of elem_rel_err carry a larger relative rounding
+# error than the largest ones, but 99 in 100 outputs stay within a small multiple of it.
+P99_FACTOR = 2.0
+
+
+def parity(y: np.ndarray, want: np.ndarray, tol: float, case: str = "", elementwise: bool = True,
+           **extra) -> dict:
+    """Both output metrics of one comparison. Asserts max |y - ref| / max |ref| <= tol and
+    (with `elementwise`) the 99th percentile of the elementwise relative error <= P99_FACTOR *
+    tol, and records the figures: with SMX_PARITY_LOG set, one JSON line per comparison is
+    appended to that file. `elementwise=False` is for outputs of a chain of layers compared
+    end to end: the inputs of its later layers already differ, and the propagated absolute
+    error makes the relative error of small outputs large by construction (each layer is
+    compared elementwise on its own input)."""
     el = elem_rel_err(y, want)
     rec = {"case": case, "max_rel_err": max_rel_err(y, want), "tol": tol,
            "elem_rel_err_median": float(np.median(el)), "elem_rel_err_p99": float(np.quantile(el, 0.99)),
@@ -57,8 +68,17 @@ def parity(y: np.ndarray, want: np.ndarray, tol: float, case: str = "", **extra)
         with open(path, "a") as f:
             f.write(json.dumps(rec) + "\n")
     assert rec["max_rel_err"] <= tol, rec
-    assert rec["elem_rel_err_median"] <= tol, rec
+    if elementwise:
+        assert rec["elem_rel_err_p99"] <= P99_FACTOR * tol, rec
     return rec
+
+
+def nan_buffers(x: torch.Tensor, nbytes: int):
+    """An output like x filled with NaN and a workspace of nbytes bytes of 0xFF (a NaN in
+    every float type), so that a kernel that reads a row the call did not write gives NaN."""
+    out = torch.full_like(x, float("nan"))
+    ws = torch.full((max(int(nbytes), 1),), 0xFF, dtype=torch.uint8, device=x.device)
+    return out, ws
 
 
 def make_pool(E: int, H: int, I: int, dtype: torch.dtype, num_slots: int | None = None,

@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 37, names
+    assert len(names) == 38, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -48,10 +48,26 @@ def test_one_hip_runtime_when_loaded_before_torch():
 
 
 def test_version_and_error_strings():
-    assert L.smx_version() == 10000
+    assert L.smx_version() == 10100
     for code, word in [(0, b"success"), (1000, b"invalid"), (1001, b"supported"),
                        (1002, b"workspace"), (1003, b"aligned")]:
         assert word in L.smx_error_string(code)
+
+
+def test_plan_info_host_query():
+    """smx_moe_plan_info runs on the host only: it answers here, without a GPU."""
+    p = _lib.plan_info(32, 4096, 14336, 8, 2, _lib.SMX_BF16)
+    assert p["tiled"] == 0 and p["span"] == 32 and p["max_ranges"] == 8 + 64 // 32
+    assert p["workspace_bytes"] == L.smx_moe_workspace_size(32, 4096, 14336, 8, 2, 2)
+    q = _lib.plan_info(256, 4096, 14336, 8, 2, _lib.SMX_BF16)
+    assert q["tiled"] == 1 and q["span"] == 128 and q["tile_gateup_grid"] == q["max_ranges"] * 112
+    s = _lib.plan_info(64, 2048, 1408, 64, 6, _lib.SMX_BF16, 2816)
+    assert s["shared_tok_groups"] == 1 and s["shared_gateup_blocks"] > 0
+    out = (ctypes.c_int64 * 2)()
+    assert L.smx_moe_plan_info(32, 4096, 14336, 8, 2, 0, 2, out, 2) == len(_lib.PLAN_FIELDS)
+    assert L.smx_moe_plan_info(32, 4096, 14336, 8, 9, 0, 2, out, 2) == _lib.SMX_ERR_INVALID_ARG
+    assert L.smx_moe_plan_info(32, 4000, 14336, 8, 2, 0, 2, out, 2) == _lib.SMX_ERR_UNSUPPORTED
+    assert L.smx_moe_plan_info(32, 4096, 14336, 8, 2, 0, 2, None, 2) == _lib.SMX_ERR_INVALID_ARG
 
 
 def test_workspace_size():

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 from oracle import moe_ref as ref
+from ae_amd import _lib
 from ae_amd.layers import (fused_moe_forward, fused_moe_shared_forward, gateup_item_walk,
                            gateup_waves, routing_in_gateup, stack_fused_moe)
 from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, parity, to_oracle
@@ -184,6 +185,10 @@ def test_gateup_k_split_shared_block(dtype, in_launch, T):
     8 in fp32; ffn 1408 and a shared ffn of 2816 give grids of 800+ 4-wave workgroups), against
     the oracle; bit-stable run to run; the forced 4-wave shape (unsplit) against the oracle too."""
     H, I, E, k, Is = 512, 1408, 64, 6, 2816
+    dt = {torch.bfloat16: _lib.SMX_BF16, torch.float32: _lib.SMX_F32}[dtype]
+    assert _lib.plan_info(T, H, I, E, k, dt, Is)["gateup_ksplit"] == 1, "the default takes the split"
+    with gateup_waves(4):
+        assert _lib.plan_info(T, H, I, E, k, dt, Is)["gateup_ksplit"] == 0, "a forced shape does not"
     x, logits = _inputs(T, H, E, dtype, seed=300 + T)
     pool, slots = make_pool(E, H, I, dtype, seed=301)
     g = torch.Generator(device=DEV).manual_seed(302)

@@ -200,6 +200,32 @@ def test_fused_moe_routed_scaling_factor_accepted():
     parity(f32_of(outs[1]), y_ref, TOL[dtype], case="FusedMoE routed_scaling_factor=2.5")
 
 
+def test_fused_moe_ignored_options_give_the_default_output():
+    """FusedMoE built with the options the reference's forward_cuda ignores
+    (activation="gelu", apply_router_weight_on_input=True, inplace=False, no_combine=True)
+    computes what the reference computes for them: the default SiLU, combined, in-place
+    output."""
+    import warnings
+    T, H, I, E, k = 9, 256, 256, 8, 2
+    dtype = torch.bfloat16
+    pool, slots = make_pool(E, H, I, dtype, num_slots=E, seed=25)
+    x, logits = _inputs(T, H, E, dtype, seed=26)
+    outs = []
+    for opts in ({}, dict(activation="gelu", apply_router_weight_on_input=True, inplace=False,
+                          no_combine=True)):
+        moe = FusedMoE(num_experts=E, top_k=k, hidden_size=H, intermediate_size=I,
+                       params_dtype=dtype, tp_size=1, **opts)
+        set_weight_attrs(moe.ws, {"gpu_cache": pool})
+        x_in = x.clone()
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore", RuntimeWarning)
+            out = moe(x_in, logits, slots)
+        assert out.data_ptr() == x_in.data_ptr()
+        outs.append(out)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_mixtral_moe_block():
     T, H, I, E, k = 10, 256, 128, 8, 2
     dtype = torch.bfloat16

@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from oracle import moe_ref as ref
+from ae_amd import _lib
 from ae_amd.layers import (DeepseekV2MoE, Qwen2MoeSparseMoeBlock, fused_moe_forward,
                            fused_moe_shared_forward, set_weight_attrs, tiled_min_tokens)
 from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, parity, to_oracle
@@ -100,24 +101,43 @@ def test_qwen15_moe_shape():
     _check(x, logits, pool, slots, k, False, page, sgate, 1.0)
 
 
-@pytest.mark.parametrize("T", [1, 8, 32, 128])
+# The default plan's distinguishing features at each DeepSeek-V2-Lite verify size (so that
+# every kernel form the stack runs is covered at its full shape).
+DSV2_PLANS = {
+    1: dict(fused_down=1, gateup_waves=4, gateup_ksplit=0),    # down + combine in one kernel
+    2: dict(fused_down=1, gateup_waves=2, gateup_ksplit=0),    # 2-wave gate/up workgroups
+    4: dict(fused_down=0, down_rows=1, gateup_ksplit=0),       # one W2 row tile per wave
+    8: dict(fused_down=0, gateup_ksplit=1),                    # gate/up K split
+    16: dict(fused_down=0, gateup_ksplit=1, down_rows=2),      # K split at full H = 2048
+    32: dict(fused_down=0, gateup_ksplit=1, tok_tiles=2),
+    64: dict(fused_down=0, gateup_ksplit=0, tok_tiles=4, down_rows=1),  # the row-tile rule
+    128: dict(fused_down=0, tok_tiles=4, down_rows=1, shared_tok_groups=2),  # two token ranges
+}
+
+
+@pytest.mark.parametrize("T", sorted(DSV2_PLANS))
 def test_deepseek_v2_lite_shape(T):
     """DeepSeek-V2-Lite block: H 2048, 64 experts of I 1408, top-6 without renormalisation,
-    2 shared experts fused into one MLP of I 2816, routed scaling 1.0."""
+    2 shared experts fused into one MLP of I 2816, routed scaling 1.0, on the default plan of
+    each verify size (the plan's features asserted first)."""
     H, I, E, k, Is = 2048, 1408, 64, 6, 2816
+    plan = _lib.plan_info(T, H, I, E, k, _lib.SMX_BF16, Is)
+    assert plan["tiled"] == 0
+    for key, want in DSV2_PLANS[T].items():
+        assert plan[key] == want, (T, key, plan)
     x, logits, _ = _inputs(T, H, E, torch.bfloat16, seed=40 + T)
     pool, slots = make_pool(E, H, I, torch.bfloat16, num_slots=E, seed=41)
     page = _shared_page(H, Is, torch.bfloat16, seed=42)
     _check(x, logits, pool, slots, k, False, page, None, 1.0)
 
 
-@pytest.mark.parametrize("T", [1, 4])
-def test_deepseek_v2_lite_layer_chain_in_place(T):
-    """Three DeepSeek-V2-Lite blocks with distinct weights run in place one after another on
-    one hidden-state buffer (each layer's output is the next one's input, as in the stack the
+@pytest.mark.parametrize("T,L", [(1, 8), (4, 3)])
+def test_deepseek_v2_lite_layer_chain_in_place(T, L):
+    """L DeepSeek-V2-Lite blocks with distinct weights run in place one after another on one
+    hidden-state buffer (each layer's output is the next one's input, as in the stack the
     benchmark times), against the oracle: every layer fed the GPU's input of that layer, and
-    the whole chain fed its own outputs (three layers of 1e-2 each)."""
-    H, I, E, k, Is, L = 2048, 1408, 64, 6, 2816, 3
+    the whole chain fed its own outputs (L layers of 1e-2 each)."""
+    H, I, E, k, Is = 2048, 1408, 64, 6, 2816
     x0, _, _ = _inputs(T, H, E, torch.bfloat16, seed=60 + T)
     layers = []
     for l in range(L):
@@ -137,7 +157,8 @@ def test_deepseek_v2_lite_layer_chain_in_place(T):
             ref.f32_to_bf16_bits(y_chain) if y_chain.dtype != np.uint16 else y_chain,
             f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, False, "bf16",
             shared_page=to_oracle(page))
-    parity(f32_of(buf), y_chain, L * TOL[torch.bfloat16], case=f"dsv2lite chain T={T} end to end")
+    parity(f32_of(buf), y_chain, L * TOL[torch.bfloat16], case=f"dsv2lite chain T={T} end to end",
+           elementwise=False)
 
 
 def test_shared_block_deterministic_bitwise():

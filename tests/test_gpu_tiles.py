@@ -1,7 +1,9 @@
 """GPU parity of the tiled expert kernels (MFMA output tiles of 128 tokens, the path for
 experts that see many tokens) against the oracle, through the C ABI. Most cases force the
 tiled path on small shapes (threshold 0) so the oracle stays fast; the Mixtral cases run it
-at its default threshold."""
+at its default threshold. Every call runs on an output filled with NaN and a workspace of
+0xFF bytes (NaN in every float type): a kernel that reads a row the call did not write, or
+LDS a DMA has not filled yet with such a row, turns the output NaN on the first run."""
 import numpy as np
 import pytest
 import torch
@@ -9,8 +11,8 @@ import torch
 from oracle import moe_ref as ref
 from ae_amd.layers import fused_moe_forward, fused_moe_shared_forward, tiled_min_tokens
 from ae_amd import _lib
-from tests.helpers import (TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, to_oracle,
-                           zipf_gate_logits)
+from tests.helpers import (TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, nan_buffers,
+                           to_oracle, zipf_gate_logits)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -29,10 +31,25 @@ def _oracle_forward(x, logits, pool, slots, k, renorm):
                                  slots.cpu().numpy(), k, renorm, dt)
 
 
+def _poisoned(x, logits, pool, k, Is=0):
+    """NaN output and 0xFF workspace for a call on these shapes."""
+    T, H = x.shape
+    E = logits.shape[1]
+    I = pool.shape[1] // (3 * H)
+    dt = {torch.float32: _lib.SMX_F32, torch.float16: _lib.SMX_F16, torch.bfloat16: _lib.SMX_BF16}[x.dtype]
+    if Is:
+        nbytes = _lib.lib().smx_moe_shared_workspace_size(T, H, I, E, k, Is, dt)
+    else:
+        nbytes = _lib.lib().smx_moe_workspace_size(T, H, I, E, k, dt)
+    return nan_buffers(x, nbytes)
+
+
 def _run_and_check(x, logits, pool, slots, k, renorm=True):
+    out, ws = _poisoned(x, logits, pool, k)
     y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, renorm, inplace=False,
-                                  return_routing=True)
+                                  return_routing=True, out=out, workspace=ws)
     torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all(), "NaN in the output: a read of unwritten memory"
     y_ref, w_ref, ids_ref = _oracle_forward(x, logits, pool, slots, k, renorm)
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
@@ -77,8 +94,11 @@ def test_tiled_equals_streaming_within_tolerance_and_is_deterministic():
     x, logits = _inputs(T, H, E, torch.bfloat16, seed=5)
     pool, slots = make_pool(E, H, I, torch.bfloat16, seed=6)
     with tiled_min_tokens(0):
-        ys = [fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False)
-              for _ in range(3)]
+        ys = []
+        for _ in range(3):
+            out, ws = _poisoned(x, logits, pool, k)
+            ys.append(fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                        out=out, workspace=ws))
     with tiled_min_tokens(1 << 62):
         ystream = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False)
     torch.cuda.synchronize()
@@ -119,9 +139,12 @@ def test_tiled_shared_block_matches_oracle(dtype, gated, T, H, I, E, k, Is):
     pool, slots = make_pool(E, H, I, dtype, num_slots=E + 2, seed=E + 1)
     scale = 1.0 if gated else 2.5
     with tiled_min_tokens(0):
+        out, ws = _poisoned(x, logits, pool, k, Is=Is)  # sized for the plan in force
         y, w, ids = fused_moe_shared_forward(x.clone(), logits, pool, slots, k, gated, page,
-                                             sgate, scale, inplace=False, return_routing=True)
+                                             sgate, scale, inplace=False, return_routing=True,
+                                             out=out, workspace=ws)
     torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
     y_ref, w_ref, ids_ref = ref.fused_moe_shared_forward(
         to_oracle(x), f32_of(logits), to_oracle(pool), slots.cpu().numpy(), k, gated,
         TORCH_TO_ORACLE[dtype], shared_page=to_oracle(page),
@@ -164,9 +187,11 @@ def test_mixtral_max_assignments_sampled(path):
     logits = zipf_gate_logits(x, E, seed=3)
     pool, slots = make_pool(E, H, I, torch.bfloat16, seed=9)
     with tiled_min_tokens(0 if path == "tiled" else 1 << 62):
+        out, ws = _poisoned(x, logits, pool, k)  # sized for the plan in force
         y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
-                                      return_routing=True)
+                                      return_routing=True, out=out, workspace=ws)
     torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
     w_ref, ids_ref = ref.topk_softmax(f32_of(logits), k, True)
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))

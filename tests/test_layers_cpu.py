@@ -68,6 +68,29 @@ def test_unsupported_options_raise():
         FusedMoE(4, 2, 8, 8, params_dtype=torch.float32, tp_size=1, quant_config=object())
 
 
+def test_options_the_reference_ignores_are_accepted():
+    """activation, apply_router_weight_on_input, inplace and no_combine are accepted and
+    ignored, as the reference's forward_cuda ignores them (specmoe/layers/FusedMoE.py:155-196);
+    a non-default value warns once."""
+    import warnings
+    from ae_amd.layers.FusedMoE import _warned, warn_ignored_options
+    moe = FusedMoE(4, 2, 128, 128, params_dtype=torch.bfloat16, tp_size=1, activation="gelu",
+                   apply_router_weight_on_input=True, no_combine=True, inplace=False)
+    assert moe.no_combine and moe.apply_router_weight_on_input and moe.activation == "gelu"
+    _warned.clear()
+    with warnings.catch_warnings(record=True) as got:
+        warnings.simplefilter("always")
+        warn_ignored_options(activation="silu", apply_router_weight_on_input=False, inplace=True,
+                             no_combine=False)
+        assert not got
+        warn_ignored_options(activation="gelu", apply_router_weight_on_input=True, inplace=False,
+                             no_combine=True)
+        assert len(got) == 4 and all(issubclass(w.category, RuntimeWarning) for w in got)
+        warn_ignored_options(activation="gelu", apply_router_weight_on_input=True, inplace=False,
+                             no_combine=True)
+        assert len(got) == 4  # once per option and value
+
+
 def test_forward_requires_pool_and_gpu_tensors():
     moe = FusedMoE(4, 2, 128, 128, params_dtype=torch.bfloat16, tp_size=1)
     x = torch.zeros((2, 128), dtype=torch.bfloat16)
