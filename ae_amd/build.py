@@ -19,7 +19,8 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_NAME = "libspecmoe_mi355x.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["routing.hip", "experts.hip", "tiles.hip", "capi.hip", "transfer.hip", "stream_probe.hip"]
+SOURCES = ["routing.hip", "experts.hip", "layer1.hip", "tiles.hip", "capi.hip", "transfer.hip",
+           "stream_probe.hip"]
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for every HIP translation unit (the host pass warns

@@ -7,8 +7,10 @@
 #include "smx_kernels.h"
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <mutex>
+#include <random>
 
 // Device-resident scratch of smx_fused_moe_forward_noalloc: the workspace of a call that may
 // not allocate. Each GPU the library runs on holds its own copy (allocated with the code object
@@ -59,6 +61,18 @@ int g_gateup_waves = 0;
 // Gate/up grids larger than one residency of the chip run as workgroups walking several items
 // (smx_set_gateup_item_walk).
 bool g_gateup_walk = true;
+// One-token layers as one launch where the plan allows (smx_set_single_launch_layer). Off by
+// default: measured on the DeepSeek-V2-Lite block at one token, 37.0 us per layer against 31.1
+// for the two launches (timelines: while the down workgroups stream their W2 rows the last
+// gate/up workgroups end at ~27.5 us instead of ~19 us, and ~8 us of wait, staging and dot
+// products follow the last publication).
+bool g_layer1 = false;
+// The single-launch layer's in-launch wait (smx_set_layer_sync_test): whether the gate/up
+// workgroups publish (0 only in tests of the give-up path) and the longest wait of a down
+// workgroup. Measured layers take ~30 us; the bound only ends a wait that would never end.
+int g_sync_publish = 1;
+constexpr int64_t kSyncWaitDefaultUs = 100000;
+int64_t g_sync_wait_us = kSyncWaitDefaultUs;
 // The default rule: 4 waves per workgroup, unless the 4-wave grid has a little more than one
 // workgroup per CU (more than kChipCUs but fewer than kGateupFillBlocks): then some CUs hold two
 // of them and finish last, and 2 waves per workgroup (twice the workgroups) spread the load.
@@ -139,6 +153,11 @@ struct Plan {
   size_t act_s = 0, part_s = 0;
   // whole-layer form: router logits and shared-expert gate logits
   size_t logits = 0, sgl = 0;
+  // single-launch layer (one token, fused down): eligible, its gate/up workgroups and the
+  // workspace offset of their flags (the status word follows them)
+  bool layer1 = false;
+  int sync_blocks = 0;
+  size_t sync = 0;
 };
 
 // Shape limits shared by the workspace query and the entry points.
@@ -321,6 +340,21 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
       p.s_down_blocks = static_cast<int>(p.s_tok_groups * ((H / (kRowTile * p.down_rows) + kExpertWaves - 1) / kExpertWaves) * ss);
     }
   }
+  if (p.rows && T == 1) {
+    // The single-launch form (layer1.hip): 4-wave gate/up workgroups without the K split (their
+    // grid: the shared expert's, then every range's weight groups), the down waves' W2 units
+    // and the activation rows within the kernel's registers and LDS, 4 output rows per
+    // workgroup, and the in-launch routing of one token (E <= 64).
+    const int64_t gu_tiles = p.gu_ks ? 2 : p.gu_waves;
+    const int64_t groups = (I / kRowTile + gu_tiles - 1) / gu_tiles;
+    const int64_t units = (I * eb + kRowsUnitBytes - 1) / kRowsUnitBytes;
+    const int64_t units_s = (Is * eb + kRowsUnitBytes - 1) / kRowsUnitBytes;
+    const int64_t act_bytes = (Is * eb + 15) / 16 * 16 + k * I * eb;
+    p.sync_blocks = static_cast<int>(p.s_gateup_blocks + p.max_ranges * groups);
+    p.layer1 = p.gu_waves == kExpertWaves && !p.gu_ks && E <= kWave && H % kExpertWaves == 0 &&
+               units_s + k * units <= kLayerMaxUnits && act_bytes <= kLayerMaxActBytes &&
+               p.sync_blocks <= kLayerMaxGuBlocks;
+  }
   size_t o = 0;
   p.hdr = o;        o = align_up(o + 64);
   p.ranges = o;     o = align_up(o + sizeof(RangeRec) * static_cast<size_t>(p.max_ranges > 0 ? p.max_ranges : 1));
@@ -342,6 +376,9 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
   if (layer) {
     p.logits = o;   o = align_up(o + static_cast<size_t>(eb) * T * E);
     p.sgl = o;      o = align_up(o + static_cast<size_t>(eb) * T);
+  }
+  if (p.layer1) {
+    p.sync = o;     o = align_up(o + sizeof(uint64_t) * (static_cast<size_t>(p.sync_blocks) + 1));
   }
   p.total = o;
   return p;
@@ -420,6 +457,41 @@ int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logit
   return 0;
 }
 
+// A value unique to one single-launch layer call within this process (never 0): the high 32
+// bits are random per process (so workspace bytes left by another process, or any other data,
+// match a call's value only by a 2^-64 chance), the low bits count calls.
+uint64_t next_epoch() {
+  static std::atomic<uint64_t> counter{[] {
+    std::random_device rd;
+    return (static_cast<uint64_t>(rd()) | 1u) << 32;
+  }()};
+  return counter.fetch_add(1, std::memory_order_relaxed) + 1;
+}
+
+// Wall-clock (s_memrealtime) ticks per microsecond of the current device (100 on MI355X).
+int64_t wall_ticks_per_us() {
+  static std::atomic<int> cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 100;
+  if (dev < 64) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int khz = 0;
+  if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz < 1000) khz = 100000;
+  const int per_us = khz / 1000;
+  if (dev < 64) cached[dev].store(per_us, std::memory_order_relaxed);
+  return per_us;
+}
+
+// The single-launch form is kept out of stream capture: its per-call value is a kernel
+// argument, and a graph would replay one value.
+bool capturing(hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess) return true;
+  return st != hipStreamCaptureStatusNone;
+}
+
 // Shared tail of the MoE entry points: expert kernels then combine. route_g > 0: the gate/up
 // launch routes the batch itself (rt).
 int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t T, int64_t H,
@@ -460,6 +532,26 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
     a.sh.down_blocks = p.s_down_blocks;
   }
   a.rt = rt;
+  if (p.layer1 && g_layer1 && route_g > 0 && !route_multi && !capturing(s)) {
+    // one launch: gate/up workgroups, then the fused down + combine workgroups
+    a.ls.flags = reinterpret_cast<uint64_t*>(b + p.sync);
+    a.ls.status = a.ls.flags + p.sync_blocks;
+    a.ls.epoch = next_epoch();
+    a.ls.gu_blocks = p.sync_blocks;
+    a.ls.publish = g_sync_publish;
+    a.ls.wait_ticks = g_sync_wait_us * wall_ticks_per_us();
+    a.lo.y = out;
+    a.lo.block = bt.block ? 1 : 0;
+    a.lo.scale = bt.scale;
+    a.lo.sgate = bt.sgate;
+    a.lo.sgate_dtype = bt.sgate_dtype;
+    hipError_t err = launch_layer1(dtype, a, p.max_ranges, route_g, s);
+    if (err != hipSuccess) return static_cast<int>(err);
+    mark(2, s);
+    mark(3, s);  // no down or combine launch
+    mark(4, s);
+    return SMX_OK;
+  }
   hipError_t err = p.tiled ? launch_tile_gateup(dtype, a, p.max_ranges, s)
                            : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s, route_g, route_multi);
   if (err != hipSuccess) return static_cast<int>(err);
@@ -627,6 +719,9 @@ int smx_moe_plan_info(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
     v[SMX_PLAN_TILE_GATEUP_GRID] = tile_grid_blocks(0, H, I, p.s_gateup_blocks, p.max_ranges, 1);
     v[SMX_PLAN_TILE_DOWN_GRID] = tile_grid_blocks(1, H, I, p.s_down_blocks, p.max_ranges, p.splits);
   }
+  v[SMX_PLAN_SINGLE_LAUNCH] = p.layer1 && g_layer1;
+  v[SMX_PLAN_SYNC_BLOCKS] = p.layer1 ? p.sync_blocks : 0;
+  v[SMX_PLAN_SYNC_OFFSET] = p.layer1 ? static_cast<int64_t>(p.sync) : -1;
   v[SMX_PLAN_CHUNK_TOKENS] = tc;
   v[SMX_PLAN_WORKSPACE_BYTES] = static_cast<int64_t>(workspace_for(T, H, I, E, top_k, dtype, shared_I, false));
   for (int i = 0; i < n && i < SMX_PLAN_FIELDS; ++i) out[i] = v[i];
@@ -1019,6 +1114,19 @@ int smx_set_gateup_item_walk(int on) {
 }
 
 int smx_gateup_item_walk(void) { return g_gateup_walk ? 1 : 0; }
+
+int smx_set_single_launch_layer(int on) {
+  g_layer1 = on != 0;
+  return SMX_OK;
+}
+
+int smx_single_launch_layer(void) { return g_layer1 ? 1 : 0; }
+
+int smx_set_layer_sync_test(int publish, int64_t wait_us) {
+  g_sync_publish = publish != 0 ? 1 : 0;
+  g_sync_wait_us = wait_us > 0 ? wait_us : kSyncWaitDefaultUs;
+  return SMX_OK;
+}
 
 int smx_set_profile_events(void* const* events, int count) {
   if (events == nullptr || count == 0) {

@@ -8,6 +8,7 @@ namespace smx {
 
 constexpr int kBufDword3 = 0x00020000;            // gfx9 raw-buffer resource word 3
 constexpr int kNonTemporal = 2;                   // cache-policy bit: streaming (read once)
+constexpr int kDeviceScope = 16;                  // cache-policy bit: device scope (sc1)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), kBufDword3);
@@ -73,6 +74,29 @@ __device__ __forceinline__ void store4(void* base, int64_t idx, float v0, float 
                         (static_cast<uint32_t>(Elem<DT>::from_f32(v3)) << 16);
     u32x2 v = {lo, hi};
     *reinterpret_cast<u32x2*>(static_cast<S*>(base) + idx) = v;
+  }
+}
+
+// store4 with device-scope stores (relaxed atomic stores at agent scope: written through to the
+// level every XCD reads from). Once the wave's vector-memory counter is zero they are visible
+// to device-scope loads on any XCD. idx is a multiple of 4 (8-byte aligned in 16-bit types).
+template <int DT>
+__device__ __forceinline__ void store4_agent(void* base, int64_t idx, float v0, float v1, float v2,
+                                             float v3) {
+  using S = typename Elem<DT>::S;
+  auto put = [](void* p, uint64_t v) {
+    __hip_atomic_store(static_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  if constexpr (DT == kF32) {
+    float* p = static_cast<float*>(base) + idx;
+    put(p, static_cast<uint64_t>(__float_as_uint(v0)) | (static_cast<uint64_t>(__float_as_uint(v1)) << 32));
+    put(p + 2, static_cast<uint64_t>(__float_as_uint(v2)) | (static_cast<uint64_t>(__float_as_uint(v3)) << 32));
+  } else {
+    const uint64_t v = static_cast<uint64_t>(Elem<DT>::from_f32(v0)) |
+                       (static_cast<uint64_t>(Elem<DT>::from_f32(v1)) << 16) |
+                       (static_cast<uint64_t>(Elem<DT>::from_f32(v2)) << 32) |
+                       (static_cast<uint64_t>(Elem<DT>::from_f32(v3)) << 48);
+    put(static_cast<S*>(base) + idx, v);
   }
 }
 

@@ -163,4 +163,8 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
+// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding
+// (the expcnt and lgkmcnt fields at their maxima: no wait on them).
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
 }  // namespace smx

@@ -105,6 +105,29 @@ struct InRoute {
   int E, renorm;
 };
 
+// The single-launch layer (layer1.hip): one launch holds the gate/up workgroups [0, gu_blocks)
+// and after them the down workgroups of the fused down projection + combine. A gate/up
+// workgroup stores its activation rows through to device scope, waits for the stores to
+// complete, and then stores `epoch` into its flag; a down workgroup waits (bounded in time)
+// until every flag holds `epoch` and then reads the activation rows at device scope.
+struct LayerSync {
+  uint64_t* flags;      // [gu_blocks] (workspace)
+  uint64_t* status;     // (workspace) set to `epoch` by a down workgroup that gave up waiting
+  uint64_t epoch;       // this call's value: unique within the process, never 0
+  int gu_blocks;        // gate/up workgroups; the down workgroups follow them in the grid
+  int publish;          // 0: the gate/up workgroups do not publish (tests of the give-up path)
+  int64_t wait_ticks;   // longest wait of a down workgroup, in wall-clock (s_memrealtime) ticks
+};
+
+// The combine arguments of the single-launch layer's down workgroups (as RowsArgs).
+struct LayerOut {
+  void* y;              // [T, H]
+  int block;
+  float scale;
+  const void* sgate;
+  int sgate_dtype;
+};
+
 struct ExpertArgs {
   const void* x;        // [T, H] hidden states
   const void* pool;     // [num_slots, page_elems] expert pages
@@ -127,6 +150,8 @@ struct ExpertArgs {
                         // (2 weight tiles per workgroup; sh.gateup_blocks and the grid follow it)
   InRoute rt;           // used by the gate/up launch with routing inside (route_g > 0)
   SharedArgs sh;
+  LayerSync ls;         // the single-launch layer only
+  LayerOut lo;          // the single-launch layer only
 };
 
 struct CombineArgs {
@@ -179,6 +204,15 @@ struct RowsArgs {
 };
 
 hipError_t launch_down_rows(int dtype, const RowsArgs& a, hipStream_t s);
+
+// The single-launch layer for one token (layer1.hip): the gate/up launch with routing inside
+// (route_g lanes per token, 4 waves per workgroup) followed, in the same grid, by one down
+// workgroup per 4 output rows. Its limits: T = 1, E <= 64, the down waves' W2 units
+// (kLayerMaxUnits) and the activation rows staged in LDS (kLayerMaxActBytes).
+constexpr int kLayerMaxUnits = 24;
+constexpr int kLayerMaxActBytes = 32768;
+constexpr int kLayerMaxGuBlocks = 512;  // gate/up workgroups one polling wave watches (8 per lane)
+hipError_t launch_layer1(int dtype, const ExpertArgs& a, int max_ranges, int route_g, hipStream_t s);
 
 // Post-attention residual add + RMSNorm + router gate (+ shared-expert gate row, + top-k).
 constexpr int kNormThreads = 256;

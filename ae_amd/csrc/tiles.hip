@@ -124,9 +124,6 @@ __device__ __forceinline__ void store_t(const TRegs& r, u32x4* stage, int wbase)
   for (int j = 0; j < kTBLoads; ++j) stage[wbase + j * kTRowsPerLoad * kTSlots] = r.v[j];
 }
 
-// s_waitcnt immediate that waits until at most n vector-memory operations are outstanding.
-constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
-
 // Token rows of a step straight into an LDS stage (buffer_load ... lds, 16 bytes per lane, no
 // registers): instruction j of wave w fills stage slots [256 j + 64 w, +64) in lane order. Slot
 // 256 j + 64 w + l is row q = 32 j + 8 w + l / 8 at position l % 8, which the swizzled layout

@@ -390,6 +390,10 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
     sort_in_launch = in_launch or (on and not tiled and E <= 64 and T * k <= 256 and T <= 64)
     if args.layer:  # the layer call routes from the norm kernel's picks (one token: in the norm)
         in_launch = not tiled and E <= 64 and (T == 1 or (on and T * k <= 256 and T <= 64))
+    # one token in one launch (gate/up, then the fused down + combine workgroups in the same
+    # grid): the library's plan, when the routing runs inside the launch and nothing captures
+    single = (bool(_lib.plan_info(T, H, I, E, k, dcode, Is)["single_launch"]) and in_launch
+              and not args.layer and not args.graph)
 
     for i in range(args.warmup):
         step(i)
@@ -477,7 +481,9 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
         "tokens": T, "hidden": H, "ffn": I, "experts": E, "top_k": k,
         "routing": routing, "active_experts": len(active), "tokens_per_expert": counts,
         "pool_copies_rotated": copies,
-        "expert_kernels": "tiled" if tiled else "streaming",
+        "expert_kernels": ("tiled" if tiled else
+                           "streaming, one launch (gate/up and the fused down + combine)" if single
+                           else "streaming"),
         "down_combine": "fused" if fused_down else "split",
         "routing_launch": ("inside the gate/up launch" if in_launch else
                            "top-k kernel, sort inside the gate/up launch" if sort_in_launch
@@ -534,7 +540,22 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
                            "gate_up": round(stage_us[1], 2),
                            "down": round(stage_us[2], 2),
                            "combine": 0.0 if fused_down else round(stage_us[3], 2)}
-        if tiled:  # many tokens per expert: the matrix cores bound the tiled kernels
+        if single:  # one launch streams every weight row of the layer
+            layer_gbs = layer_bytes / (stage_us[1] * 1e-6) / 1e9
+            out["stage_us"]["down"] = 0.0  # no down launch: the interval is only an event's cost
+            out["roofline"] = {
+                "kernel": "gateup_kernel with the fused down + combine workgroups (the whole layer "
+                          "in one launch: W1/W3 and W2 streams, SiLU*up, combine)",
+                "bound": "hbm",
+                "achieved": round(layer_gbs, 1),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+                "traffic": None,
+                "algorithmic_bytes": layer_bytes,
+                "us_per_launch": round(stage_us[1], 2),
+            }
+        elif tiled:  # many tokens per expert: the matrix cores bound the tiled kernels
             tflops = gateup_flops / (stage_us[1] * 1e-6) / 1e12
             peak = MFMA_BF16_PEAK_TFLOPS if dname == "bf16" else MFMA_FP32_PEAK_TFLOPS
             out["roofline"] = {

@@ -363,6 +363,33 @@ int smx_set_gateup_item_walk(int on);
 int smx_gateup_item_walk(void);
 
 /*
+ * One-token MoE calls in one launch. A call of one token whose down projection and combine run
+ * as one kernel (smx_set_fused_down_max_tokens) and whose routing runs inside the gate/up launch
+ * -- the DeepSeek-V2-Lite and Qwen1.5-MoE blocks at one token -- runs, with `on`, as a single
+ * launch: the gate/up workgroups, then in the same grid the fused down + combine
+ * workgroups, which load their W2 rows while gate/up runs and wait inside the launch (bounded
+ * in time) until every gate/up workgroup has stored its activation rows. Outputs are identical
+ * to the two-launch form's. Not used while `stream` is capturing a graph (the two-launch form
+ * runs instead). Off by default: on MI355X the two launches measured faster (DeepSeek-V2-Lite
+ * block at one token: 31.1 vs 37.0 us per layer). Process-wide, like smx_set_tiled_min_tokens.
+ * Replaces, at one token, the launch sequence of stack_fused_moe after routing -- the two
+ * fused_moe_kernel GEMMs, silu_and_mul and the torch.sum combine
+ * (specmoe/layers/fused_moe_kernel.py:329-347).
+ */
+int smx_set_single_launch_layer(int on);
+int smx_single_launch_layer(void);
+
+/*
+ * Test hook of the single-launch form's in-launch wait. publish = 0: the gate/up workgroups do
+ * not publish their activation rows, so every down workgroup gives up after wait_us
+ * microseconds, writes NaN to its outputs and stores the call's value in the status word (the
+ * workspace word after the flags: SMX_PLAN_SYNC_OFFSET); every workgroup still ends normally.
+ * publish = 1 is normal operation. wait_us <= 0 restores the default bound (100 ms).
+ * No counterpart in the reference: a failure-path test hook.
+ */
+int smx_set_layer_sync_test(int publish, int64_t wait_us);
+
+/*
  * The launch plan a MoE call of these sizes takes under the current settings, on the host
  * only (no device work; usable without a GPU). Fills out[i] for i < min(n, SMX_PLAN_FIELDS)
  * in the order of enum smx_plan_field and returns SMX_PLAN_FIELDS, or an SMX_ERR_* code for
@@ -391,6 +418,11 @@ enum smx_plan_field {
   SMX_PLAN_SHARED_DOWN_BLOCKS,  /* leading down workgroups running the shared expert */
   SMX_PLAN_TILE_GATEUP_GRID,    /* tiled path: gate/up workgroups launched (0 otherwise) */
   SMX_PLAN_TILE_DOWN_GRID,      /* tiled path: down workgroups launched (0 otherwise) */
+  SMX_PLAN_SINGLE_LAUNCH,       /* 1: one token in one launch (smx_set_single_launch_layer), when
+                                   the routing runs inside it and the stream is not capturing */
+  SMX_PLAN_SYNC_BLOCKS,         /* single launch: gate/up workgroups the down workgroups wait for */
+  SMX_PLAN_SYNC_OFFSET,         /* single launch: workspace byte offset of their flags (8 bytes
+                                   each), followed by the status word; -1 otherwise */
   SMX_PLAN_CHUNK_TOKENS,        /* tokens per pass */
   SMX_PLAN_WORKSPACE_BYTES,     /* workspace of the whole call */
   SMX_PLAN_FIELDS
