@@ -79,6 +79,8 @@ SIGNATURES = [
     ("smx_gateup_waves", _i32, []),
     ("smx_set_gateup_item_walk", ctypes.c_int, [_i32]),
     ("smx_gateup_item_walk", _i32, []),
+    ("smx_set_gateup_expert_items", ctypes.c_int, [_i32]),
+    ("smx_gateup_expert_items", _i32, []),
     ("smx_set_single_launch_layer", ctypes.c_int, [_i32]),
     ("smx_single_launch_layer", _i32, []),
     ("smx_set_layer_sync_test", ctypes.c_int, [_i32, _i64]),
@@ -131,7 +133,8 @@ PLAN_FIELDS = ("tiled", "fused_down", "span", "max_ranges", "tok_tiles", "splits
                "down_rows", "gateup_waves", "gateup_ksplit", "shared_splits",
                "shared_split_steps", "shared_tok_groups", "shared_gateup_blocks",
                "shared_down_blocks", "tile_gateup_grid", "tile_down_grid", "single_launch",
-               "sync_blocks", "sync_offset", "chunk_tokens", "workspace_bytes")
+               "sync_blocks", "sync_offset", "topk_in_gateup", "expert_items", "chunk_tokens",
+               "workspace_bytes")
 
 
 def plan_info(T: int, H: int, I: int, E: int, top_k: int, dtype: int, shared_I: int = 0) -> dict:

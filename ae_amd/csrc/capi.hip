@@ -61,6 +61,9 @@ int g_gateup_waves = 0;
 // Gate/up grids larger than one residency of the chip run as workgroups walking several items
 // (smx_set_gateup_item_walk).
 bool g_gateup_walk = true;
+// Routed gate/up items in expert order, the first item's weights issued before the in-launch
+// routing (smx_set_gateup_expert_items).
+bool g_expert_items = true;
 // One-token layers as one launch where the plan allows (smx_set_single_launch_layer). Off by
 // default: measured on the DeepSeek-V2-Lite block at one token, 37.0 us per layer against 31.1
 // for the two launches (timelines: while the down workgroups stream their W2 rows the last
@@ -433,6 +436,27 @@ constexpr int64_t kRouteInLaunchTopkMax = 512;
 // Lanes per token of the one-wave top-k: the power of two >= E, at least 8.
 int route_group(int64_t E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 64; }
 
+// Expert-ordered gate/up items (expert_item) apply to the multi-wave in-launch routing when
+// every expert is one token range of one pass (T <= span <= the launch's token tiles, at most
+// kExpertItemsMaxTiles) and the batch is expected to leave fewer than 1 in 20 experts without
+// tokens: the grid then has a workgroup per (expert, weight group), and the weights an idle
+// expert's workgroup issues before the routing are read for nothing. Measured per layer
+// against range-ordered items: DeepSeek-V2-Lite 32 tokens (4.3% of experts expected idle)
+// 175.4 -> 174.3 us, the 26-layer stack 4561 -> 4524 us; Qwen1.5-MoE 32 tokens (11% idle)
+// 161.8 -> 163.7, DeepSeek-V2-Lite 16 tokens (21% idle) 155.9 -> 157.1. The top-k of such
+// batches repeated in every gate/up workgroup instead of its own launch measured slower still
+// (DeepSeek-V2-Lite 32 tokens 182.5 us, Qwen1.5-MoE 32 tokens 172.3), as did item walks with
+// given ids (Qwen1.5-MoE 32 tokens 166.5).
+constexpr double kExpertItemsMaxIdle = 0.05;
+bool expert_items_apply(const Plan& p, int64_t T, int64_t E, int64_t k) {
+  if (!g_expert_items || T > p.span || p.span > kTokTile * p.tok_tiles ||
+      p.tok_tiles > kExpertItemsMaxTiles || E > kWave || k > E)
+    return false;
+  // expected fraction of experts no token picks (picks uniform over the experts)
+  const double idle = std::pow(1.0 - static_cast<double>(k) / static_cast<double>(E), static_cast<double>(T));
+  return idle < kExpertItemsMaxIdle;
+}
+
 // The routing runs inside the gate/up launch (no routing launch) for batches one wave routes:
 // T*k <= 64 assignments over E <= 64 experts, every expert one token range of at most two
 // token tiles, the top-k (when logits are given, in the activation dtype) in at most 4 passes
@@ -517,6 +541,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
   a.down_rows = p.down_rows;
   a.gu_waves = p.gu_waves;
   a.gu_ks = p.gu_ks ? 1 : 0;
+  const bool ei = route_g > 0 && route_multi && expert_items_apply(p, T, E, k);
   // the walk pays where every item's prologue would be the top-k from logits and the sort
   a.gu_items = g_gateup_walk && route_g > 0 && rt.logits != nullptr ? 1 : 0;
   a.f16out = dtype == kF32 && g_fp32_f16out ? 1 : 0;
@@ -553,7 +578,7 @@ int run_experts(const Plan& p, int dtype, const void* hidden, void* out, int64_t
     return SMX_OK;
   }
   hipError_t err = p.tiled ? launch_tile_gateup(dtype, a, p.max_ranges, s)
-                           : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s, route_g, route_multi);
+                           : launch_gateup(dtype, a, p.max_ranges, p.tok_tiles, s, route_g, route_multi, ei);
   if (err != hipSuccess) return static_cast<int>(err);
   mark(2, s);
   if (p.rows) {
@@ -722,6 +747,11 @@ int smx_moe_plan_info(int64_t T, int64_t H, int64_t I, int64_t E, int64_t top_k,
   v[SMX_PLAN_SINGLE_LAUNCH] = p.layer1 && g_layer1;
   v[SMX_PLAN_SYNC_BLOCKS] = p.layer1 ? p.sync_blocks : 0;
   v[SMX_PLAN_SYNC_OFFSET] = p.layer1 ? static_cast<int64_t>(p.sync) : -1;
+  const int64_t Tp = std::min(T, tc);
+  bool multi = false;
+  v[SMX_PLAN_TOPK_IN_GATEUP] = in_launch_route_g(p, Tp, E, top_k, true, true, &multi) > 0;
+  const bool ids_multi = in_launch_route_g(p, Tp, E, top_k, false, true, &multi) > 0 && multi;
+  v[SMX_PLAN_EXPERT_ITEMS] = ids_multi && expert_items_apply(p, Tp, E, top_k);
   v[SMX_PLAN_CHUNK_TOKENS] = tc;
   v[SMX_PLAN_WORKSPACE_BYTES] = static_cast<int64_t>(workspace_for(T, H, I, E, top_k, dtype, shared_I, false));
   for (int i = 0; i < n && i < SMX_PLAN_FIELDS; ++i) out[i] = v[i];
@@ -1114,6 +1144,13 @@ int smx_set_gateup_item_walk(int on) {
 }
 
 int smx_gateup_item_walk(void) { return g_gateup_walk ? 1 : 0; }
+
+int smx_set_gateup_expert_items(int on) {
+  g_expert_items = on != 0;
+  return SMX_OK;
+}
+
+int smx_gateup_expert_items(void) { return g_expert_items ? 1 : 0; }
 
 int smx_set_single_launch_layer(int on) {
   g_layer1 = on != 0;

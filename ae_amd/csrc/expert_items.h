@@ -41,8 +41,9 @@ struct ChunkOrder {
 // on a few residues, was slower than none at H = 4096). The down projection's rows (pitch I)
 // are walked in order: its K splits already start at different chunks, and rotating them
 // measured no gain.
-// (index >> 2) < 2^23 for every launch: index < (active experts + 1) * (workgroups per item)
-// + workgroups per item. The modulo is taken with a float reciprocal (div_small): a runtime
+// (index >> 2) < 2^23 for every launch: index < (experts + 1) * (workgroups per item)
+// + workgroups per item (the index of a routed item is (expert + 1) * (its expert's
+// workgroups per item) + its weight group: known before the routing). The modulo is taken with a float reciprocal (div_small): a runtime
 // integer division costs ~20 dependent VALU steps, on every workgroup's path to its first load.
 __device__ __forceinline__ ChunkOrder rotated_order(int n, int index) {
   const int q = index >> 2;
@@ -264,6 +265,46 @@ __device__ __forceinline__ bool work_item(const ExpertArgs& a, int shared_blocks
                                           WorkItem& w, const int32_t* hdr, const RangeRec* ranges) {
   return work_item<S, kExpertWaves, kByXcd>(a, static_cast<int>(blockIdx.x), shared_blocks, per_item,
                                             per_item, w, hdr, ranges);
+}
+
+// Routed items in expert order, for the in-launch routing when every expert is one token range
+// (T <= span): item b >= shared_blocks is weight group g of expert e, b - shared_blocks =
+// e * per_item + g, whether or not e has tokens; shared items as work_item. The rotation is
+// work_item's (the records' key is the expert index). by_expert == nullptr (before the
+// routing): the item's page, I and rotation from the expert-to-slot map -- false when e has
+// no valid slot (the routing then gives it no tokens either). Otherwise by_expert[e] is the
+// routing's record of expert e (every e < E, cnt 0 without routable assignments): also the
+// token range -- false when it is empty.
+template <typename S, int W>
+__device__ __forceinline__ bool expert_item(const ExpertArgs& a, int b, int shared_blocks, int per_item,
+                                            int rot_items, WorkItem& w, const RangeRec* by_expert) {
+  if (b < shared_blocks)
+    return work_item<S, W, false>(a, b, shared_blocks, per_item, rot_items, w, nullptr, nullptr);
+  const int rb = b - shared_blocks;
+  const int e = div_small(rb, per_item, 1.0f / static_cast<float>(per_item));
+  const int g = rb - e * per_item;
+  int64_t slot;
+  if (by_expert == nullptr) {
+    slot = a.e2s[e];
+    if (slot < 0 || slot >= a.rt.num_slots) return false;
+    w.off = 0;
+    w.m = 0;
+  } else {
+    const RangeRec& rr = by_expert[e];
+    const int cnt = uniform(rr.cnt);
+    if (cnt == 0) return false;
+    slot = uniform64(rr.slot);
+    w.off = uniform(rr.off);
+    w.m = cnt;
+  }
+  w.page_bytes = a.page_elems * static_cast<int64_t>(sizeof(S));
+  w.page = static_cast<const char*>(a.pool) + slot * w.page_bytes;
+  w.I = a.I;
+  w.tg = g;
+  w.rot = (e + 1) * rot_items + g * W / kExpertWaves;
+  w.nr = 1;
+  w.shared = false;
+  return true;
 }
 
 }  // namespace smx

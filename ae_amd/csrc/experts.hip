@@ -537,14 +537,15 @@ static int resident_slots() {
 // 4-wave grid with more items than one residency of the chip (a.gu_items > 0 asks for it)
 // runs as G workgroups that walk ceil(items / G) items each (G a multiple of 8, so that every
 // workgroup stays on one XCD's items), when such a G keeps at least 7/8 of the slots busy.
-template <bool kMulti, int DT, int MT, int RG, bool RM>
+// ST: routed items in expert order (expert_item): E items per weight group, not max_ranges.
+template <bool kMulti, int DT, int MT, int RG, bool RM, bool ST = false>
 static void launch_gateup_w(const ExpertArgs& a, int max_ranges, hipStream_t s) {
   auto go = [&](auto wc, auto ksc) {
     constexpr int W = decltype(wc)::value;
     constexpr bool KS = decltype(ksc)::value;
     constexpr int TW = KS ? 2 : W;
     const int64_t groups = (a.I / kRowTile + TW - 1) / TW;
-    const int64_t items = a.sh.gateup_blocks + max_ranges * groups;
+    const int64_t items = a.sh.gateup_blocks + (ST ? a.rt.E : max_ranges) * groups;
     const int slots = resident_slots();
     if constexpr (W == kExpertWaves) {
       // the fewest workgroups that walk equal item counts, if that keeps 7/8 of the slots busy
@@ -553,14 +554,16 @@ static void launch_gateup_w(const ExpertArgs& a, int max_ranges, hipStream_t s) 
       if (a.gu_items > 0 && items > slots && 8 * g >= 7 * static_cast<int64_t>(slots)) {
         ExpertArgs b = a;
         b.gu_items = static_cast<int>(items);
-        gateup_kernel<kMulti, DT, MT, RG, RM, W, true, KS><<<static_cast<unsigned>(g), W * kWave, 0, s>>>(b);
+        gateup_kernel<kMulti, DT, MT, RG, RM, W, true, KS, false, ST>
+            <<<static_cast<unsigned>(g), W * kWave, 0, s>>>(b);
         return;
       }
     }
-    gateup_kernel<kMulti, DT, MT, RG, RM, W, false, KS><<<static_cast<unsigned>(items), W * kWave, 0, s>>>(a);
+    gateup_kernel<kMulti, DT, MT, RG, RM, W, false, KS, false, ST>
+        <<<static_cast<unsigned>(items), W * kWave, 0, s>>>(a);
   };
   using No = std::false_type;
-  if constexpr (!kMulti && MT <= 2) {
+  if constexpr (!kMulti && MT <= 2 && !ST) {
     if (a.gu_waves == 1) return go(std::integral_constant<int, 1>{}, No{});
     if (a.gu_waves == 2) return go(std::integral_constant<int, 2>{}, No{});
   }
@@ -611,34 +614,40 @@ static hipError_t launch_stage(int stage, int dtype, const ExpertArgs& a, int ma
   }
 }
 
-template <int DT, int MT, bool RM>
+template <int DT, int MT, bool RM, bool ST = false>
 static void launch_gateup_routed(const ExpertArgs& a, int max_ranges, int route_g, hipStream_t s) {
   switch (route_g) {
-    case 8: launch_gateup_w<false, DT, MT, 8, RM>(a, max_ranges, s); break;
-    case 16: launch_gateup_w<false, DT, MT, 16, RM>(a, max_ranges, s); break;
-    case 32: launch_gateup_w<false, DT, MT, 32, RM>(a, max_ranges, s); break;
-    default: launch_gateup_w<false, DT, MT, 64, RM>(a, max_ranges, s); break;
+    case 8: launch_gateup_w<false, DT, MT, 8, RM, ST>(a, max_ranges, s); break;
+    case 16: launch_gateup_w<false, DT, MT, 16, RM, ST>(a, max_ranges, s); break;
+    case 32: launch_gateup_w<false, DT, MT, 32, RM, ST>(a, max_ranges, s); break;
+    default: launch_gateup_w<false, DT, MT, 64, RM, ST>(a, max_ranges, s); break;
+  }
+}
+
+template <int DT, bool ST>
+static void launch_gateup_multi(const ExpertArgs& a, int max_ranges, int tok_tiles, int route_g, hipStream_t s) {
+  switch (tok_tiles) {
+    case 1: launch_gateup_routed<DT, 1, true, ST>(a, max_ranges, route_g, s); break;
+    case 2: launch_gateup_routed<DT, 2, true, ST>(a, max_ranges, route_g, s); break;
+    case 3: if constexpr (!ST) launch_gateup_routed<DT, 3, true>(a, max_ranges, route_g, s); break;
+    default: if constexpr (!ST) launch_gateup_routed<DT, 4, true>(a, max_ranges, route_g, s); break;
   }
 }
 
 template <int DT>
 static void launch_gateup_routed_dt(const ExpertArgs& a, int max_ranges, int tok_tiles, int route_g,
-                                    bool multi, hipStream_t s) {
+                                    bool multi, bool expert_items, hipStream_t s) {
   if (!multi) {
     if (tok_tiles <= 1) launch_gateup_routed<DT, 1, false>(a, max_ranges, route_g, s);
     else launch_gateup_routed<DT, 2, false>(a, max_ranges, route_g, s);
     return;
   }
-  switch (tok_tiles) {
-    case 1: launch_gateup_routed<DT, 1, true>(a, max_ranges, route_g, s); break;
-    case 2: launch_gateup_routed<DT, 2, true>(a, max_ranges, route_g, s); break;
-    case 3: launch_gateup_routed<DT, 3, true>(a, max_ranges, route_g, s); break;
-    default: launch_gateup_routed<DT, 4, true>(a, max_ranges, route_g, s); break;
-  }
+  if (expert_items) launch_gateup_multi<DT, true>(a, max_ranges, tok_tiles, route_g, s);
+  else launch_gateup_multi<DT, false>(a, max_ranges, tok_tiles, route_g, s);
 }
 
 hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles, hipStream_t s,
-                         int route_g, bool route_multi) {
+                         int route_g, bool route_multi, bool expert_items) {
   if (route_g == 0) return launch_stage(0, dtype, a, max_ranges, tok_tiles, s);
   // routing inside the launch, every expert one token range (T <= span): one wave routes
   // T*k <= 64 assignments over E <= 64 experts in at most 4 top-k passes; the multi-wave form
@@ -647,14 +656,18 @@ hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok
   if (a.rt.E > kWave || a.T > a.rb.span || tok_tiles > kMaxTokTiles) return hipErrorInvalidValue;
   if (route_multi) {
     if (a.T * a.k > kSortWaveMax) return hipErrorInvalidValue;
+    // expert-ordered items have one pass of at most tok_tiles token tiles (gateup_passes PRE),
+    // at most two (kExpertItemsMaxTiles)
+    if (expert_items && (a.rb.span > kTokTile * tok_tiles || tok_tiles > kExpertItemsMaxTiles))
+      return hipErrorInvalidValue;
   } else if (a.T * a.k > kWave || tok_tiles > 2 ||
              (a.rt.logits != nullptr && a.T * route_g > kWave * kSmallRoutePasses)) {
     return hipErrorInvalidValue;
   }
   switch (dtype) {
-    case kF32: launch_gateup_routed_dt<kF32>(a, max_ranges, tok_tiles, route_g, route_multi, s); break;
-    case kF16: launch_gateup_routed_dt<kF16>(a, max_ranges, tok_tiles, route_g, route_multi, s); break;
-    default: launch_gateup_routed_dt<kBF16>(a, max_ranges, tok_tiles, route_g, route_multi, s); break;
+    case kF32: launch_gateup_routed_dt<kF32>(a, max_ranges, tok_tiles, route_g, route_multi, expert_items, s); break;
+    case kF16: launch_gateup_routed_dt<kF16>(a, max_ranges, tok_tiles, route_g, route_multi, expert_items, s); break;
+    default: launch_gateup_routed_dt<kBF16>(a, max_ranges, tok_tiles, route_g, route_multi, expert_items, s); break;
   }
   return hipGetLastError();
 }

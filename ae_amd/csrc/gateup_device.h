@@ -198,10 +198,34 @@ __device__ __forceinline__ void stream_wg(const WeightStream& w, const SharedTok
 // in half the time. bsh then holds two stages.
 // CO: the activation rows are stored at device scope (store4_agent), for the single-launch
 // layer whose down workgroups read them in the same launch.
-template <int CP, int DT, int MT, int W, bool KS = false, bool CO = false>
+// The weight stream of wave tile p of an item (tile 0: gate rows [16p, 16p+16); tile 1: the
+// matching up rows) and the wave's chunk order (KS: its K half). Needs only the item's page,
+// I and rotation.
+template <int DT, bool KS>
+__device__ __forceinline__ void gateup_stream(const ExpertArgs& a, const WorkItem& it, int p,
+                                              WeightStream& ws, ChunkOrder& ord) {
+  using S = typename Elem<DT>::S;
+  const int lane = lane_id();
+  const int h = KS ? wave_id() >> 1 : 0;
+  const int64_t row_bytes = static_cast<int64_t>(a.H) * sizeof(S);
+  ws.rsrc = make_rsrc(it.page, static_cast<uint32_t>(it.page_bytes));
+  ws.base = static_cast<uint32_t>(kRowTile * p * row_bytes);
+  ws.tile_stride = static_cast<uint32_t>(it.I * row_bytes);
+  ws.row4 = static_cast<uint32_t>(4 * row_bytes);
+  ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
+  const int nch = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
+  ord = rotated_order(KS ? nch / 2 : nch, it.rot);
+  ord.base = h * ord.n;
+}
+
+// PRE: the item's first two weight chunks are already in flight in *pa, *pb (issued by
+// gateup_stream + issue_weights for the same item and tile before the routing); the item then
+// has one pass (m <= MT token tiles: the host's condition for such items).
+template <int CP, int DT, int MT, int W, bool KS = false, bool CO = false, bool PRE = false>
 __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkItem& it, int p,
                                               bool owner, u32x4* lds, u32x4* bsh,
-                                              const int32_t* sorted) {
+                                              const int32_t* sorted, Raw<2>* pa = nullptr,
+                                              Raw<2>* pb = nullptr) {
   using S = typename Elem<DT>::S;
   static_assert(!KS || W == kExpertWaves, "the K split pairs the waves of a 4-wave workgroup");
   constexpr int WT = KS ? 2 : W;  // waves sharing one token stage
@@ -210,24 +234,23 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
   const int h = KS ? wave >> 1 : 0;     // K half
   const int wv = KS ? wave & 1 : wave;  // index among the waves of the token stage
   const int r = lane & 15, g = lane >> 4;
-  const int H = a.H, I = it.I, off = it.off, m = it.m;
-  const int64_t row_bytes = static_cast<int64_t>(H) * sizeof(S);
-  WeightStream ws;  // tile 0: gate rows [16p, 16p+16); tile 1: the matching up rows
-  ws.rsrc = make_rsrc(it.page, static_cast<uint32_t>(it.page_bytes));
-  ws.base = static_cast<uint32_t>(kRowTile * p * row_bytes);
-  ws.tile_stride = static_cast<uint32_t>(I * row_bytes);
-  ws.row4 = static_cast<uint32_t>(4 * row_bytes);
-  ws.lane_off = static_cast<uint32_t>((lane >> 4) * row_bytes + (lane & 15) * 16);
-  const int nch = static_cast<int>(row_bytes / (kStepBytes * kUnroll));
-  ChunkOrder ord = rotated_order(KS ? nch / 2 : nch, it.rot);
-  ord.base = h * ord.n;
+  const int I = it.I, off = it.off, m = it.m;
+  const int64_t row_bytes = static_cast<int64_t>(a.H) * sizeof(S);
+  WeightStream ws;
+  ChunkOrder ord;
+  gateup_stream<DT, KS>(a, it, p, ws, ord);
   u32x4* stage = bsh + h * 2 * MT * kTileSlots;
   S* act = static_cast<S*>(it.shared ? a.sh.act : a.act);
   const int f16out = it.shared ? 0 : a.f16out;
   const float rk = 1.0f / static_cast<float>(a.k);  // flat assignment f -> token f / k
   for (int q0 = 0; q0 < m; q0 += kTokTile * MT) {
     Raw<2> wa, wb;
-    issue_weights<CP>(wa, wb, ws, ord);
+    if constexpr (PRE) {
+      wa = *pa;
+      wb = *pb;
+    } else {
+      issue_weights<CP>(wa, wb, ws, ord);
+    }
     SharedTokens<MT, WT> tb;
     tb.rsrc = make_rsrc(a.x, static_cast<uint32_t>(static_cast<int64_t>(a.T) * row_bytes));
     tb.base = 0;
@@ -289,14 +312,19 @@ __device__ __forceinline__ void gateup_passes(const ExpertArgs& a, const WorkIte
 // wave of a workgroup runs the same chunks and barriers. The token tiles per pass follow
 // the item's token count (up to MT): an expert with few tokens streams its weights with
 // one tile of 16 tokens.
-template <int CP, int DT, int MT, int W, bool KS = false, bool CO = false>
+template <int CP, int DT, int MT, int W, bool KS = false, bool CO = false, bool PRE = false>
 __device__ __forceinline__ void gateup_item(const ExpertArgs& a, const WorkItem& it, int p,
                                             bool owner, u32x4* lds, u32x4* bsh,
-                                            const int32_t* sorted) {
-  if (MT == 1 || it.m <= kTokTile) gateup_passes<CP, DT, 1, W, KS, CO>(a, it, p, owner, lds, bsh, sorted);
-  else if (MT == 2 || it.m <= 2 * kTokTile) gateup_passes<CP, DT, (MT >= 2 ? 2 : 1), W, KS, CO>(a, it, p, owner, lds, bsh, sorted);
-  else if (MT == 3 || it.m <= 3 * kTokTile) gateup_passes<CP, DT, (MT >= 3 ? 3 : 1), W, KS, CO>(a, it, p, owner, lds, bsh, sorted);
-  else gateup_passes<CP, DT, MT, W, KS, CO>(a, it, p, owner, lds, bsh, sorted);
+                                            const int32_t* sorted, Raw<2>* pa = nullptr,
+                                            Raw<2>* pb = nullptr) {
+  if (MT == 1 || it.m <= kTokTile)
+    gateup_passes<CP, DT, 1, W, KS, CO, PRE>(a, it, p, owner, lds, bsh, sorted, pa, pb);
+  else if (MT == 2 || it.m <= 2 * kTokTile)
+    gateup_passes<CP, DT, (MT >= 2 ? 2 : 1), W, KS, CO, PRE>(a, it, p, owner, lds, bsh, sorted, pa, pb);
+  else if (MT == 3 || it.m <= 3 * kTokTile)
+    gateup_passes<CP, DT, (MT >= 3 ? 3 : 1), W, KS, CO, PRE>(a, it, p, owner, lds, bsh, sorted, pa, pb);
+  else
+    gateup_passes<CP, DT, MT, W, KS, CO, PRE>(a, it, p, owner, lds, bsh, sorted, pa, pb);
 }
 
 // The down workgroups of the single-launch layer (defined in layer1.hip, the one translation
@@ -329,11 +357,15 @@ __device__ void layer_down_role(const ExpertArgs& a, u32x4* stage);
 // workgroup has completed, publish a.ls.epoch in their flag. Items per workgroup, never per
 // wave: every wave of a workgroup has the same role.
 template <bool kMulti, int DT, int MT, int RG, bool RM = false, int W = kExpertWaves, bool P = false,
-          bool KS = false, bool FD = false>
+          bool KS = false, bool FD = false, bool ST = false>
 __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
+  using S = typename Elem<DT>::S;
   constexpr int TW = KS ? 2 : W;  // weight tiles per workgroup
   static_assert(!FD || (RG > 0 && !RM && !P && !KS && MT == 1 && !kMulti),
                 "the single-launch layer takes one token, routed inside the launch by one wave");
+  static_assert(!ST || (RG > 0 && RM && !FD && !kMulti && W == kExpertWaves),
+                "expert-ordered items: the multi-wave in-launch routing, 4-wave workgroups");
+  static_assert(!ST || MT <= kExpertItemsMaxTiles, "expert-ordered items: at most two token tiles");
   __shared__ u32x4 lds_all[W][2 * kTileSlots];
   if constexpr (FD) {
     if (static_cast<int>(blockIdx.x) >= a.ls.gu_blocks) {
@@ -348,6 +380,45 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
   const int32_t* hdr = a.rb.hdr;
   const RangeRec* ranges = a.rb.ranges;
   const int32_t* sorted = a.rb.sorted_f;
+  // ST: the workgroup's first item is known before the routing (expert_item): its first two
+  // weight chunks are issued now, and the routing below runs while they are in flight. The
+  // routing's own loads (caller ids -- one per thread: T*k <= 256 -- and the expert-to-slot
+  // map) are issued before them: vector loads complete in issue order, so waiting for these
+  // does not wait for the weights.
+  [[maybe_unused]] int st_id = 0;
+  [[maybe_unused]] int64_t st_slot = -1;
+  [[maybe_unused]] Raw<2> pre_a, pre_b;
+  [[maybe_unused]] bool pre = false;
+  if constexpr (ST) {
+    if (!in_shared) {
+      const int tid = threadIdx.x;
+      if (a.rt.logits == nullptr && tid < a.T * a.k) st_id = a.rt.ids_in[tid];
+      if (tid < a.rt.E) st_slot = a.e2s[tid];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int b0 = static_cast<int>(blockIdx.x);
+    const int tiles = (b0 < a.sh.gateup_blocks ? a.sh.I : a.I) / kRowTile;
+    WorkItem it0;
+    pre = (!P || b0 < a.gu_items) &&
+          expert_item<S, TW>(a, b0, a.sh.gateup_blocks, (tiles + TW - 1) / TW,
+                             (tiles + kExpertWaves - 1) / kExpertWaves, it0, nullptr);
+    // The loads are issued on every path (without a first item: from an empty buffer resource,
+    // which returns zeros and reads nothing), so that every path has the same loads in flight
+    // after the routing's: the waits for those then leave the weights outstanding.
+    if (!pre) {
+      it0.page = static_cast<const char*>(a.pool);
+      it0.page_bytes = 0;
+      it0.I = a.I;
+      it0.rot = 0;
+    }
+    const int praw = pre ? it0.tg * TW + (KS ? wave & 1 : wave) : 0;
+    WeightStream ws;
+    ChunkOrder ord;
+    gateup_stream<DT, KS>(a, it0, praw < tiles ? praw : tiles - 1, ws, ord);
+    // both chunks on every path (a one-chunk walk loads chunk 0 twice and never uses pre_b)
+    load_raw<kNonTemporal>(pre_a, ws, ord.at(0));
+    load_raw<kNonTemporal>(pre_b, ws, ord.at(ord.n > 1 ? 1 : 0));
+  }
   if constexpr (RG > 0 && RM) {
     __shared__ int16_t ids_l[kSortWaveMax];
     __shared__ int64_t slot_l[kWave];
@@ -364,7 +435,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
       const int N = a.T * a.k;
       const int E = a.rt.E;
       const bool writer = writer_wg;
-      const int64_t my_slot = tid < E ? a.e2s[tid] : -1;
+      const int64_t my_slot = ST ? st_slot : (tid < E ? a.e2s[tid] : -1);
       if (tid < kWave) cnt_l[tid] = 0;
       if (tid == 0) me_l = -1;
       auto keep = [&](int t, int slot, float wv, int id) {
@@ -380,6 +451,8 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
         const int stride = W * TPW;
         for (int t0 = wave * TPW + lane / RG; t0 - lane / RG < a.T; t0 += stride * kTokBatch)
           topk_batch<DT, RG, 1>(a.rt.logits, a.T, E, a.k, a.rt.renorm != 0, t0, stride, keep);
+      } else if constexpr (ST) {
+        if (tid < N) ids_l[tid] = static_cast<int16_t>((st_id >= 0 && st_id < E) ? st_id : -2);
       } else {
         for (int f = tid; f < N; f += W * kWave) {
           const int x = a.rt.ids_in[f];
@@ -407,6 +480,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
           l.hdr = hdr_l;
           l.ranges = rr_l;
           l.sorted_f = sf_l;
+          l.by_expert = ST;
           if (writer) {
             g.hdr = a.rb.hdr;
             g.ranges = a.rb.ranges;
@@ -420,6 +494,7 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
         // Own-range form: only the record of this workgroup's range j and its expert's sorted
         // assignments -- the values sort_wave gives them (counts of routable assignments per
         // expert, exclusive scans over the experts, the expert's assignments in ascending f).
+        // ST: j is the expert (expert-ordered items), its record kept even when it is empty.
         for (int f = tid; f < N; f += W * kWave) {
           const int e = ids_l[f];
           if (e >= 0 && slot_l[e] >= 0) atomicAdd(&cnt_l[e], 1);
@@ -433,16 +508,16 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
           const int act = c > 0 ? 1 : 0;
           const int ic = wave_incl_scan(c), ia = wave_incl_scan(act), ir = wave_incl_scan(nr);
           const int j = (static_cast<int>(blockIdx.x) - a.sh.gateup_blocks) / groups;
-          if (c > 0 && j >= ir - nr && j < ir) {
+          if (ST ? lane == j : (c > 0 && j >= ir - nr && j < ir)) {
             RangeRec rec{};
             rec.slot = slot_l[lane];
             rec.off = ic - c;
             rec.cnt = c;
-            rec.key = ia - act;
+            rec.key = lane;
             rec.j0 = ir - nr;
             rec.nr = nr;
-            rr_l[j] = rec;  // j < the launch's range bound <= kSortRangesMax
-            me_l = lane;
+            rr_l[j] = rec;  // j < the launch's range bound (ST: j < E) <= kSortRangesMax
+            if (c > 0) me_l = lane;
           }
           if (lane == kWave - 1) {
             hdr_l[0] = ir;
@@ -479,6 +554,12 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
       ranges = rr_l;
       sorted = sf_l;
     }
+    if constexpr (ST) {
+      // the routed items read only these LDS tables (shared items read neither): as LDS
+      // pointers on every path their reads wait for LDS alone, not for the weights in flight
+      ranges = rr_l;
+      sorted = sf_l;
+    }
   } else if constexpr (RG > 0) {
     __shared__ SmallRouteLds sc;
     __shared__ RangeRec rr_l[kSmallRangesMax];
@@ -512,7 +593,27 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
   __shared__ u32x4 bsh[(KS ? 4 : 2) * MT * kTileSlots];
   u32x4* lds = lds_all[wave];
   const int nitems = P ? a.gu_items : static_cast<int>(blockIdx.x) + 1;
-  for (int b = blockIdx.x; b < nitems; b += gridDim.x) {
+  int b_first = blockIdx.x;
+  if constexpr (ST) {
+    // The first item, its weights in flight since before the routing (pre is false only for a
+    // workgroup whose first item is empty: past the items, or an expert without a valid slot,
+    // which the routing gives no tokens). Peeled off the walk so that pre_a and pre_b are dead
+    // after it.
+    b_first += gridDim.x;
+    if (pre) {
+      const int b = blockIdx.x;
+      const int tiles = (b < a.sh.gateup_blocks ? a.sh.I : a.I) / kRowTile;
+      WorkItem it;
+      if (expert_item<S, TW>(a, b, a.sh.gateup_blocks, (tiles + TW - 1) / TW,
+                             (tiles + kExpertWaves - 1) / kExpertWaves, it, ranges)) {
+        const int praw = it.tg * TW + (KS ? wave & 1 : wave);
+        const bool owner = praw < tiles;
+        gateup_item<kNonTemporal, DT, MT, W, KS, FD, true>(a, it, owner ? praw : tiles - 1, owner, lds,
+                                                           bsh, sorted, &pre_a, &pre_b);
+      }
+    }
+  }
+  for (int b = b_first; b < nitems; b += gridDim.x) {
     const int Iw = b < a.sh.gateup_blocks ? a.sh.I : a.I;
     const int tiles = Iw / kRowTile;
     const int groups = (tiles + TW - 1) / TW;
@@ -520,9 +621,11 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     WorkItem it;
     // XCD order only with the routing kernel's records (inside the launch it measured slower:
     // DeepSeek-V2-Lite 32 tokens 175.8 -> 177.0 us, Qwen1.5-MoE 32 tokens 162.4 -> 163.8)
-    if (!work_item<typename Elem<DT>::S, TW, RG == 0>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr,
-                                                     ranges))
+    if constexpr (ST) {
+      if (!expert_item<S, TW>(a, b, a.sh.gateup_blocks, groups, groups4, it, ranges)) continue;
+    } else if (!work_item<S, TW, RG == 0>(a, b, a.sh.gateup_blocks, groups, groups4, it, hdr, ranges)) {
       continue;
+    }
     const int praw = it.tg * TW + (KS ? wave & 1 : wave);
     const bool owner = praw < tiles;
     const int p = owner ? praw : tiles - 1;

@@ -151,7 +151,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOut
         rec.slot = sl;
         rec.off = bc;
         rec.cnt = c;
-        rec.key = ia - act;
+        rec.key = e;
         rec.j0 = ir - nrg;
         rec.nr = nrg;
         for (int r = 0; r < nrg; ++r) out.ranges[rec.j0 + r] = rec;
@@ -193,7 +193,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOut
     const int ic = wave_incl_scan(sc), ip = wave_incl_scan(sp), ia = wave_incl_scan(sa),
               ir = wave_incl_scan(sr);
     if (lane == kWave - 1) { sh.nranges = ir; sh.nactive = ia; }
-    int bc = ic - sc, bp = ip - sp, ba = ia - sa, br = ir - sr;
+    int bc = ic - sc, bp = ip - sp, br = ir - sr;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = lane * 4 + i;
@@ -207,7 +207,7 @@ __device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOut
           rec.slot = kCheckSlots ? sh.slot[e] : -1;
           rec.off = bc;
           rec.cnt = c[i];
-          rec.key = ba;
+          rec.key = e;
           rec.j0 = br;
           rec.nr = nrg[i];
           for (int r = 0; r < rec.nr; ++r) out.ranges[br + r] = rec;
@@ -215,7 +215,6 @@ __device__ void align_block(AlignShared& sh, int N, int E, int k, const AlignOut
       }
       bc += c[i];
       bp += pd[i];
-      ba += c[i] > 0;
       br += nrg[i];
     }
     if (E == 4 * kWave && lane == kWave - 1) { sh.off[E] = bc; sh.seg[E] = bp; }
@@ -550,7 +549,7 @@ __global__ __launch_bounds__(kNormThreads) void norm_gate_kernel(NormGateArgs a)
         rec.slot = sl;
         rec.off = pos;
         rec.cnt = 1;
-        rec.key = pos;
+        rec.key = id[0];
         rec.j0 = pos;
         rec.nr = 1;
         a.rb.ranges[pos] = rec;

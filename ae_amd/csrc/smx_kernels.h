@@ -28,6 +28,10 @@ constexpr int kUnroll = 4;                          // load steps per chunk (256
 constexpr int kDownRows = 2;                        // row tiles per wave in the down projection
                                                     // (1 for grids that would not fill the chip)
 constexpr int kMaxTokTiles = 4;                     // token tiles per pass (64 tokens)
+// Expert-ordered gate/up items: token tiles per pass at most. The first item's prefetched
+// chunks are copied into the stream's registers; with three or four token tiles that copy
+// exceeds the registers of two workgroups per CU (the kernels spill).
+constexpr int kExpertItemsMaxTiles = 2;
 
 static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
               "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");
@@ -57,7 +61,7 @@ struct RangeRec {
   int64_t slot;  // pool slot of the expert
   int32_t off;   // first sorted position of the expert
   int32_t cnt;   // sorted positions of the expert
-  int32_t key;   // active-expert index
+  int32_t key;   // expert index (the gate/up K-walk rotation)
   int32_t j0;    // first range of the expert
   int32_t nr;    // ranges of the expert: ceil(cnt / span)
   int32_t pad;
@@ -251,9 +255,12 @@ hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int re
                         const int64_t* e2s, int64_t num_slots, const RouteBuffers& rb,
                         hipStream_t s);
 // route_g > 0: the routing runs inside the launch (a.rt), with route_g lanes per token in the
-// top-k; route_multi: the multi-wave form (up to 256 assignments).
+// top-k; route_multi: the multi-wave form (up to 256 assignments); expert_items: its routed
+// items in expert order (every expert one range of one pass), the first item's weights issued
+// before the routing.
 hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
-                         hipStream_t s, int route_g = 0, bool route_multi = false);
+                         hipStream_t s, int route_g = 0, bool route_multi = false,
+                         bool expert_items = false);
 hipError_t launch_down(int dtype, const ExpertArgs& a, int max_ranges, int tok_tiles,
                        hipStream_t s);
 hipError_t launch_combine(int dtype, const CombineArgs& c, hipStream_t s);

@@ -403,6 +403,8 @@ struct AlignOutputs {
   int32_t* tmask;       // [T] per token: bit j set if assignment t*k+j is routable
   int32_t* fpos;        // [N] sorted position of each routable assignment
   int64_t* fslot;       // [N] pool slot of each routable assignment (route only)
+  bool by_expert;       // ranges[e] = expert e's record for every e < E (cnt 0 when it has no
+                        // routable assignment) instead of the compact list (second output only)
   // reference-format outputs (may be null)
   int32_t* sorted_ids;  // [N + E*(BM-1)]
   int32_t* expert_ids;  // [ceil((N + E*(BM-1)) / BM)]
@@ -444,8 +446,10 @@ struct SortWaveLds {
   int run[kWave];
 };
 
+// Inlined: as a call it holds its output structs in scratch, and the call waits for every
+// vector load in flight (the gate/up launch issues its first weight chunks before routing).
 template <bool kCheckSlots>
-__device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E, SortWaveLds& sc,
+__device__ __forceinline__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E, SortWaveLds& sc,
                           const AlignOutputs& out, const AlignOutputs& out2) {
   const int lane = lane_id();
   const int nbits = E > 1 ? 32 - __clz(E - 1) : 0;
@@ -466,7 +470,7 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
     if (e >= 0 && (same & below) == 0) run[e] += __popcll(same);
     __builtin_amdgcn_wave_barrier();
   }
-  // exclusive scans over the experts: compact offset, block-padded segment, active index, range
+  // exclusive scans over the experts: compact offset, block-padded segment, active count, range
   const int ce = lane < E ? run[lane] : 0;
   const int bm = out.bm > 0 ? out.bm : 1;
   const int span = out.span > 0 ? out.span : 1;
@@ -475,7 +479,7 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
   const int nr = div_small(ce + span - 1, span, 1.0f / span);
   const int ic = wave_incl_scan(ce), ip = wave_incl_scan(pad), ia = wave_incl_scan(act),
             ir = wave_incl_scan(nr);
-  const int off = ic - ce, seg = ip - pad, ai = ia - act, br = ir - nr;
+  const int off = ic - ce, seg = ip - pad, br = ir - nr;
   const int seg_total = last_lane(ip);
   const int ranges_total = last_lane(ir);
   const int active_total = last_lane(ia);
@@ -485,19 +489,20 @@ __device__ void sort_wave(const int16_t* ids, const int64_t* slot, int N, int E,
     sc.off[lane] = off;
     sc.seg[lane] = seg;
     run[lane] = off;
-    if (ce > 0 && (out.ranges || out2.ranges)) {
-      RangeRec rec{};
-      rec.slot = kCheckSlots ? slot[lane] : -1;
-      rec.off = off;
-      rec.cnt = ce;
-      rec.key = ai;
-      rec.j0 = br;
-      rec.nr = nr;
+    RangeRec rec{};
+    rec.slot = kCheckSlots ? slot[lane] : -1;
+    rec.off = off;
+    rec.cnt = ce;
+    rec.key = lane;
+    rec.j0 = br;
+    rec.nr = nr;
+    if (ce > 0 && (out.ranges || (out2.ranges && !out2.by_expert))) {
       for (int r = 0; r < nr; ++r) {
         if (out.ranges) out.ranges[br + r] = rec;
-        if (out2.ranges) out2.ranges[br + r] = rec;
+        if (out2.ranges && !out2.by_expert) out2.ranges[br + r] = rec;
       }
     }
+    if (out2.ranges && out2.by_expert) out2.ranges[lane] = rec;  // every expert, cnt 0 if idle
   }
   if (lane == 0) {
     sc.seg[E] = seg_total;
@@ -674,7 +679,7 @@ __device__ __forceinline__ void route_small_wave(const void* logits, int T, int 
       rec.slot = sl;
       rec.off = nless;
       rec.cnt = cnt;
-      rec.key = ai;
+      rec.key = e;
       rec.j0 = j0;
       rec.nr = nr;
       for (int r = 0; r < nr; ++r) {

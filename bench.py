@@ -130,6 +130,9 @@ def parse():
     ap.add_argument("--gateup-waves", type=int, default=None, choices=[0, 1, 2, 4],
                     help="waves per workgroup of the weight-streaming gate/up kernel (0 = the "
                          "library's rule)")
+    ap.add_argument("--expert-items", type=int, default=None, choices=[0, 1],
+                    help="gate/up items of the in-launch routing in expert order where the "
+                         "library's rule takes them (1, the default) or by range (0)")
     ap.add_argument("--gateup-item-walk", type=int, default=None, choices=[0, 1],
                     help="gate/up grids beyond one residency as workgroups walking several items "
                          "(1, the library's default) or one workgroup per item (0)")
@@ -381,19 +384,16 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
     fused_down = not tiled and 1 <= T <= 8 and (T <= fd if fd >= 0 else units <= 48)
     # and whether the routing runs inside the gate/up launch (small batches, logits in the
     # activation dtype)
-    group = 8 if E <= 8 else 16 if E <= 16 else 32 if E <= 32 else 64
+    plan = _lib.plan_info(T, H, I, E, k, dcode, Is)
     on = bool(L.smx_routing_in_gateup())
-    in_launch = on and not tiled and E <= 64 and (
-        (T * k <= 64 and T <= 32 and T * group <= 256) or
-        (T * k <= 256 and T <= 64 and T * group <= 512))
+    in_launch = bool(plan["topk_in_gateup"])
     # larger top-k: its own launch, the sort inside the gate/up launch
     sort_in_launch = in_launch or (on and not tiled and E <= 64 and T * k <= 256 and T <= 64)
     if args.layer:  # the layer call routes from the norm kernel's picks (one token: in the norm)
         in_launch = not tiled and E <= 64 and (T == 1 or (on and T * k <= 256 and T <= 64))
     # one token in one launch (gate/up, then the fused down + combine workgroups in the same
     # grid): the library's plan, when the routing runs inside the launch and nothing captures
-    single = (bool(_lib.plan_info(T, H, I, E, k, dcode, Is)["single_launch"]) and in_launch
-              and not args.layer and not args.graph)
+    single = bool(plan["single_launch"]) and in_launch and not args.layer and not args.graph
 
     for i in range(args.warmup):
         step(i)
@@ -489,6 +489,8 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
                            "top-k kernel, sort inside the gate/up launch" if sort_in_launch
                            else "routing kernels"),
     }
+    if sort_in_launch and plan["expert_items"]:
+        config["gateup_items"] = "expert order, first weights issued before the routing"
     if Is:
         config.update({"shared_ffn": Is, "shared_gate": wl["gated"]})
     if len(layers) > 1:
@@ -698,6 +700,8 @@ def main():
         _lib.check("smx_set_gateup_waves", L.smx_set_gateup_waves(args.gateup_waves))
     if args.gateup_item_walk is not None:
         _lib.check("smx_set_gateup_item_walk", L.smx_set_gateup_item_walk(args.gateup_item_walk))
+    if args.expert_items is not None:
+        _lib.check("smx_set_gateup_expert_items", L.smx_set_gateup_expert_items(args.expert_items))
     g = torch.Generator(device=dev).manual_seed(0)
     es = DTYPES[args.dtype][1]
     page_bytes = 3 * args.hidden * args.ffn * es

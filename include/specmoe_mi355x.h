@@ -363,6 +363,20 @@ int smx_set_gateup_item_walk(int on);
 int smx_gateup_item_walk(void);
 
 /*
+ * Batches routed inside the gate/up launch by its multi-wave form (up to 256 assignments over
+ * at most 64 experts, at most 32 tokens: every expert's tokens one range of one pass) number
+ * their routed work items by expert rather than by the routing's ranges, so that each
+ * workgroup knows its first item before routing the batch and issues that item's first weight
+ * loads first. `on` (the default) does this where fewer than 1 in 20 experts are expected to
+ * get no token (their workgroups' early loads are wasted); 0 numbers items by range. Outputs
+ * are identical either way (same items' arithmetic, same K walk). Process-wide.
+ * Part of the expert-kernel configuration that replaces the reference's per-call Triton grid
+ * (specmoe/layers/fused_moe_kernel.py:293-306).
+ */
+int smx_set_gateup_expert_items(int on);
+int smx_gateup_expert_items(void);
+
+/*
  * One-token MoE calls in one launch. A call of one token whose down projection and combine run
  * as one kernel (smx_set_fused_down_max_tokens) and whose routing runs inside the gate/up launch
  * -- the DeepSeek-V2-Lite and Qwen1.5-MoE blocks at one token -- runs, with `on`, as a single
@@ -423,6 +437,12 @@ enum smx_plan_field {
   SMX_PLAN_SYNC_BLOCKS,         /* single launch: gate/up workgroups the down workgroups wait for */
   SMX_PLAN_SYNC_OFFSET,         /* single launch: workspace byte offset of their flags (8 bytes
                                    each), followed by the status word; -1 otherwise */
+  SMX_PLAN_TOPK_IN_GATEUP,      /* 1: a call given router logits (in the activation dtype) runs
+                                   the top-k inside the gate/up launch (no routing launch) */
+  SMX_PLAN_EXPERT_ITEMS,        /* 1: a call whose gate/up launch routes the batch in its
+                                   multi-wave form (given ids; given logits when
+                                   SMX_PLAN_TOPK_IN_GATEUP is also 1) numbers its routed items
+                                   by expert (smx_set_gateup_expert_items) */
   SMX_PLAN_CHUNK_TOKENS,        /* tokens per pass */
   SMX_PLAN_WORKSPACE_BYTES,     /* workspace of the whole call */
   SMX_PLAN_FIELDS

@@ -22,7 +22,8 @@ import pytest
 
 from ae_amd import build as libbuild
 
-FD_RE = re.compile(r"^(_ZN3smx13gateup_kernel\w*Lb1EEEvNS_10ExpertArgsE):")
+# gateup_kernel<..., FD = true, ST = false>: its last two template arguments
+FD_RE = re.compile(r"^(_ZN3smx13gateup_kernel\w*Lb1ELb0EEEvNS_10ExpertArgsE):")
 
 
 @pytest.fixture(scope="module")
