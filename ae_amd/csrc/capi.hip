@@ -76,15 +76,28 @@ bool g_layer1 = false;
 int g_sync_publish = 1;
 constexpr int64_t kSyncWaitDefaultUs = 100000;
 int64_t g_sync_wait_us = kSyncWaitDefaultUs;
-// The default rule: 4 waves per workgroup, unless the 4-wave grid has a little more than one
-// workgroup per CU (more than kChipCUs but fewer than kGateupFillBlocks): then some CUs hold two
-// of them and finish last, and 2 waves per workgroup (twice the workgroups) spread the load.
+// The default rule: 4 waves per workgroup, unless the 4-wave grid holds between one and two
+// workgroups per CU and 2 waves (twice the workgroups) balance the work over the CUs better by
+// more than kGateupBalanceMargin: a grid of n workgroups keeps n / (kChipCUs * ceil(n /
+// kChipCUs)) of the CUs' time busy when the CUs holding the most workgroups finish last (one
+// to two workgroups per CU at 4 waves leaves many CUs half idle; larger grids have the K split
+// and the item walk).
 // Measured, us per layer, 4 / 2 / 1 waves (same box): DeepSeek-V2-Lite 2 tokens (286
-// workgroups at 4) 51.8 / 48.1 / 50.0 (later 49.8 / 46.1); 1 token (176) 31.1 / 31.9 / 31.8
-// (later 30.3 / 31.1; rocprof gate/up 18.5 / 19.7 us); 4 tokens (506) 73.3 / 73.9 / 82.6;
-// Qwen1.5-MoE 1 token (176) 31.2 / 30.3 / 30.5; Mixtral 1 token (448) 113.5 / 118.7 / 114.1.
+// workgroups at 4; balance 0.56 vs 0.75 at 2 waves) 51.8 / 48.1 / 50.0 (later 49.8 / 46.1);
+// 1 token (176; 0.69 vs 0.69) 31.1 / 31.9 / 31.8 (later 30.3 / 31.1; rocprof gate/up 18.5 /
+// 19.7 us); 4 tokens (506; 0.99 vs 0.99) 73.3 / 73.9 / 82.6; Qwen1.5-MoE 1 token (176) 31.2 /
+// 30.3 / 30.5; Mixtral 1 token (448; 0.875 vs 0.875) 113.5 / 118.7 / 114.1; the fp32 layer of
+// hidden 1024, ffn 2816, 8 experts at 32 tokens (352; 0.69 vs 0.92) 68.4 / 62.3 / 75.0 (gate/up
+// 43.7 / 38.9 / 52.9).
 constexpr int64_t kChipCUs = 256;
-constexpr int64_t kGateupFillBlocks = 320;
+constexpr double kGateupBalanceMargin = 0.05;
+
+// Share of the CUs' time a grid of n equal workgroups keeps busy (the CUs that hold the most of
+// them finish last).
+double cu_balance(int64_t n) {
+  if (n <= 0) return 0.0;
+  return static_cast<double>(n) / static_cast<double>(kChipCUs * ((n + kChipCUs - 1) / kChipCUs));
+}
 // 4-wave gate/up launches of at most two token tiles over rows of at most kGateupKSplitChunks
 // 256-byte chunks split each item's K walk between wave pairs (items of half the length: the
 // launch's last round drains in half the time), unless smx_set_gateup_waves fixes the workgroup
@@ -107,7 +120,10 @@ int gateup_waves(int64_t tiles, int64_t s_tiles, int64_t items, int64_t s_groups
   if (g_gateup_waves > 0) return g_gateup_waves;
   const int64_t blocks4 = items * ((tiles + kExpertWaves - 1) / kExpertWaves) +
                           s_groups * ((s_tiles + kExpertWaves - 1) / kExpertWaves);
-  return blocks4 > kChipCUs && blocks4 < kGateupFillBlocks ? 2 : kExpertWaves;
+  const int64_t blocks2 = items * ((tiles + 1) / 2) + s_groups * ((s_tiles + 1) / 2);
+  return blocks4 > kChipCUs && blocks4 < 2 * kChipCUs &&
+                 cu_balance(blocks2) > cu_balance(blocks4) + kGateupBalanceMargin
+             ? 2 : kExpertWaves;
 }
 
 bool fused_down(int64_t T, int64_t H, int64_t I, int64_t k, int64_t Is, int dtype) {
@@ -286,21 +302,28 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     // leaves only 1 and itself); the shared expert's waves stream about as many chunks as a
     // routed wave. Returns the workgroups expected.
     int64_t ss = 1;
-    auto down_split = [&](int R) {
+    // workgroups of the down grid for R row tiles per wave and sv routed splits (the shared
+    // expert's splits follow: its waves stream about as many chunks as a routed wave)
+    auto down_grid = [&](int R, int64_t sv, int64_t* ssv) {
       const int64_t rgroups = (H / (kRowTile * R) + kExpertWaves - 1) / kExpertWaves;
+      int64_t blocks = ex * rgroups * sv;
+      int64_t sso = 1;
+      if (Is > 0) {
+        const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
+        const int64_t per = nchunks / sv;
+        sso = divisor_at_most(schunks, (schunks + per - 1) / per);
+        blocks += ((T + p.span - 1) / p.span) * rgroups * sso;
+      }
+      if (ssv) *ssv = sso;
+      return blocks;
+    };
+    auto down_split = [&](int R) {
       const int64_t units = ex * (H / (kRowTile * R));
       int64_t want = (kTargetDownWaves + units - 1) / units;
       if (want < 1) want = 1;
       s = divisor_at_least(nchunks, want);
       if (s > 4 * want) s = divisor_at_most(nchunks, want);
-      int64_t blocks = ex * rgroups * s;
-      if (Is > 0) {
-        const int64_t schunks = Is * eb / (static_cast<int64_t>(kStepBytes) * kUnroll);
-        const int64_t per = nchunks / s;
-        ss = divisor_at_most(schunks, (schunks + per - 1) / per);
-        blocks += ((T + p.span - 1) / p.span) * rgroups * ss;
-      }
-      return blocks;
+      return down_grid(R, s, &ss);
     };
     // Two row tiles per wave, unless that grid would not fill one residency of the chip (two
     // workgroups per CU): then one, which doubles the workgroups. Measured, us per down launch,
@@ -314,11 +337,40 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
     // (1088) 72.6 vs 70.7; Qwen1.5-MoE 96 (1088) 70.7 vs 69.0, 128 (1088) 70.9 vs 70.4. Below
     // two residencies the results were mixed (Qwen1.5-MoE 32 tokens, 912: 55.3 vs 56.4;
     // DeepSeek-V2-Lite 16, 848: 52.2 vs 49.5), and there the rule keeps two.
+    // Between one and two residencies with the last round at most half full, the grid of at
+    // most two residencies (both row-tile counts, every split of the K chunks) of the fewest
+    // rounds per workgroup byte -- rounds x (bytes / workgroups), the time of equal workgroups
+    // dealt in rounds -- keeping the wave-target grid on ties. Measured on the fp32 layer of hidden 1024, ffn 2816, 8
+    // experts at 32 tokens (704 workgroups: 2 row tiles, 11 splits), us per down launch: 1
+    // row tile and 4 splits (512) 21.3, 2 and 4 (256) 21.7, 1 and 11 (1408) 22.2, 2 and 11 22.9,
+    // 2 and 22 (1408) 25.5, 2 and 2 (128) 28.0; per layer 68.4 -> 65.7 (fewer partials too).
     const int64_t b2 = down_split(kDownRows);
     const int64_t last = b2 % kDownFillBlocks;
+    auto rounds_per_byte = [](int64_t b) {
+      return static_cast<double>((b + kDownFillBlocks - 1) / kDownFillBlocks) / static_cast<double>(b);
+    };
     if (b2 < kDownFillBlocks || (b2 > 2 * kDownFillBlocks && last > 0 && 2 * last <= kDownFillBlocks)) {
       p.down_rows = 1;
       down_split(1);
+    } else if (b2 > kDownFillBlocks && last > 0 && 2 * last <= kDownFillBlocks) {
+      double best = rounds_per_byte(b2) * (1.0 - 1e-9);
+      int best_r = kDownRows;
+      int64_t best_s = s;
+      for (int R : {kDownRows, 1}) {
+        for (int64_t d = 1; d <= nchunks; ++d) {
+          if (nchunks % d != 0) continue;
+          const int64_t b = down_grid(R, d, nullptr);
+          const double c = rounds_per_byte(b);
+          if (b <= 2 * kDownFillBlocks && c < best) {
+            best = c;
+            best_r = R;
+            best_s = d;
+          }
+        }
+      }
+      p.down_rows = best_r;
+      s = best_s;
+      down_grid(best_r, best_s, &ss);
     }
     p.splits = static_cast<int>(s);
     p.split_steps = static_cast<int>(nchunks / s * kUnroll);
