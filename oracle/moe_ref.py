@@ -1,7 +1,7 @@
 """CPU oracle for SpecMoE's verify-step MoE path -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module,
-and only as the checker (or as the timed CPU restatement in the baseline). The product path
+and only to check results against (or as the timed CPU restatement in the baseline). The product path
 (ae_amd) never imports it and has no CPU fallback.
 
 A plain numpy restatement of the reference's arithmetic:

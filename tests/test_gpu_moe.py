@@ -262,7 +262,7 @@ def test_other_model_shapes(T, H, I, E, k, renorm):
 
 @pytest.mark.parametrize("path", ["default", "tiled"])
 def test_cpu_reference_config(path):
-    """The survey's CPU-path configuration: hidden 1024, ffn 2816, 8 experts, top-2, fp32,
+    """The reference's CPU-runnable configuration: hidden 1024, ffn 2816, 8 experts, top-2, fp32,
     32 tokens (4 sequences x 8 draft tokens) of N(0,1) hidden states, gate and expert weights
     N(0, 0.02), seed 0; the router logits are x Wg^T. On the default plan (weight-streaming
     kernels at 8 tokens per expert) and with the tiled kernels forced."""
