@@ -194,3 +194,34 @@ def test_repeated_calls_on_one_workspace():
                                        inplace=False, workspace=ws) for _ in range(10)]
     torch.cuda.synchronize()
     assert all(torch.equal(y, want) for y in ys)
+
+
+def test_graph_replays_match_eager():
+    """A captured call with expert-ordered items (the top-k launch, then the gate/up launch that
+    sorts its ids) replays to the eager result, with eager calls between the replays."""
+    T, H, I, E, k, Is = 32, 2048, 1408, 64, 6, 2816
+    assert _lib.plan_info(T, H, I, E, k, _lib.SMX_BF16, Is)["expert_items"] == 1
+    x, logits, _, page = _inputs(T, H, E, Is, torch.bfloat16, seed=19, idle=(11,))
+    pool, slots = make_pool(E, H, I, torch.bfloat16, num_slots=E, seed=20)
+    nbytes = _lib.lib().smx_moe_shared_workspace_size(T, H, I, E, k, Is, _lib.SMX_BF16)
+    ws = torch.empty((nbytes,), dtype=torch.uint8, device=DEV)
+    y = torch.empty_like(x)
+    want = fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page, None, 1.0, inplace=False)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fused_moe_shared_forward(x, logits, pool, slots, k, False, page, None, 1.0, inplace=False,
+                                 out=y, workspace=ws)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fused_moe_shared_forward(x, logits, pool, slots, k, False, page, None, 1.0, inplace=False,
+                                 out=y, workspace=ws)
+    for _ in range(4):
+        y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want)
+        fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page, None, 1.0, inplace=False)
+        torch.cuda.synchronize()
