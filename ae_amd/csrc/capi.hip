@@ -501,8 +501,9 @@ int route_group(int64_t E) { return E <= 8 ? 8 : E <= 16 ? 16 : E <= 32 ? 32 : 6
 // given ids (Qwen1.5-MoE 32 tokens 166.5).
 constexpr double kExpertItemsMaxIdle = 0.05;
 bool expert_items_apply(const Plan& p, int64_t T, int64_t E, int64_t k) {
+  // (their routing loads one caller id per thread: at most 256 assignments)
   if (!g_expert_items || T > p.span || p.span > kTokTile * p.tok_tiles ||
-      p.tok_tiles > kExpertItemsMaxTiles || E > kWave || k > E)
+      p.tok_tiles > kExpertItemsMaxTiles || E > kWave || k > E || T * k > kExpertWaves * kWave)
     return false;
   // expected fraction of experts no token picks (picks uniform over the experts)
   const double idle = std::pow(1.0 - static_cast<double>(k) / static_cast<double>(E), static_cast<double>(T));
@@ -525,8 +526,8 @@ int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logit
       p.max_ranges <= kSmallRangesMax)
     return g;
   // the multi-wave form: the workgroup's 4 waves run the top-k, one wave sorts
-  if (T * k <= kRouteInLaunchMax && T <= kWave && (!logits || T * g <= kRouteInLaunchTopkMax) &&
-      p.max_ranges <= kSortRangesMax) {
+  if (T * k <= (logits ? kRouteInLaunchMax : kGateupSortMax) && T <= kWave &&
+      (!logits || T * g <= kRouteInLaunchTopkMax) && p.max_ranges <= kSortRangesMax) {
     *multi = true;
     return g;
   }

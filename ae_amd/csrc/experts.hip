@@ -651,14 +651,15 @@ hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok
   if (route_g == 0) return launch_stage(0, dtype, a, max_ranges, tok_tiles, s);
   // routing inside the launch, every expert one token range (T <= span): one wave routes
   // T*k <= 64 assignments over E <= 64 experts in at most 4 top-k passes; the multi-wave form
-  // takes up to kSortWaveMax assignments and up to four token tiles
+  // takes up to kGateupSortMax assignments and up to four token tiles
   if (route_g != 8 && route_g != 16 && route_g != 32 && route_g != 64) return hipErrorInvalidValue;
   if (a.rt.E > kWave || a.T > a.rb.span || tok_tiles > kMaxTokTiles) return hipErrorInvalidValue;
   if (route_multi) {
-    if (a.T * a.k > kSortWaveMax) return hipErrorInvalidValue;
+    if (a.T * a.k > (a.rt.logits != nullptr ? kSortWaveMax : kGateupSortMax)) return hipErrorInvalidValue;
     // expert-ordered items have one pass of at most tok_tiles token tiles (gateup_passes PRE),
     // at most two (kExpertItemsMaxTiles)
-    if (expert_items && (a.rb.span > kTokTile * tok_tiles || tok_tiles > kExpertItemsMaxTiles))
+    if (expert_items && (a.rb.span > kTokTile * tok_tiles || tok_tiles > kExpertItemsMaxTiles ||
+                         a.T * a.k > kExpertWaves * kWave))
       return hipErrorInvalidValue;
   } else if (a.T * a.k > kWave || tok_tiles > 2 ||
              (a.rt.logits != nullptr && a.T * route_g > kWave * kSmallRoutePasses)) {

@@ -340,7 +340,7 @@ __device__ void layer_down_role(const ExpertArgs& a, u32x4* stage);
 // workgroup meets at a barrier and takes its work item and token rows from there; the first
 // routed workgroup also writes the records (and the top-k results) the later kernels read.
 // The shared-expert workgroups need no routing and start at once.
-// RM: the larger in-launch form (up to kSortWaveMax assignments over E <= 64, T <= 64): the
+// RM: the larger in-launch form (up to kGateupSortMax assignments over E <= 64, T <= 64): the
 // workgroup's 4 waves run the top-k (RG lanes per token; or load caller ids), then wave 0 sorts
 // the assignments (sort_wave) into the workgroup's LDS; the first routed workgroup also
 // writes the records and top-k results, and its threads the token mask.
@@ -420,11 +420,11 @@ __global__ __launch_bounds__(W * kWave, 2) void gateup_kernel(ExpertArgs a) {
     load_raw<kNonTemporal>(pre_b, ws, ord.at(ord.n > 1 ? 1 : 0));
   }
   if constexpr (RG > 0 && RM) {
-    __shared__ int16_t ids_l[kSortWaveMax];
+    __shared__ int16_t ids_l[kGateupSortMax];
     __shared__ int64_t slot_l[kWave];
     __shared__ SortWaveLds sw;
     __shared__ RangeRec rr_l[kSortRangesMax];
-    __shared__ int32_t sf_l[kSortWaveMax];
+    __shared__ int32_t sf_l[kGateupSortMax];
     __shared__ int32_t hdr_l[4];
     __shared__ int32_t cnt_l[kWave];       // own-range form: routable assignments per expert
     __shared__ int32_t wcnt_l[kExpertWaves];

@@ -37,13 +37,16 @@ static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
               "a weight chunk is four 4-row x 256-byte loads covering one 16-row tile");
 
 // In-launch routing (the gate/up kernel routes a small batch itself and keeps the range records
-// in the workgroup's LDS). The one-wave form takes at most 64 assignments, the one-wave sort
-// (sort_wave) at most kSortWaveMax, over at most 64 experts. Range records at most: one per
-// active expert plus one per further span (>= kTokTile sorted positions) of an expert's
-// assignments.
+// in the workgroup's LDS). The one-wave form takes at most 64 assignments; the multi-wave form
+// sorts with the one-wave sort (sort_wave) at most kGateupSortMax given ids (the top-k from
+// logits inside the launch: at most kSortWaveMax assignments), over at most 64 experts. The
+// routing kernel sorts with sort_wave up to kSortWaveMax assignments. Range records at most:
+// one per active expert plus one per further span (>= kTokTile sorted positions) of an
+// expert's assignments.
 constexpr int kSortWaveMax = 256;
+constexpr int kGateupSortMax = 512;
 constexpr int kSmallRangesMax = kWave + kWave / kTokTile;
-constexpr int kSortRangesMax = kWave + kSortWaveMax / kTokTile;
+constexpr int kSortRangesMax = kWave + kGateupSortMax / kTokTile;
 
 // Tiled expert kernels (tiles.hip), for experts that see many tokens: output tiles of
 // 128 token rows by 128 intermediate columns (gate/up) or 256 W2 rows (down) per workgroup.

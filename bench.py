@@ -130,6 +130,9 @@ def parse():
     ap.add_argument("--gateup-waves", type=int, default=None, choices=[0, 1, 2, 4],
                     help="waves per workgroup of the weight-streaming gate/up kernel (0 = the "
                          "library's rule)")
+    ap.add_argument("--routing-in-gateup", type=int, default=None, choices=[0, 1],
+                    help="small batches routed inside the gate/up launch (1, the library's "
+                         "default) or by the routing kernels (0)")
     ap.add_argument("--expert-items", type=int, default=None, choices=[0, 1],
                     help="gate/up items of the in-launch routing in expert order where the "
                          "library's rule takes them (1, the default) or by range (0)")
@@ -388,7 +391,7 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
     on = bool(L.smx_routing_in_gateup())
     in_launch = bool(plan["topk_in_gateup"])
     # larger top-k: its own launch, the sort inside the gate/up launch
-    sort_in_launch = in_launch or (on and not tiled and E <= 64 and T * k <= 256 and T <= 64)
+    sort_in_launch = in_launch or (on and not tiled and E <= 64 and T * k <= 512 and T <= 64)
     if args.layer:  # the layer call routes from the norm kernel's picks (one token: in the norm)
         in_launch = not tiled and E <= 64 and (T == 1 or (on and T * k <= 256 and T <= 64))
     # one token in one launch (gate/up, then the fused down + combine workgroups in the same
@@ -700,6 +703,8 @@ def main():
         _lib.check("smx_set_gateup_waves", L.smx_set_gateup_waves(args.gateup_waves))
     if args.gateup_item_walk is not None:
         _lib.check("smx_set_gateup_item_walk", L.smx_set_gateup_item_walk(args.gateup_item_walk))
+    if args.routing_in_gateup is not None:
+        _lib.check("smx_set_routing_in_gateup", L.smx_set_routing_in_gateup(args.routing_in_gateup))
     if args.expert_items is not None:
         _lib.check("smx_set_gateup_expert_items", L.smx_set_gateup_expert_items(args.expert_items))
     g = torch.Generator(device=dev).manual_seed(0)

@@ -273,3 +273,86 @@ def test_in_launch_routing_many_experts(T, H, I, E, k):
                                                   slots.cpu().numpy(), k, True, TORCH_TO_ORACLE[dtype])
     np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
     assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("T,H,I,E,k,P", [
+    (43, 256, 128, 64, 6, 70),     # 258 assignments: past the routing kernel's one-wave sort
+    (64, 128, 256, 64, 6, 64),     # 384
+    (64, 256, 128, 32, 8, 36),     # 512, the largest sort inside gate/up
+    (57, 128, 128, 60, 7, 60),     # 399, ragged token tiles
+])
+def test_fused_forward_sort_in_gateup_past_256(T, H, I, E, k, P):
+    """257..512 assignments: the top-k launch, then the gate/up launch sorts its ids (one wave
+    in the records' writer, the own range in every other workgroup) -- the routing kernels'
+    records and outputs, bit for bit, and the oracle's."""
+    dtype = torch.bfloat16
+    x, logits = _inputs(T, H, E, dtype, seed=T * 13 + E)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E + k + 3)
+    if P > E:
+        slots[4] = P + 2
+    outs = _both(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                           return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y, w, ids = outs[True]
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, "bf16")
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("T", [48, 64])
+def test_deepseek_block_sort_in_gateup_past_256(T):
+    """The DeepSeek-V2-Lite block at 48 and 64 tokens (288 and 384 assignments)."""
+    H, I, E, k, Is = 2048, 1408, 64, 6, 2816
+    x, logits = _inputs(T, H, E, torch.bfloat16, seed=110 + T)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=111)
+    g = torch.Generator(device=DEV).manual_seed(112)
+    page = (torch.randn((3 * Is * H,), generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    outs = _both(lambda: fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page,
+                                                  None, 1.0, inplace=False, return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y_ref, _, _ = ref.fused_moe_shared_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                               slots.cpu().numpy(), k, False, "bf16",
+                                               shared_page=to_oracle(page))
+    assert max_rel_err(f32_of(outs[True][0]), y_ref) <= TOL[torch.bfloat16]
+
+
+def test_stack_and_layer_call_sort_in_gateup_past_256():
+    """Caller ids (repeated, dropped, out of range) at 400 assignments through stack_fused_moe,
+    and the layer call's norm picks at 384."""
+    T, H, I, E, k = 50, 256, 128, 64, 8
+    x, _ = _inputs(T, H, E, torch.bfloat16, seed=121)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=122)
+    slots[9] = 1000
+    g = torch.Generator(device=DEV).manual_seed(123)
+    ids = torch.randint(0, E, (T, k), generator=g, device=DEV, dtype=torch.int32)
+    ids[0, :3] = 5
+    ids[1, 2] = -1
+    ids[2, 4] = E + 3
+    w = torch.rand((T, k), generator=g, device=DEV)
+    logits = torch.zeros((T, E), dtype=torch.bfloat16, device=DEV)
+    outs = _both(lambda: stack_fused_moe(x.clone(), pool, slots, logits, w, ids, False))
+    assert torch.equal(outs[True], outs[False])
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
+    assert max_rel_err(f32_of(outs[True]), y_ref) <= TOL[torch.bfloat16]
+
+    T, E, k, dt = 64, 64, 6, torch.bfloat16
+    x = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    r = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    nw = (torch.randn((H,), generator=g, device=DEV) * 0.1 + 1).to(dt)
+    gw = (torch.randn((E, H), generator=g, device=DEV) * 0.05).to(dt)
+    pool, slots = make_pool(E, H, I, dt, num_slots=E + 3, seed=124)
+
+    def run():
+        xx, rr = x.clone(), r.clone()
+        y, (lg, w, ids) = moe_layer_forward(xx, rr, nw, 1e-6, gw, pool, slots, k, False,
+                                            return_routing=True)
+        return y, rr, lg, w, ids
+
+    outs = _both(run)
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
