@@ -513,21 +513,24 @@ bool expert_items_apply(const Plan& p, int64_t T, int64_t E, int64_t k) {
 // The routing runs inside the gate/up launch (no routing launch) for batches one wave routes:
 // T*k <= 64 assignments over E <= 64 experts, every expert one token range of at most two
 // token tiles, the top-k (when logits are given, in the activation dtype) in at most 4 passes
-// of 64/G tokens. Returns G, or 0 when the routing kernels run instead. With logits and a 0
+// of 64/G tokens; and in the multi-wave form (see below). Returns G, or 0 when the routing
+// kernels run instead. With logits and a 0
 // here, fused_forward asks again without them: the top-k launch runs and gate/up sorts its ids.
 int in_launch_route_g(const Plan& p, int64_t T, int64_t E, int64_t k, bool logits, bool logits_dt_ok,
                       bool* multi) {
   *multi = false;
   if (!g_route_in_gateup) return 0;
-  if (p.tiled || T < 1 || E > kWave || T > p.span || (logits && !logits_dt_ok)) return 0;
+  if (p.tiled || T < 1 || E > kWave || (logits && !logits_dt_ok)) return 0;
   const int g = route_group(E);
   // the workgroup's LDS copy of the range records holds every range the launch's grid covers
-  if (T * k <= kWave && p.tok_tiles <= 2 && (!logits || T * g <= kWave * kSmallRoutePasses) &&
+  if (T <= p.span && T * k <= kWave && p.tok_tiles <= 2 && (!logits || T * g <= kWave * kSmallRoutePasses) &&
       p.max_ranges <= kSmallRangesMax)
     return g;
-  // the multi-wave form: the workgroup's 4 waves run the top-k, one wave sorts
-  if (T * k <= (logits ? kRouteInLaunchMax : kGateupSortMax) && T <= kWave &&
-      (!logits || T * g <= kRouteInLaunchTopkMax) && p.max_ranges <= kSortRangesMax) {
+  // the multi-wave form: the workgroup's 4 waves run the top-k, one wave sorts; given ids may
+  // put an expert's assignments in several token ranges (T > span)
+  if ((logits ? T <= p.span && T <= kWave && T * k <= kRouteInLaunchMax && T * g <= kRouteInLaunchTopkMax
+              : T * k <= kGateupSortMax) &&
+      p.max_ranges <= kSortRangesMax) {
     *multi = true;
     return g;
   }

@@ -642,6 +642,11 @@ static void launch_gateup_routed_dt(const ExpertArgs& a, int max_ranges, int tok
     else launch_gateup_routed<DT, 2, false>(a, max_ranges, route_g, s);
     return;
   }
+  if (a.T > a.rb.span) {
+    // given ids whose experts may span several token ranges (the ids need no top-k lanes)
+    launch_gateup_w<true, DT, kMaxTokTiles, 64, true>(a, max_ranges, s);
+    return;
+  }
   if (expert_items) launch_gateup_multi<DT, true>(a, max_ranges, tok_tiles, route_g, s);
   else launch_gateup_multi<DT, false>(a, max_ranges, tok_tiles, route_g, s);
 }
@@ -653,7 +658,11 @@ hipError_t launch_gateup(int dtype, const ExpertArgs& a, int max_ranges, int tok
   // T*k <= 64 assignments over E <= 64 experts in at most 4 top-k passes; the multi-wave form
   // takes up to kGateupSortMax assignments and up to four token tiles
   if (route_g != 8 && route_g != 16 && route_g != 32 && route_g != 64) return hipErrorInvalidValue;
-  if (a.rt.E > kWave || a.T > a.rb.span || tok_tiles > kMaxTokTiles) return hipErrorInvalidValue;
+  if (a.rt.E > kWave || tok_tiles > kMaxTokTiles) return hipErrorInvalidValue;
+  // several token ranges per expert (T > span): given ids in the multi-wave form, four tiles
+  const bool ranges_multi = a.T > a.rb.span;
+  if (ranges_multi && (!route_multi || a.rt.logits != nullptr || tok_tiles != kMaxTokTiles || expert_items))
+    return hipErrorInvalidValue;
   if (route_multi) {
     if (a.T * a.k > (a.rt.logits != nullptr ? kSortWaveMax : kGateupSortMax)) return hipErrorInvalidValue;
     // expert-ordered items have one pass of at most tok_tiles token tiles (gateup_passes PRE),

@@ -39,12 +39,13 @@ static_assert(kUnroll * kStepBytes == 256 && kRowTile == 16,
 // In-launch routing (the gate/up kernel routes a small batch itself and keeps the range records
 // in the workgroup's LDS). The one-wave form takes at most 64 assignments; the multi-wave form
 // sorts with the one-wave sort (sort_wave) at most kGateupSortMax given ids (the top-k from
-// logits inside the launch: at most kSortWaveMax assignments), over at most 64 experts. The
+// logits inside the launch: at most kSortWaveMax assignments), over at most 64 experts; with
+// given ids an expert's assignments may span several token ranges (T > span). The
 // routing kernel sorts with sort_wave up to kSortWaveMax assignments. Range records at most:
 // one per active expert plus one per further span (>= kTokTile sorted positions) of an
 // expert's assignments.
 constexpr int kSortWaveMax = 256;
-constexpr int kGateupSortMax = 512;
+constexpr int kGateupSortMax = 768;
 constexpr int kSmallRangesMax = kWave + kWave / kTokTile;
 constexpr int kSortRangesMax = kWave + kGateupSortMax / kTokTile;
 

@@ -391,9 +391,9 @@ def run_tokens(args, wl, T, layers, L, dev, light=False):
     on = bool(L.smx_routing_in_gateup())
     in_launch = bool(plan["topk_in_gateup"])
     # larger top-k: its own launch, the sort inside the gate/up launch
-    sort_in_launch = in_launch or (on and not tiled and E <= 64 and T * k <= 512 and T <= 64)
+    sort_in_launch = in_launch or (on and not tiled and E <= 64 and T * k <= 768)
     if args.layer:  # the layer call routes from the norm kernel's picks (one token: in the norm)
-        in_launch = not tiled and E <= 64 and (T == 1 or (on and T * k <= 256 and T <= 64))
+        in_launch = not tiled and E <= 64 and (T == 1 or (on and T * k <= 768))
     # one token in one launch (gate/up, then the fused down + combine workgroups in the same
     # grid): the library's plan, when the routing runs inside the launch and nothing captures
     single = bool(plan["single_launch"]) and in_launch and not args.layer and not args.graph

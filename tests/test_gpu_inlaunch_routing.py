@@ -356,3 +356,93 @@ def test_stack_and_layer_call_sort_in_gateup_past_256():
     outs = _both(run)
     for a, b in zip(outs[True], outs[False]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("T,H,I,E,k,P,hot", [
+    (96, 256, 128, 64, 6, 70, 0),      # 576 assignments, T > span: several ranges per expert possible
+    (128, 128, 256, 64, 6, 64, 0),     # 768, the largest sort inside gate/up
+    (128, 256, 256, 8, 2, 8, 2),       # experts over 64 tokens: two to four ranges each
+    (200, 128, 128, 16, 3, 18, 3),     # 600, three experts with hot logits
+])
+def test_fused_forward_sort_in_gateup_several_ranges(T, H, I, E, k, P, hot):
+    """Given ids (the top-k launch's) past one token range per expert: the gate/up launch sorts
+    them (records of several ranges per expert, weights read side by side with normal caching),
+    with the routing kernels' records and outputs bit for bit, and the oracle's."""
+    dtype = torch.bfloat16
+    g = torch.Generator(device=DEV).manual_seed(T + E + k)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dtype)
+    lg = torch.randn((T, E), generator=g, device=DEV) * 2.0
+    lg[:, :hot] += 4.0  # most tokens pick the first `hot` experts
+    logits = lg.to(dtype)
+    pool, slots = make_pool(E, H, I, dtype, num_slots=P, seed=E + k + 5)
+    if P > E:
+        slots[E - 1] = P + 4
+    outs = _both(lambda: fused_moe_forward(x.clone(), logits, pool, slots, k, True, inplace=False,
+                                           return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y, w, ids = outs[True]
+    if hot:
+        assert int((ids == 0).sum()) > 64  # expert 0 spans several ranges
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, True, "bf16")
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    assert max_rel_err(f32_of(y), y_ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("T", [96, 128])
+def test_deepseek_block_sort_in_gateup_several_ranges(T):
+    """The DeepSeek-V2-Lite block at 96 and 128 tokens (576 and 768 assignments)."""
+    H, I, E, k, Is = 2048, 1408, 64, 6, 2816
+    x, logits = _inputs(T, H, E, torch.bfloat16, seed=130 + T)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=131)
+    g = torch.Generator(device=DEV).manual_seed(132)
+    page = (torch.randn((3 * Is * H,), generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    outs = _both(lambda: fused_moe_shared_forward(x.clone(), logits, pool, slots, k, False, page,
+                                                  None, 1.0, inplace=False, return_routing=True))
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
+    y_ref, _, _ = ref.fused_moe_shared_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                               slots.cpu().numpy(), k, False, "bf16",
+                                               shared_page=to_oracle(page))
+    assert max_rel_err(f32_of(outs[True][0]), y_ref) <= TOL[torch.bfloat16]
+
+
+def test_stack_and_layer_call_several_ranges():
+    """Caller ids at 700 assignments with one expert named by most tokens (several ranges),
+    repeats and drops, through stack_fused_moe; the layer call's norm picks at 128 tokens."""
+    T, H, I, E, k = 100, 256, 128, 64, 7
+    x, _ = _inputs(T, H, E, torch.bfloat16, seed=141)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=142)
+    slots[9] = 1000
+    g = torch.Generator(device=DEV).manual_seed(143)
+    ids = torch.randint(0, E, (T, k), generator=g, device=DEV, dtype=torch.int32)
+    ids[:90, 0] = 3        # expert 3 takes 90+ assignments: two ranges
+    ids[0, :3] = 5
+    ids[1, 2] = -1
+    ids[2, 4] = E + 3
+    w = torch.rand((T, k), generator=g, device=DEV)
+    logits = torch.zeros((T, E), dtype=torch.bfloat16, device=DEV)
+    outs = _both(lambda: stack_fused_moe(x.clone(), pool, slots, logits, w, ids, False))
+    assert torch.equal(outs[True], outs[False])
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(),
+                                w.cpu().numpy(), ids.cpu().numpy(), "bf16", E)
+    assert max_rel_err(f32_of(outs[True]), y_ref) <= TOL[torch.bfloat16]
+
+    T, E, k, dt = 128, 64, 6, torch.bfloat16
+    x = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    r = torch.randn((T, H), generator=g, device=DEV).to(dt)
+    nw = (torch.randn((H,), generator=g, device=DEV) * 0.1 + 1).to(dt)
+    gw = (torch.randn((E, H), generator=g, device=DEV) * 0.05).to(dt)
+    pool, slots = make_pool(E, H, I, dt, num_slots=E + 3, seed=144)
+
+    def run():
+        xx, rr = x.clone(), r.clone()
+        y, (lg, w, ids) = moe_layer_forward(xx, rr, nw, 1e-6, gw, pool, slots, k, False,
+                                            return_routing=True)
+        return y, rr, lg, w, ids
+
+    outs = _both(run)
+    for a, b in zip(outs[True], outs[False]):
+        assert torch.equal(a, b)
