@@ -30,6 +30,9 @@ SIGNATURES = [
     ("smx_error_string", ctypes.c_char_p, [_i32]),
     ("smx_topk_softmax", ctypes.c_int,
      [_c_void_p, _i32, _i64, _i64, _i64, _i32, _c_void_p, _c_void_p, _c_void_p]),
+    ("smx_grouped_topk", ctypes.c_int,
+     [_c_void_p, _i32, _i64, _i64, _i64, _i32, _i64, _i64, _c_void_p, _c_void_p, _c_void_p,
+      _c_void_p]),
     ("smx_moe_align_block_size", ctypes.c_int,
      [_c_void_p, _i64, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     ("smx_moe_workspace_size", _sz, [_i64, _i64, _i64, _i64, _i64, _i32]),

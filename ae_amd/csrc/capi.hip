@@ -760,6 +760,24 @@ int smx_topk_softmax(const void* logits, int logits_dtype, int64_t T, int64_t E,
                                               static_cast<hipStream_t>(stream)));
 }
 
+int smx_grouped_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t top_k,
+                     int renormalize, int64_t num_expert_group, int64_t topk_group,
+                     const float* correction_bias, float* topk_weights, int32_t* topk_ids, void* stream) {
+  if (T < 0 || E <= 0 || top_k <= 0 || !valid_dtype(logits_dtype) || num_expert_group <= 0 ||
+      topk_group <= 0 || topk_group > num_expert_group || E % num_expert_group != 0)
+    return SMX_ERR_INVALID_ARG;
+  const int64_t gs = E / num_expert_group;
+  if (top_k > topk_group * gs || (correction_bias && gs < 2)) return SMX_ERR_INVALID_ARG;
+  if (E > kMaxExperts || top_k > kMaxTopK || num_expert_group > kWave || T > (int64_t{1} << 30) / top_k)
+    return SMX_ERR_UNSUPPORTED;
+  if (T == 0) return SMX_OK;
+  if (!logits || !topk_weights || !topk_ids) return SMX_ERR_INVALID_ARG;
+  return static_cast<int>(launch_grouped_topk(
+      logits, logits_dtype, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k), renormalize,
+      static_cast<int>(num_expert_group), static_cast<int>(topk_group), correction_bias, topk_weights,
+      topk_ids, static_cast<hipStream_t>(stream)));
+}
+
 int smx_moe_align_block_size(const int32_t* topk_ids, int64_t numel, int64_t E, int64_t block_size,
                              int32_t* sorted_ids, int32_t* expert_ids, int32_t* num_tokens_post_pad,
                              void* stream) {

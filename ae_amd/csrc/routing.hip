@@ -34,6 +34,179 @@ __global__ __launch_bounds__(256) void topk_softmax_kernel(const void* __restric
 }
 
 // ---------------------------------------------------------------------------------------
+// Grouped top-k: sglang 0.4.5.post3's grouped_topk (no correction bias) and
+// biased_grouped_topk (with one), which select_experts runs for use_grouped_topk (call site
+// specmoe/layers/FusedMoE.py:174-185; sglang is not vendored). The E experts form ng groups
+// of gs = E / ng consecutive experts. One wave per token; lane l holds experts l + 64 i.
+//   score s   softmax (the arithmetic of topk_softmax_kernel, so the same p bit for bit), or
+//             with a bias sigmoid(x): 1 / (1 + exp(-x)) for x >= 0, e / (1 + e) with
+//             e = exp(x) below, exp by exp_nonpos;
+//   choice c  s, or s + bias[e];
+//   group     max of c over the group, or with a bias the sum of its two largest c; the
+//             topk_group best groups (descending, ties to the lower group) stay selectable;
+//   picks     the k best selectable experts by c (descending, ties to the lower expert) in
+//             that order; weight = s of the pick, renormalised by the picks' sum in pick order.
+// Ranks compare 64-bit keys: the order-preserving image of the value's bits (NaN ranks as
+// -inf, -0 as +0) above 0xffff - index; key 0 is "not selectable", below every value.
+// ---------------------------------------------------------------------------------------
+struct GroupedTopkArgs {
+  const void* logits;
+  const float* bias;  // [E] correction bias; null: softmax scores
+  float* w;           // [T, k]
+  int32_t* ids;       // [T, k]
+  int T, E, k, ng, tg, renorm;
+};
+
+constexpr int kGroupedWaves = 4;
+
+__device__ __forceinline__ uint64_t rank_key(float v, int idx) {
+#pragma clang fp contract(off)
+  v = (v != v) ? -__builtin_inff() : v + 0.0f;
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // -inf -> 0x007fffff > 0
+  return (static_cast<uint64_t>(o) << 32) | static_cast<uint32_t>(0xffff - idx);
+}
+
+__device__ __forceinline__ int rank_index(uint64_t key) {
+  return 0xffff - static_cast<int>(static_cast<uint32_t>(key) & 0xffffu);
+}
+
+// Maximum over the wave's 64 lanes; every lane gets it.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint64_t o = __shfl_xor(k, off, kWave);
+    k = o > k ? o : k;
+  }
+  return k;
+}
+
+__device__ __forceinline__ float sigmoid_score(float x) {
+#pragma clang fp contract(off)
+  if (x >= 0.0f) return 1.0f / (1.0f + exp_nonpos(-x));
+  const float e = exp_nonpos(x);  // x < 0 or NaN
+  return e / (1.0f + e);
+}
+
+template <int LDT>
+__global__ __launch_bounds__(kGroupedWaves * kWave) void grouped_topk_kernel(GroupedTopkArgs a) {
+#pragma clang fp contract(off)
+  constexpr int PL = kMaxExpertsPerLane;
+  __shared__ float cs[kGroupedWaves][kMaxExperts];  // choice per expert
+  __shared__ float ss[kGroupedWaves][kMaxExperts];  // score per expert
+  const int wave = threadIdx.x / kWave;
+  const int lane = lane_id();
+  const int E = a.E;
+  const int gs = E / a.ng;
+  const bool biased = a.bias != nullptr;
+  float b[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int e = lane + kWave * i;
+    b[i] = (biased && e < E) ? a.bias[e] : 0.0f;
+  }
+  for (int t = blockIdx.x * kGroupedWaves + wave; t < a.T; t += gridDim.x * kGroupedWaves) {
+    float v[PL];
+    load_logits<LDT, kWave, PL>(a.logits, t, a.T, E, v);  // experts past E read -inf
+    float s[PL], c[PL];
+    if (!biased) {
+      float m = v[0];
+#pragma unroll
+      for (int i = 1; i < PL; ++i) m = fmaxf(m, v[i]);
+      m = group_reduce<kWave>(m, [](float p, float q) { return fmaxf(p, q); });
+      float sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        s[i] = (lane + kWave * i < E) ? exp_nonpos(v[i] - m) : 0.0f;
+        sum = (i == 0) ? s[i] : sum + s[i];
+      }
+      sum = group_reduce<kWave>(sum, [](float p, float q) { return p + q; });
+      const float inv = 1.0f / sum;
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        s[i] = s[i] * inv;
+        c[i] = s[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < PL; ++i) {
+        s[i] = sigmoid_score(v[i]);
+        c[i] = s[i] + b[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int e = lane + kWave * i;
+      if (e < E) {
+        cs[wave][e] = c[i];
+        ss[wave][e] = s[i];
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // group scores: lane g < ng scans group g
+    uint64_t gk = 0;
+    if (lane < a.ng) {
+      const float* cg = &cs[wave][lane * gs];
+      float score;
+      if (!biased) {
+        score = cg[0];
+        for (int q = 1; q < gs; ++q) score = fmaxf(score, cg[q]);
+      } else {
+        float m1 = -__builtin_inff(), m2 = -__builtin_inff();
+        for (int q = 0; q < gs; ++q) {
+          const float x = cg[q];
+          if (x > m1) {
+            m2 = m1;
+            m1 = x;
+          } else if (x > m2) {
+            m2 = x;
+          }
+        }
+        score = m1 + m2;
+      }
+      gk = rank_key(score, lane);
+    }
+    uint64_t gsel = 0;  // bit g: group g selectable (tg <= ng: every round finds a group)
+    for (int r = 0; r < a.tg; ++r) {
+      const int g = rank_index(wave_max_key(gk)) & (kWave - 1);
+      gsel |= uint64_t{1} << g;
+      if (lane == g) gk = 0;
+    }
+    uint64_t ck[PL];
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int e = lane + kWave * i;
+      ck[i] = (e < E && ((gsel >> (e / gs)) & 1)) ? rank_key(c[i], e) : 0;
+    }
+    // k <= tg * gs: every round picks a selectable expert
+    float wv = 0.0f, sum = 0.0f;
+    int id = 0;
+    for (int r = 0; r < a.k; ++r) {
+      uint64_t best = ck[0];
+#pragma unroll
+      for (int i = 1; i < PL; ++i) best = ck[i] > best ? ck[i] : best;
+      int e = rank_index(wave_max_key(best));
+      e = e < E ? e : E - 1;  // in range whenever the host's limits hold
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        if (lane + kWave * i == e) ck[i] = 0;
+      const float se = ss[wave][e];
+      if (lane == r) {
+        wv = se;
+        id = e;
+      }
+      sum = (r == 0) ? se : sum + se;
+    }
+    if (lane < a.k) {
+      const int64_t o = static_cast<int64_t>(t) * a.k + lane;
+      a.w[o] = a.renorm ? wv / sum : wv;
+      a.ids[o] = id;
+    }
+    __builtin_amdgcn_wave_barrier();  // the next token rewrites this wave's LDS rows
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Expert sort of flat assignments f = t*k + j held in LDS (ids_l[f], -1 = dropped).
 // Stable: within an expert, assignments appear in ascending f. Each wave walks a contiguous
 // range of f in 64-wide chunks; the lanes of a chunk that share an expert are found with one
@@ -629,6 +802,19 @@ hipError_t launch_topk_softmax(const void* logits, int ldt, int T, int E, int k,
     case kF32: topk_launch_g<kF32>(logits, T, E, k, renorm, w, ids, s); break;
     case kF16: topk_launch_g<kF16>(logits, T, E, k, renorm, w, ids, s); break;
     default: topk_launch_g<kBF16>(logits, T, E, k, renorm, w, ids, s); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_grouped_topk(const void* logits, int ldt, int T, int E, int k, int renorm, int ng,
+                               int tg, const float* bias, float* w, int32_t* ids, hipStream_t s) {
+  const GroupedTopkArgs a{logits, bias, w, ids, T, E, k, ng, tg, renorm};
+  int blocks = (T + kGroupedWaves - 1) / kGroupedWaves;
+  if (blocks > 4096) blocks = 4096;  // the waves walk the rest
+  switch (ldt) {
+    case kF32: grouped_topk_kernel<kF32><<<blocks, kGroupedWaves * kWave, 0, s>>>(a); break;
+    case kF16: grouped_topk_kernel<kF16><<<blocks, kGroupedWaves * kWave, 0, s>>>(a); break;
+    default: grouped_topk_kernel<kBF16><<<blocks, kGroupedWaves * kWave, 0, s>>>(a); break;
   }
   return hipGetLastError();
 }

@@ -252,6 +252,10 @@ hipError_t launch_norm_gate(const NormGateArgs& a, hipStream_t s);
 
 hipError_t launch_topk_softmax(const void* logits, int ldt, int T, int E, int k, int renorm,
                                float* w, int32_t* ids, hipStream_t s);
+// Grouped top-k (ng groups of E / ng experts, topk_group of them selectable; bias: the
+// sigmoid scores with a correction bias, else softmax). Limits checked by the caller.
+hipError_t launch_grouped_topk(const void* logits, int ldt, int T, int E, int k, int renorm, int ng,
+                               int tg, const float* bias, float* w, int32_t* ids, hipStream_t s);
 hipError_t launch_align(const int32_t* ids, int N, int E, int bm, int32_t* sorted_ids,
                         int32_t* expert_ids, int32_t* ntp, hipStream_t s);
 hipError_t launch_route(const void* logits, int ldt, int T, int E, int k, int renorm,

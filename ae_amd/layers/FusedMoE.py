@@ -21,7 +21,7 @@ from typing import Callable, List, Optional, Tuple
 import torch
 
 from .fused_moe_kernel import fused_moe_forward, stack_fused_moe
-from .topk import check_routing_options, select_experts
+from .topk import check_routing_options, needs_grouped_topk, select_experts
 
 
 def _tp_rank_world() -> Tuple[int, int]:
@@ -118,11 +118,15 @@ class UnquantizedFusedMoEMethod:
         pool = getattr(layer.ws, "gpu_cache", None)
         if pool is None:
             raise RuntimeError("no expert pool attached: set ws.gpu_cache before forward")
-        if custom_routing_function is not None:
-            # the caller's routing, then the experts on the pool (reference :174-196)
+        if custom_routing_function is not None or needs_grouped_topk(
+                use_grouped_topk, topk_group, num_expert_group, correction_bias):
+            # a caller's routing or the grouped top-k, then the experts on the pool
+            # (reference :174-196)
             topk_weights, topk_ids = select_experts(
-                x, router_logits, top_k, use_grouped_topk, renormalize,
-                custom_routing_function=custom_routing_function)
+                x, router_logits, top_k, use_grouped_topk, renormalize, topk_group=topk_group,
+                num_expert_group=num_expert_group,
+                custom_routing_function=custom_routing_function,
+                correction_bias=correction_bias, routed_scaling_factor=routed_scaling_factor)
             return stack_fused_moe(x, pool, expert_cache_indices, router_logits, topk_weights,
                                    topk_ids, renormalize, inplace=True)
         return fused_moe_forward(x, router_logits, pool, expert_cache_indices, top_k,

@@ -10,12 +10,13 @@ from .layernorm import RMSNorm, add_rmsnorm_gate
 from .mixtral_moe import MixtralMoE
 from .moe_layer import PostAttentionMoE, moe_layer_forward
 from .shared_moe import DeepseekV2MoE, Qwen2MoeSparseMoeBlock, SharedExpertMoE
-from .topk import fused_topk, select_experts
+from .topk import fused_topk, grouped_topk, select_experts
 
 __all__ = [
     "FusedMoE", "UnquantizedFusedMoEMethod", "set_weight_attrs", "fused_moe_forward",
     "fused_moe_shared_forward", "moe_align_block_size", "stack_fused_moe", "MixtralMoE",
-    "SharedExpertMoE", "Qwen2MoeSparseMoeBlock", "DeepseekV2MoE", "fused_topk", "select_experts",
+    "SharedExpertMoE", "Qwen2MoeSparseMoeBlock", "DeepseekV2MoE", "fused_topk", "grouped_topk",
+    "select_experts",
     "RMSNorm", "add_rmsnorm_gate", "PostAttentionMoE", "moe_layer_forward",
     "set_tiled_min_tokens", "tiled_min_tokens", "set_fused_down_max_tokens",
     "fused_down_max_tokens", "set_fp32_gemm_outputs_fp16", "fp32_gemm_outputs_fp16",

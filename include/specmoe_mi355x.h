@@ -74,6 +74,30 @@ int smx_topk_softmax(const void* logits, int logits_dtype, int64_t T, int64_t E,
                      float* topk_weights, int32_t* topk_ids, void* stream);
 
 /*
+ * Grouped routing: the E experts form num_expert_group groups of gs = E / num_expert_group
+ * consecutive experts, and only the topk_group best groups are selectable.
+ *   correction_bias == NULL: scores s = the fp32 softmax of smx_topk_softmax (same bits);
+ *     choice c = s; a group's score is the max of c over it.
+ *   correction_bias [E] fp32: scores s = sigmoid(logit) (1/(1+exp(-x)) for x >= 0,
+ *     e/(1+e) with e = exp(x) below); c = s + correction_bias; a group's score is the sum of
+ *     its two largest c (needs gs >= 2).
+ * Groups rank by descending score (ties to the lower group); the top_k selectable experts
+ * by descending c (ties to the lower expert) are the picks, in that order; their weights are
+ * s (not c), renormalised by the picks' sum when renormalize != 0. NaN ranks as -inf.
+ * Replaces sglang.srt.layers.moe.topk.select_experts(use_grouped_topk=True) as called at
+ * specmoe/layers/FusedMoE.py:174-185 (sglang==0.4.5.post3: grouped_topk without a bias,
+ * biased_grouped_topk with one).
+ *   logits [T, E] of logits_dtype; topk_weights [T, top_k] fp32 out, topk_ids [T, top_k]
+ *   int32 out. Needs E % num_expert_group == 0, 1 <= topk_group <= num_expert_group and
+ *   top_k <= topk_group * gs (SMX_ERR_INVALID_ARG otherwise); num_expert_group <= 64 (else
+ *   SMX_ERR_UNSUPPORTED).
+ */
+int smx_grouped_topk(const void* logits, int logits_dtype, int64_t T, int64_t E, int64_t top_k,
+                     int renormalize, int64_t num_expert_group, int64_t topk_group,
+                     const float* correction_bias, float* topk_weights, int32_t* topk_ids,
+                     void* stream);
+
+/*
  * Token/expert alignment in the reference's padded format.
  * Replaces moe_align_block_size (specmoe/layers/fused_moe_kernel.py:16-85, which wraps
  * sgl_kernel.moe_align_block_size from sgl-kernel==0.1.2).

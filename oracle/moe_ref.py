@@ -183,6 +183,74 @@ def topk_softmax(logits: np.ndarray, top_k: int, renormalize: bool):
 select_experts = topk_softmax
 
 
+def sigmoid_scores(logits: np.ndarray) -> np.ndarray:
+    """fp32 sigmoid with the routing exp: 1 / (1 + exp(-x)) for x >= 0, e / (1 + e) with
+    e = exp(x) for x < 0 (exp_nonpos either way; each step one IEEE fp32 operation)."""
+    x = np.asarray(logits, dtype=np.float32)
+    pos = x >= _f32(0.0)
+    e = exp_nonpos(np.where(pos, -x, x))
+    one = _f32(1.0)
+    out = np.empty_like(x)
+    out[pos] = one / (one + e[pos])
+    neg = ~pos
+    out[neg] = e[neg] / (one + e[neg])
+    return out
+
+
+def grouped_topk(logits: np.ndarray, top_k: int, renormalize: bool, num_expert_group: int,
+                 topk_group: int, correction_bias=None):
+    """select_experts(use_grouped_topk=True) as called at specmoe/layers/FusedMoE.py:174-185:
+    sglang 0.4.5.post3's grouped_topk (correction_bias None) and biased_grouped_topk (not
+    vendored) -> (topk_weights float32 [T,k], topk_ids int32 [T,k]).
+
+    Experts form num_expert_group groups of gs = E / num_expert_group consecutive experts.
+    Scores s: softmax_probs (no bias) or sigmoid_scores (bias); choice c = s (+ bias). Group
+    score: max of c over the group, or with a bias the sum of its two largest c. The
+    topk_group best groups (descending score, ties to the lower group) stay selectable; the
+    top_k best selectable experts by c (descending, ties to the lower expert) are the picks
+    in that order, with weight s, renormalised by the in-order sum. NaN ranks as -inf.
+    sglang's torch.topk(sorted=False) leaves the order of picks and of equal values open;
+    this fixes both as the ungrouped top-k does."""
+    x = np.asarray(logits, dtype=np.float32)
+    T, E = x.shape
+    ng, tg = int(num_expert_group), int(topk_group)
+    if ng <= 0 or E % ng or not 1 <= tg <= ng:
+        raise ValueError("bad expert groups")
+    gs = E // ng
+    if not 1 <= top_k <= tg * gs:
+        raise ValueError("top_k out of range")
+    if correction_bias is None:
+        s = softmax_probs(x)
+        c = s
+    else:
+        if gs < 2:
+            raise ValueError("a biased group score needs two experts per group")
+        s = sigmoid_scores(x)
+        c = s + np.asarray(correction_bias, dtype=np.float32).reshape(1, E)
+    c = np.where(np.isnan(c), _f32(-np.inf), c)
+    cg = c.reshape(T, ng, gs)
+    if correction_bias is None:
+        gscore = cg.max(axis=2)
+    else:
+        top2 = np.sort(cg, axis=2)
+        gscore = top2[:, :, -1] + top2[:, :, -2]
+    gscore = np.where(np.isnan(gscore), _f32(-np.inf), gscore)
+    rows = np.arange(T)[:, None]
+    gorder = np.lexsort((np.broadcast_to(np.arange(ng), (T, ng)), -gscore), axis=-1)
+    allowed = np.zeros((T, ng), dtype=bool)
+    allowed[rows, gorder[:, :tg]] = True
+    allowed = np.repeat(allowed, gs, axis=1)
+    eorder = np.lexsort((np.broadcast_to(np.arange(E), (T, E)), -c, ~allowed), axis=-1)
+    ids = eorder[:, :top_k].astype(np.int32)
+    w = s[rows, ids].astype(np.float32)
+    if renormalize:
+        tot = w[:, 0].copy()
+        for j in range(1, top_k):
+            tot = tot + w[:, j]
+        w = w / tot[:, None]
+    return w.astype(np.float32), ids
+
+
 # ---------------------------------------------------------------------------------------------
 # alignment
 # ---------------------------------------------------------------------------------------------

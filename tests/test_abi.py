@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 43, names
+    assert len(names) == 44, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -122,6 +122,28 @@ def test_forward_and_routing_reject_before_launch():
     assert L.smx_topk_softmax(A, 2, 4, 300, 2, 1, A, A, VP(0)) == _lib.SMX_ERR_UNSUPPORTED
     assert L.smx_moe_align_block_size(A, 10, 0, 16, A, A, A, VP(0)) == _lib.SMX_ERR_INVALID_ARG
     assert L.smx_moe_align_block_size(A, 20000, 8, 16, A, A, A, VP(0)) == _lib.SMX_ERR_UNSUPPORTED
+
+
+def test_grouped_topk_rejects_before_launch():
+    g = L.smx_grouped_topk
+    ok, bad, uns = _lib.SMX_OK, _lib.SMX_ERR_INVALID_ARG, _lib.SMX_ERR_UNSUPPORTED
+    # (T, E, k, groups, selected groups, bias) -> status
+    cases = [((0, 160, 6, 8, 3, None), ok),
+             ((4, 12, 1, 5, 1, None), bad),      # E not a multiple of the groups
+             ((4, 12, 1, 4, 5, None), bad),      # more selected groups than groups
+             ((4, 12, 1, 4, 0, None), bad),
+             ((4, 12, 4, 4, 1, None), bad),      # k above the selectable experts (3)
+             ((4, 12, 1, 12, 3, A), bad),        # a biased group score needs 2 experts a group
+             ((4, 12, 0, 4, 1, None), bad),
+             ((-1, 12, 1, 4, 1, None), bad),
+             ((4, 300, 2, 1, 1, None), uns),     # E > 256
+             ((4, 256, 1, 128, 1, None), uns),   # more groups than lanes
+             ((4, 256, 17, 1, 1, None), uns)]    # k > 16
+    for (T, E, k, ng, tg, bias), want in cases:
+        assert g(A, 2, T, E, k, 1, ng, tg, bias, A, A, VP(0)) == want, (T, E, k, ng, tg)
+    assert g(A, 7, 4, 160, 6, 1, 8, 3, None, A, A, VP(0)) == bad      # logits dtype
+    assert g(None, 2, 4, 160, 6, 1, 8, 3, None, A, A, VP(0)) == bad   # no logits
+    assert g(A, 2, 4, 160, 6, 1, 8, 3, None, None, A, VP(0)) == bad   # no weights out
 
 
 def test_noalloc_forward_rejects_before_touching_the_device():

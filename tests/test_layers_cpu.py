@@ -52,18 +52,23 @@ def test_expert_params_mapping():
     assert len(m) == 6
 
 
-def test_unsupported_options_raise():
-    with pytest.raises(NotImplementedError):
-        check_routing_options(True, 2, 4, None, None, None)
-    check_routing_options(True, 1, 1, None, None, None)  # one group == plain top-k
+def test_routing_options():
+    from ae_amd.layers.topk import needs_grouped_topk
+    with pytest.raises(ValueError):  # sglang asserts both group sizes
+        check_routing_options(True, None, 4, None, None, None)
+    check_routing_options(True, 2, 4, None, None, None)
+    check_routing_options(True, 1, 1, None, None, None)
     check_routing_options(False, None, None, lambda **kw: kw, None, None)  # custom routing
-    with pytest.raises(NotImplementedError):
-        check_routing_options(True, 1, 1, lambda **kw: kw, None, None)
-    with pytest.raises(NotImplementedError):
-        check_routing_options(False, None, None, None, torch.zeros(4), None)
+    check_routing_options(True, 2, 4, lambda **kw: kw, torch.zeros(4), None)
     check_routing_options(False, None, None, None, None, 2.5)  # accepted (no effect on top-k)
     with pytest.raises(ValueError):
         check_routing_options(False, None, None, None, None, float("nan"))
+    # one group, or all groups selectable, without a bias: the plain top-k of the one-call path
+    assert not needs_grouped_topk(False, 2, 4, torch.zeros(4))  # the bias needs the grouped branch
+    assert not needs_grouped_topk(True, 1, 1, None)
+    assert not needs_grouped_topk(True, 4, 4, None)
+    assert needs_grouped_topk(True, 3, 8, None)
+    assert needs_grouped_topk(True, 1, 1, torch.zeros(4))
     with pytest.raises(NotImplementedError):
         FusedMoE(4, 2, 8, 8, params_dtype=torch.float32, tp_size=1, quant_config=object())
 

@@ -169,6 +169,114 @@ def test_topk_bf16_logits_select_like_logits():
     np.testing.assert_array_equal(ids, _select_by_lexsort(x, 2))
 
 
+# ------------------------------------------------------------------------------- grouped top-k
+def test_sigmoid_scores_against_float64():
+    rng = np.random.default_rng(11)
+    x = np.concatenate([(rng.random(400_000, dtype=np.float32) - 0.5) * np.float32(160.0),
+                        (rng.random(100_000, dtype=np.float32) - 0.5) * np.float32(1e-3),
+                        np.array([0.0, -0.0, 1e-30, -1e-30, 80.0, -80.0, 17.0, -17.0], np.float32)])
+    got = ref.sigmoid_scores(x)
+    exact = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    ulp = np.spacing(exact.astype(np.float32)).astype(np.float64)
+    err = np.abs(got.astype(np.float64) - exact) / ulp
+    assert err.max() <= 3.0, err.max()
+    assert ref.sigmoid_scores(np.float32([0.0]))[0] == np.float32(0.5)
+    edge = ref.sigmoid_scores(np.array([np.inf, -np.inf, -1000.0, 1000.0], np.float32))
+    np.testing.assert_array_equal(edge, [1.0, 0.0, 0.0, 1.0])
+
+
+def _grouped_by_python_sort(s, c, k, ng, tg, biased):
+    """The grouped selection re-derived with Python's sorted() on tuple keys, token by token."""
+    T, E = c.shape
+    gs = E // ng
+    ids = np.empty((T, k), np.int32)
+    for t in range(T):
+        row = [float(v) for v in c[t]]
+        score = []
+        for g in range(ng):
+            members = row[g * gs:(g + 1) * gs]
+            if biased:
+                a, b = sorted(members)[-2:]
+                score.append(float(np.float32(a) + np.float32(b)))
+            else:
+                score.append(max(members))
+        groups = set(sorted(range(ng), key=lambda g: (-score[g], g))[:tg])
+        cand = [e for e in range(E) if e // gs in groups]
+        ids[t] = sorted(cand, key=lambda e: (-row[e], e))[:k]
+    return ids
+
+
+@pytest.mark.parametrize("E,ng,tg,k,biased", [(160, 8, 3, 6, False), (256, 8, 4, 8, True),
+                                              (8, 4, 2, 3, False), (8, 4, 2, 3, True),
+                                              (64, 8, 2, 6, False), (60, 6, 1, 4, True),
+                                              (96, 32, 5, 7, False), (128, 64, 16, 16, True)])
+def test_grouped_topk_against_python_sort(E, ng, tg, k, biased):
+    rng = np.random.default_rng(E + 7 * ng + k + int(biased))
+    x = (rng.standard_normal((40, E)) * 1.5).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.3).astype(np.float32) if biased else None
+    w, ids = ref.grouped_topk(x, k, False, ng, tg, bias)
+    s = ref.sigmoid_scores(x) if biased else ref.softmax_probs(x)
+    c = s + bias[None, :] if biased else s
+    np.testing.assert_array_equal(ids, _grouped_by_python_sort(s, c, k, ng, tg, biased))
+    np.testing.assert_array_equal(w, np.take_along_axis(s, ids.astype(np.int64), 1))
+    # renormalised: the same picks, weights / their in-order sum
+    wr, idr = ref.grouped_topk(x, k, True, ng, tg, bias)
+    np.testing.assert_array_equal(idr, ids)
+    np.testing.assert_allclose(wr.sum(axis=1, dtype=np.float64), 1.0, rtol=4e-7 * k)
+
+
+@pytest.mark.parametrize("E,k", [(8, 2), (64, 6), (160, 6), (256, 8)])
+def test_grouped_topk_reduces_to_plain_topk(E, k):
+    # one group, or every group selectable: the plain top-k, bit for bit
+    rng = np.random.default_rng(E + k)
+    x = (rng.standard_normal((60, E)) * 2).astype(np.float32)
+    for renorm in (False, True):
+        w0, i0 = ref.topk_softmax(x, k, renorm)
+        for ng, tg in ((1, 1), (8, 8), (4, 4)):
+            if E % ng:
+                continue
+            w, ids = ref.grouped_topk(x, k, renorm, ng, tg)
+            np.testing.assert_array_equal(ids, i0)
+            np.testing.assert_array_equal(w.view(np.uint32), w0.view(np.uint32))
+
+
+def test_grouped_topk_known_answers():
+    # softmax, groups of 2: group 3's best (1.45) loses to group 2's (1.5), so expert 6 (the
+    # plain top-3's third pick) is dropped for expert 5 of a selected group
+    x = np.array([[0.0, 0.0, 2.0, -3.0, 1.5, 1.4, 1.45, 1.0]], np.float32)
+    w, ids = ref.grouped_topk(x, 3, False, 4, 2)
+    np.testing.assert_array_equal(ids[0], [2, 4, 5])
+    np.testing.assert_array_equal(ref.topk_softmax(x, 3, False)[1][0], [2, 4, 6])
+    p = np.exp(x[0].astype(np.float64))
+    p /= p.sum()
+    np.testing.assert_allclose(w[0], p[[2, 4, 5]], rtol=3e-7)
+    # sigmoid + top-2 group sums: group 0 holds the single best expert (sigmoid(3)) but its
+    # sum (0.9526 + 0.0067) loses to groups 1 (2 x 0.7311) and 2 (2 x 0.7109); equal picks
+    # renormalise to exactly 1/2
+    x = np.array([[3.0, -5.0, 1.0, 1.0, 0.9, 0.9, -1.0, -1.0]], np.float32)
+    w, ids = ref.grouped_topk(x, 2, True, 4, 2, np.zeros(8, np.float32))
+    np.testing.assert_array_equal(ids[0], [2, 3])
+    np.testing.assert_array_equal(w[0], [0.5, 0.5])
+    # the bias steers the choice, the weight stays the unbiased score
+    x = np.array([[2.0, 0.0, 1.0, 1.0]], np.float32)
+    bias = np.array([0.0, 0.0, 0.5, 0.5], np.float32)
+    w, ids = ref.grouped_topk(x, 1, False, 2, 1, bias)
+    assert ids[0, 0] == 2
+    np.testing.assert_allclose(w[0, 0], 1.0 / (1.0 + np.exp(-1.0)), rtol=2e-7)
+    w, ids = ref.grouped_topk(x, 1, True, 2, 1, bias)
+    assert ids[0, 0] == 2 and w[0, 0] == np.float32(1.0)
+    # equal logits: the lowest groups, then the lowest experts
+    w, ids = ref.grouped_topk(np.zeros((1, 16), np.float32), 3, False, 4, 2)
+    np.testing.assert_array_equal(ids[0], [0, 1, 2])
+
+
+def test_grouped_topk_rejects_bad_groups():
+    x = np.zeros((2, 12), np.float32)
+    for ng, tg, k in ((5, 1, 1), (4, 5, 1), (4, 0, 1), (4, 1, 4), (12, 3, 1)):
+        with pytest.raises(ValueError):
+            ref.grouped_topk(x, k, False, ng, tg, np.zeros(12, np.float32) if ng == 12 else None)
+
+
 # --------------------------------------------------------------------------------------- align
 def test_align_docstring_example():
     """specmoe/layers/fused_moe_kernel.py:41-54 (read with expert 0 empty, E=5)."""
