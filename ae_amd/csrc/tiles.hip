@@ -145,19 +145,26 @@ __device__ __forceinline__ void dma_t(const TRows& t, u32x4* stage, int step) {
 // moving LDS accesses across it.
 __device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// 64 MFMAs of one step: acc[i][bt] += A_i . B_bt over the step's two k-groups.
+// 64 MFMAs of one step: acc[i][bt] += A_i . B_bt over the step's two k-groups. The 16 B
+// fragments (k-group u, token tile bt) are read from the stage two ahead of their use, in a
+// ring of three, and a scheduling barrier closes each group (one read, then the four MFMAs of
+// the fragment read two groups before), so that the compiler keeps that distance: a
+// fragment's LDS latency then overlaps eight MFMAs of this wave.
 template <int DT>
 __device__ __forceinline__ void mma_step(const WRegs& a, const u32x4* stage, int rb0, int rb1,
                                          f32x4 (&acc)[kTATiles][kTBTiles]) {
+  constexpr int kFrags = 2 * kTBTiles;
+  auto slot = [&](int n) { return (n % kTBTiles) * kTokTile * kTSlots + (n < kTBTiles ? rb0 : rb1); };
+  u32x4 b[3];
+  b[0] = stage[slot(0)];
+  b[1] = stage[slot(1)];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int rb = u == 0 ? rb0 : rb1;
+  for (int n = 0; n < kFrags; ++n) {
+    if (n + 2 < kFrags) b[(n + 2) % 3] = stage[slot(n + 2)];
+    const int u = n / kTBTiles, bt = n % kTBTiles;
 #pragma unroll
-    for (int bt = 0; bt < kTBTiles; ++bt) {
-      const u32x4 bf = stage[bt * kTokTile * kTSlots + rb];
-#pragma unroll
-      for (int i = 0; i < kTATiles; ++i) acc[i][bt] = Elem<DT>::mfma(a.v[i][u], bf, acc[i][bt]);
-    }
+    for (int i = 0; i < kTATiles; ++i) acc[i][bt] = Elem<DT>::mfma(a.v[i][u], b[n % 3], acc[i][bt]);
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
