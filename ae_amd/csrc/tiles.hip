@@ -149,11 +149,17 @@ __device__ __forceinline__ void bare_barrier() { asm volatile("s_barrier" ::: "m
 // fragments (k-group u, token tile bt) are read from the stage two ahead of their use, in a
 // ring of three, and a scheduling barrier closes each group (one read, then the four MFMAs of
 // the fragment read two groups before), so that the compiler keeps that distance: a
-// fragment's LDS latency then overlaps eight MFMAs of this wave.
-template <int DT>
+// fragment's LDS latency then overlaps eight MFMAs of this wave. With kStore, the next step's
+// weights (`wnext`, loaded two steps back) go to the wave's tile one write every second
+// group, spread over the step rather than gathered before the barrier; the tile's A fragments
+// of this step were read before (a wave's LDS operations run in issue order).
+template <int DT, bool kStore = false>
 __device__ __forceinline__ void mma_step(const WRegs& a, const u32x4* stage, int rb0, int rb1,
-                                         f32x4 (&acc)[kTATiles][kTBTiles]) {
+                                         f32x4 (&acc)[kTATiles][kTBTiles],
+                                         const WRegs* wnext = nullptr, u32x4* tile = nullptr,
+                                         const int* wa = nullptr) {
   constexpr int kFrags = 2 * kTBTiles;
+  static_assert(kFrags / 2 == kTATiles * 2, "one weight write every second group");
   auto slot = [&](int n) { return (n % kTBTiles) * kTokTile * kTSlots + (n < kTBTiles ? rb0 : rb1); };
   u32x4 b[3];
   b[0] = stage[slot(0)];
@@ -161,6 +167,12 @@ __device__ __forceinline__ void mma_step(const WRegs& a, const u32x4* stage, int
 #pragma unroll
   for (int n = 0; n < kFrags; ++n) {
     if (n + 2 < kFrags) b[(n + 2) % 3] = stage[slot(n + 2)];
+    if constexpr (kStore) {
+      if (n % 2 == 1) {
+        const int q = n / 2, i = q / 2, h = q % 2;
+        tile[wa[h] + i * kRowTile * kTSlots] = wnext->v[i][h];
+      }
+    }
     const int u = n / kTBTiles, bt = n % kTBTiles;
 #pragma unroll
     for (int i = 0; i < kTATiles; ++i) acc[i][bt] = Elem<DT>::mfma(a.v[i][u], b[n % 3], acc[i][bt]);
@@ -187,8 +199,8 @@ constexpr int kVmAfterDma = 2 * kTATiles * 2 + kTBLoads;  // 8 + 4 + 8
 
 // One step of the 16-bit walk, for step c: its token rows are in stage `cur` and its weights in
 // the wave's tile. Step c+2's token rows go out by DMA into `dma_dst` (the stage step c-1 read)
-// and then its weights into `issue_to`; after the MFMAs, step c+1's weights (`next`, loaded two
-// steps back) are written to the tile, the wave waits until step c+1's DMA has landed -- loads
+// and then its weights into `issue_to`; during the MFMAs, step c+1's weights (`next`, loaded two
+// steps back) are written to the tile; then the wave waits until step c+1's DMA has landed -- loads
 // issued after it: step c+1's weights (8), step c+2's DMA (4) and weights (8) -- and the
 // workgroup meets at the barrier.
 template <int CP, int DT>
@@ -200,9 +212,8 @@ __device__ __forceinline__ void dma_step(WRegs& issue_to, const WRegs& next, WRe
   load_w<CP>(issue_to, wk.w, issue);
   __builtin_amdgcn_sched_barrier(0);
   read_frags(frag, wtile, wk.rb0, wk.rb1);
-  mma_step<DT>(frag, cur, wk.rb0, wk.rb1, acc);
+  mma_step<DT, true>(frag, cur, wk.rb0, wk.rb1, acc, &next, wtile, wk.wa);
   __builtin_amdgcn_sched_barrier(0);
-  store_w(next, wtile, wk.wa);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(kVmAfterDma));
   bare_barrier();
 }
