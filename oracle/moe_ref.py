@@ -8,7 +8,9 @@ A plain numpy restatement of the reference's arithmetic:
 
   routing   select_experts as called at specmoe/layers/FusedMoE.py:174-185 (sglang 0.4.5.post3
             -> sgl_kernel.topk_softmax, not vendored): fp32 softmax, top-k with ties to the
-            lower expert index, optional w / sum(w).
+            lower expert index, optional w / sum(w). Grouped (use_grouped_topk): sglang's
+            grouped_topk / biased_grouped_topk -- softmax or sigmoid + correction bias scores,
+            only the topk_group best of num_expert_group groups selectable.
   align     moe_align_block_size, specmoe/layers/fused_moe_kernel.py:16-85 (sgl-kernel 0.1.2
             underneath, not vendored); pinned by the docstring example at :41-54.
   experts   stack_fused_moe, specmoe/layers/fused_moe_kernel.py:253-349: per routed
@@ -36,7 +38,9 @@ tree, correctly rounded fp32 divide), so GPU routing weights match this oracle b
 GEMM accumulation order is not restated; outputs agree to a stated tolerance.
 
 Parity pinning (tests/test_oracle.py): the align docstring example; brute-force sorting;
-top-k against np.argsort/lexsort selection and hand-built tie cases; exp_nonpos against float64
+top-k against np.argsort/lexsort selection and hand-built tie cases; the grouped top-k against
+a Python sorted() re-derivation, the plain top-k where grouping removes nothing, and
+hand-worked cases (sigmoid_scores within 3 ulp of float64); exp_nonpos against float64
 exp (<= 2 ulp); the expert math against a float64 textbook SwiGLU MoE built from separate
 gate/up/down matrices through the page packing; the shared-expert block against a float64
 textbook block and its reductions (zero shared page -> routed result, zero routed pages ->
