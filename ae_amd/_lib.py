@@ -39,6 +39,10 @@ SIGNATURES = [
     ("smx_stack_fused_moe", ctypes.c_int,
      [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
       _c_void_p, _c_void_p, _i64, _c_void_p, _sz, _c_void_p]),
+    ("smx_stack_fused_moe_shared", ctypes.c_int,
+     [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i64, _i64, _c_void_p, _i64,
+      _c_void_p, _c_void_p, _i64, _c_void_p, _i64, _c_void_p, ctypes.c_float, _c_void_p, _sz,
+      _c_void_p]),
     ("smx_fused_moe_forward", ctypes.c_int,
      [_c_void_p, _c_void_p, _i32, _i64, _i64, _c_void_p, _i32, _i64, _i64, _i32,
       _c_void_p, _i64, _i64, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _sz, _c_void_p]),

@@ -731,6 +731,62 @@ int check_pool(const void* hidden, const void* out, const void* pool, int64_t nu
 
 }  // namespace
 
+namespace {
+
+// Expert computation on the caller's routing (smx_stack_fused_moe and its block form).
+int stack_forward(const void* hidden, void* out, int dtype, int64_t T, int64_t H, const void* pool,
+                  int64_t num_slots, int64_t page_elems, const int64_t* expert_to_slot, int64_t E,
+                  const float* topk_weights, const int32_t* topk_ids, int64_t top_k, int64_t Is,
+                  const BlockTerms& bt, void* workspace, size_t workspace_bytes, void* stream) {
+  if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype)) return SMX_ERR_INVALID_ARG;
+  if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
+  int64_t I = 0;
+  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, dtype, &I);
+  if (rc != SMX_OK) return rc;
+  rc = check_shape(T, H, I, E, top_k, dtype);
+  if (rc != SMX_OK) return rc;
+  rc = check_shared(T, H, Is, dtype);
+  if (rc != SMX_OK) return rc;
+  if (!topk_weights || !topk_ids || !workspace) return SMX_ERR_INVALID_ARG;
+  const int64_t tc = chunk_tokens(T, H, I, top_k, Is, dtype);
+  if (T > tc) {
+    if (workspace_bytes < workspace_for(T, H, I, E, top_k, dtype, Is, false)) return SMX_ERR_WORKSPACE;
+    const int64_t rb = H * dtype_bytes(dtype);
+    for (int64_t t0 = 0; t0 < T; t0 += tc) {
+      BlockTerms bc = bt;
+      if (bc.sgate) bc.sgate = static_cast<const char*>(bc.sgate) + t0 * dtype_bytes(bc.sgate_dtype);
+      rc = stack_forward(static_cast<const char*>(hidden) + t0 * rb, static_cast<char*>(out) + t0 * rb, dtype,
+                         std::min(tc, T - t0), H, pool, num_slots, page_elems, expert_to_slot, E,
+                         topk_weights + t0 * top_k, topk_ids + t0 * top_k, top_k, Is, bc, workspace,
+                         workspace_bytes, stream);
+      if (rc != SMX_OK) return rc;
+    }
+    return SMX_OK;
+  }
+  const Plan p = make_plan(T, H, I, E, top_k, dtype, Is);
+  if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  mark(0, s);
+  bool rmulti = false;
+  const int rg = in_launch_route_g(p, T, E, top_k, false, true, &rmulti);
+  InRoute rt{};
+  if (rg > 0) {
+    rt.ids_in = topk_ids;
+    rt.num_slots = num_slots;
+    rt.E = static_cast<int>(E);
+  } else {
+    hipError_t err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k),
+                                  0, nullptr, nullptr, topk_ids, expert_to_slot, num_slots, carve(p, workspace), s);
+    if (err != hipSuccess) return static_cast<int>(err);
+  }
+  mark(1, s);
+  return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
+                     expert_to_slot, topk_weights, topk_ids, workspace, s, bt, rg, rt, rmulti);
+}
+
+}  // namespace
+
 extern "C" {
 
 int smx_version(void) { return kVersion; }
@@ -842,47 +898,30 @@ int smx_stack_fused_moe(const void* hidden, void* out, int dtype, int64_t T, int
                         const int64_t* expert_to_slot, int64_t E,
                         const float* topk_weights, const int32_t* topk_ids, int64_t top_k,
                         void* workspace, size_t workspace_bytes, void* stream) {
-  if (T < 0 || H <= 0 || E <= 0 || top_k <= 0 || top_k > E || !valid_dtype(dtype)) return SMX_ERR_INVALID_ARG;
-  if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
-  int64_t I = 0;
-  int rc = check_pool(hidden, out, pool, num_slots, page_elems, expert_to_slot, H, dtype, &I);
-  if (rc != SMX_OK) return rc;
-  rc = check_shape(T, H, I, E, top_k, dtype);
-  if (rc != SMX_OK) return rc;
-  if (!topk_weights || !topk_ids || !workspace) return SMX_ERR_INVALID_ARG;
-  const int64_t tc = chunk_tokens(T, H, I, top_k, 0, dtype);
-  if (T > tc) {
-    if (workspace_bytes < workspace_for(T, H, I, E, top_k, dtype, 0, false)) return SMX_ERR_WORKSPACE;
-    const int64_t rb = H * dtype_bytes(dtype);
-    for (int64_t t0 = 0; t0 < T; t0 += tc) {
-      rc = smx_stack_fused_moe(static_cast<const char*>(hidden) + t0 * rb, static_cast<char*>(out) + t0 * rb,
-                               dtype, std::min(tc, T - t0), H, pool, num_slots, page_elems, expert_to_slot,
-                               E, topk_weights + t0 * top_k, topk_ids + t0 * top_k, top_k, workspace,
-                               workspace_bytes, stream);
-      if (rc != SMX_OK) return rc;
-    }
-    return SMX_OK;
-  }
-  const Plan p = make_plan(T, H, I, E, top_k, dtype);
-  if (workspace_bytes < p.total) return SMX_ERR_WORKSPACE;
-  if (!aligned16(workspace)) return SMX_ERR_MISALIGNED;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  mark(0, s);
-  bool rmulti = false;
-  const int rg = in_launch_route_g(p, T, E, top_k, false, true, &rmulti);
-  InRoute rt{};
-  if (rg > 0) {
-    rt.ids_in = topk_ids;
-    rt.num_slots = num_slots;
-    rt.E = static_cast<int>(E);
-  } else {
-    hipError_t err = launch_route(nullptr, kF32, static_cast<int>(T), static_cast<int>(E), static_cast<int>(top_k),
-                                  0, nullptr, nullptr, topk_ids, expert_to_slot, num_slots, carve(p, workspace), s);
-    if (err != hipSuccess) return static_cast<int>(err);
-  }
-  mark(1, s);
-  return run_experts(p, dtype, hidden, out, T, H, I, E, top_k, pool, num_slots, page_elems,
-                     expert_to_slot, topk_weights, topk_ids, workspace, s, BlockTerms{}, rg, rt, rmulti);
+  return stack_forward(hidden, out, dtype, T, H, pool, num_slots, page_elems, expert_to_slot, E,
+                       topk_weights, topk_ids, top_k, 0, BlockTerms{}, workspace, workspace_bytes,
+                       stream);
+}
+
+int smx_stack_fused_moe_shared(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                               const void* pool, int64_t num_slots, int64_t page_elems,
+                               const int64_t* expert_to_slot, int64_t E,
+                               const float* topk_weights, const int32_t* topk_ids, int64_t top_k,
+                               const void* shared_page, int64_t shared_I,
+                               const void* shared_gate_logits, float routed_scaling_factor,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (shared_I < 0 || (shared_I == 0) != (shared_page == nullptr) ||
+      (shared_I == 0 && shared_gate_logits != nullptr) || !std::isfinite(routed_scaling_factor))
+    return SMX_ERR_INVALID_ARG;
+  if (T > 0 && shared_page && !aligned16(shared_page)) return SMX_ERR_MISALIGNED;
+  BlockTerms bt;
+  bt.block = true;
+  bt.scale = routed_scaling_factor;
+  bt.shared_page = shared_page;
+  bt.sgate = shared_gate_logits;
+  bt.sgate_dtype = dtype;
+  return stack_forward(hidden, out, dtype, T, H, pool, num_slots, page_elems, expert_to_slot, E,
+                       topk_weights, topk_ids, top_k, shared_I, bt, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -5,7 +5,8 @@ from .fused_moe_kernel import (fp32_gemm_outputs_fp16, fused_down_max_tokens, fu
                                moe_align_block_size, routing_in_gateup, set_fp32_gemm_outputs_fp16,
                                set_fused_down_max_tokens, set_gateup_item_walk, set_gateup_waves,
                                set_routing_in_gateup,
-                               set_tiled_min_tokens, stack_fused_moe, tiled_min_tokens)
+                               set_tiled_min_tokens, stack_fused_moe, stack_fused_moe_shared,
+                               tiled_min_tokens)
 from .layernorm import RMSNorm, add_rmsnorm_gate
 from .mixtral_moe import MixtralMoE
 from .moe_layer import PostAttentionMoE, moe_layer_forward
@@ -14,7 +15,8 @@ from .topk import fused_topk, grouped_topk, select_experts
 
 __all__ = [
     "FusedMoE", "UnquantizedFusedMoEMethod", "set_weight_attrs", "fused_moe_forward",
-    "fused_moe_shared_forward", "moe_align_block_size", "stack_fused_moe", "MixtralMoE",
+    "fused_moe_shared_forward", "moe_align_block_size", "stack_fused_moe",
+    "stack_fused_moe_shared", "MixtralMoE",
     "SharedExpertMoE", "Qwen2MoeSparseMoeBlock", "DeepseekV2MoE", "fused_topk", "grouped_topk",
     "select_experts",
     "RMSNorm", "add_rmsnorm_gate", "PostAttentionMoE", "moe_layer_forward",

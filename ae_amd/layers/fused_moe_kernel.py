@@ -290,6 +290,26 @@ def fused_moe_forward(
     return out
 
 
+def _shared_terms(hidden_states: torch.Tensor, shared_w: Optional[torch.Tensor],
+                  shared_gate_logits: Optional[torch.Tensor], T: int, H: int,
+                  gate_dtype: torch.dtype):
+    """-> (shared_I, contiguous gate logits or None), checking the shared expert's operands."""
+    Is = 0
+    if shared_w is not None:
+        assert shared_w.is_contiguous(), "shared expert weights must be contiguous"
+        assert shared_w.dtype == hidden_states.dtype, "shared expert and hidden states dtypes differ"
+        assert shared_w.numel() % (3 * H) == 0, "shared expert page is not 3*Is*H elements"
+        Is = shared_w.numel() // (3 * H)
+    sgate = None
+    if shared_gate_logits is not None:
+        assert shared_w is not None, "a shared-expert gate needs a shared expert"
+        assert shared_gate_logits.numel() == T, "one shared-expert gate logit per token"
+        assert shared_gate_logits.dtype == gate_dtype, \
+            f"shared-expert gate logits must be {gate_dtype}"
+        sgate = shared_gate_logits.contiguous()
+    return Is, sgate
+
+
 def fused_moe_shared_forward(
     hidden_states: torch.Tensor,
     router_logits: torch.Tensor,
@@ -324,19 +344,7 @@ def fused_moe_shared_forward(
     require_gpu(hidden_states, router_logits, w1, indicies, shared_w, shared_gate_logits)
     H, I = _pool_geometry(hidden_states, w1)
     T, E = router_logits.shape
-    Is = 0
-    if shared_w is not None:
-        assert shared_w.is_contiguous(), "shared expert weights must be contiguous"
-        assert shared_w.dtype == hidden_states.dtype, "shared expert and hidden states dtypes differ"
-        assert shared_w.numel() % (3 * H) == 0, "shared expert page is not 3*Is*H elements"
-        Is = shared_w.numel() // (3 * H)
-    sgate = None
-    if shared_gate_logits is not None:
-        assert shared_w is not None, "a shared-expert gate needs a shared expert"
-        assert shared_gate_logits.numel() == T, "one shared-expert gate logit per token"
-        assert shared_gate_logits.dtype == router_logits.dtype, \
-            "shared-expert gate logits and router logits dtypes differ"
-        sgate = shared_gate_logits.contiguous()
+    Is, sgate = _shared_terms(hidden_states, shared_w, shared_gate_logits, T, H, router_logits.dtype)
     logits = router_logits.contiguous()
     slots = _as_index(indicies, torch.int64)
     dt = dtype_code(hidden_states.dtype)
@@ -355,4 +363,49 @@ def fused_moe_shared_forward(
               ptr(w), ptr(ids), ptr(ws), ws.numel(), stream_of(hidden_states))
     if return_routing:
         return out, w, ids
+    return out
+
+
+def stack_fused_moe_shared(
+    hidden_states: torch.Tensor,
+    w1: torch.Tensor,
+    indicies: torch.Tensor,
+    topk_weights: torch.Tensor,
+    topk_ids: torch.Tensor,
+    shared_w: Optional[torch.Tensor],
+    shared_gate_logits: Optional[torch.Tensor] = None,
+    routed_scaling_factor: float = 1.0,
+    inplace: bool = True,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """:func:`fused_moe_shared_forward` on the caller's routing (``topk_weights`` /
+    ``topk_ids`` as :func:`stack_fused_moe` takes them), for blocks whose routing is not the
+    plain top-k softmax (DeepSeek-V2's group-limited and DeepSeek-V3's biased top-k,
+    :func:`ae_amd.layers.grouped_topk`). ``shared_gate_logits`` are in the activations' dtype.
+    One library call (``smx_stack_fused_moe_shared``)."""
+    assert hidden_states.is_contiguous(), "Hidden_states must be contiguous"
+    assert w1.is_contiguous(), "Expert weights1 must be contiguous"
+    assert hidden_states.dtype in [torch.float32, torch.float16, torch.bfloat16]
+    assert w1.dtype == hidden_states.dtype, "expert pool and hidden states dtypes differ"
+    assert topk_weights.shape == topk_ids.shape, "topk shape mismatch"
+    assert topk_ids.shape[0] == hidden_states.shape[0], "Number of tokens mismatch"
+    require_gpu(hidden_states, w1, indicies, topk_weights, topk_ids, shared_w, shared_gate_logits)
+    H, I = _pool_geometry(hidden_states, w1)
+    T, top_k = topk_ids.shape
+    E = indicies.numel()
+    Is, sgate = _shared_terms(hidden_states, shared_w, shared_gate_logits, T, H, hidden_states.dtype)
+    slots = _as_index(indicies, torch.int64)
+    ids = _as_index(topk_ids, torch.int32)
+    w = _as_index(topk_weights, torch.float32)
+    dt = dtype_code(hidden_states.dtype)
+    nbytes = _lib.lib().smx_moe_shared_workspace_size(T, H, I, E, top_k, Is, dt)
+    if nbytes == 0 and T > 0:
+        raise ValueError(f"unsupported MoE shape T={T} H={H} I={I} E={E} top_k={top_k} "
+                         f"shared I={Is}")
+    out, ws = _caller_buffers(hidden_states, inplace, out, workspace, nbytes)
+    _lib.call("smx_stack_fused_moe_shared", ptr(hidden_states), ptr(out), dt, T, H, ptr(w1),
+              w1.shape[0], w1.shape[1], ptr(slots), E, ptr(w), ptr(ids), top_k, ptr(shared_w), Is,
+              ptr(sgate), float(routed_scaling_factor), ptr(ws), ws.numel(),
+              stream_of(hidden_states))
     return out

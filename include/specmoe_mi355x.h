@@ -209,6 +209,23 @@ int smx_fused_moe_shared_forward(const void* hidden, void* out, int dtype, int64
                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * smx_fused_moe_shared_forward on routing the caller has done (topk_weights / topk_ids as
+ * smx_stack_fused_moe takes them), for blocks whose routing is not the plain top-k softmax:
+ * DeepSeek-V2's group-limited top-k and DeepSeek-V3's sigmoid top-k with a correction bias
+ * (smx_grouped_topk). Same block arithmetic, workspace (smx_moe_shared_workspace_size) and
+ * limits; shared_gate_logits [T] is of `dtype`. No counterpart in the reference (it serves no
+ * model with shared experts); the routed part is smx_stack_fused_moe, which replaces
+ * stack_fused_moe (specmoe/layers/fused_moe_kernel.py:253-349).
+ */
+int smx_stack_fused_moe_shared(const void* hidden, void* out, int dtype, int64_t T, int64_t H,
+                               const void* pool, int64_t num_slots, int64_t page_elems,
+                               const int64_t* expert_to_slot, int64_t E,
+                               const float* topk_weights, const int32_t* topk_ids, int64_t top_k,
+                               const void* shared_page, int64_t shared_I,
+                               const void* shared_gate_logits, float routed_scaling_factor,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Post-attention residual add + RMSNorm + router gate in one kernel (one workgroup per token):
  *   s = hidden + residual (fp32; residual == NULL: s = hidden)
  *   residual      = round(s)                                      (in place, when given)

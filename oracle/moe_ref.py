@@ -391,6 +391,18 @@ def fused_moe_shared_forward(x, router_logits, pool, slots, top_k: int, renormal
     y = round(round(routed * scale) + s * shared), s = round(sigmoid(gate logit)) or 1,
     the product s * shared rounded; routed = fused_moe_forward's result."""
     y, w, ids = fused_moe_forward(x, router_logits, pool, slots, top_k, renormalize, dtype)
+    y = _block_terms(x, y, dtype, shared_page, shared_gate_logits, routed_scaling_factor)
+    return y, w, ids
+
+
+def stack_fused_moe_shared(x, pool, slots, topk_weights, topk_ids, dtype: str, shared_page=None,
+                           shared_gate_logits=None, routed_scaling_factor: float = 1.0):
+    """The same block on given routing (weights / ids as stack_fused_moe takes them)."""
+    y = stack_fused_moe(x, pool, slots, topk_weights, topk_ids, dtype)
+    return _block_terms(x, y, dtype, shared_page, shared_gate_logits, routed_scaling_factor)
+
+
+def _block_terms(x, y, dtype: str, shared_page, shared_gate_logits, routed_scaling_factor: float):
     if routed_scaling_factor != 1.0:
         y = round_to(y * _f32(routed_scaling_factor), dtype)
     if shared_page is not None:
@@ -400,7 +412,7 @@ def fused_moe_shared_forward(x, router_logits, pool, slots, top_k: int, renormal
             s = round_to(sigmoid(sg), dtype)
             d = round_to(s[:, None] * d, dtype)
         y = round_to(y + d, dtype)
-    return y, w, ids
+    return y
 
 
 # ---------------------------------------------------------------------------------------------

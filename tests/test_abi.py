@@ -28,7 +28,7 @@ def test_library_built_in_tree():
 
 def test_exports_every_declared_symbol():
     names = _declared()
-    assert len(names) == 44, names
+    assert len(names) == 45, names
     assert sorted(names) == sorted(n for n, _, _ in _lib.SIGNATURES)
     for n in names:
         assert hasattr(L, n), n
@@ -106,6 +106,26 @@ def test_stack_rejects_before_launch():
     assert _stack(T=0) == _lib.SMX_OK                              # empty: nothing launched
     assert _stack(T=0, hidden=VP(0), out=VP(0), ws=VP(0)) == _lib.SMX_OK  # null data is fine
     assert _stack(T=-1) == _lib.SMX_ERR_INVALID_ARG
+
+
+def test_stack_shared_rejects_before_launch():
+    f = L.smx_stack_fused_moe_shared
+    F = ctypes.c_float
+
+    def call(**kw):
+        a = dict(T=4, Is=256, page=A, sgate=VP(0), scale=F(1.0), wsb=1 << 30, k=2)
+        a.update(kw)
+        return f(A, A, 2, a["T"], 256, A, 4, 3 * 256 * 256, A, 4, A, A, a["k"], a["page"], a["Is"],
+                 a["sgate"], a["scale"], A, a["wsb"], VP(0))
+    assert call(T=0) == _lib.SMX_OK
+    assert call(Is=-1) == _lib.SMX_ERR_INVALID_ARG
+    assert call(Is=0) == _lib.SMX_ERR_INVALID_ARG                  # a page without a size
+    assert call(Is=0, page=VP(0), sgate=A) == _lib.SMX_ERR_INVALID_ARG  # a gate without an expert
+    assert call(scale=F(float("nan"))) == _lib.SMX_ERR_INVALID_ARG
+    assert call(page=VP(0x10008)) == _lib.SMX_ERR_MISALIGNED
+    assert call(k=5) == _lib.SMX_ERR_INVALID_ARG                   # top_k > E
+    assert call(Is=100) == _lib.SMX_ERR_UNSUPPORTED                # shared I not a multiple of 128
+    assert call(wsb=16) == _lib.SMX_ERR_WORKSPACE
 
 
 def test_forward_and_routing_reject_before_launch():

@@ -1,6 +1,7 @@
-"""GPU parity of the MoE block with a shared expert (smx_fused_moe_shared_forward) against the
-oracle, through the C ABI: Qwen1.5-MoE-style gated shared expert, DeepSeek-V2-style ungated
-shared experts with a routed scaling factor, and the block modules."""
+"""GPU parity of the MoE block with a shared expert (smx_fused_moe_shared_forward, and
+smx_stack_fused_moe_shared on given routing) against the oracle, through the C ABI:
+Qwen1.5-MoE-style gated shared expert, DeepSeek-V2-style ungated shared experts with a routed
+scaling factor, the block modules, and DeepSeek-V2 / V3 grouped routing."""
 import numpy as np
 import pytest
 import torch
@@ -8,7 +9,8 @@ import torch
 from oracle import moe_ref as ref
 from ae_amd import _lib
 from ae_amd.layers import (DeepseekV2MoE, Qwen2MoeSparseMoeBlock, fused_moe_forward,
-                           fused_moe_shared_forward, set_weight_attrs, tiled_min_tokens)
+                           fused_moe_shared_forward, set_weight_attrs, stack_fused_moe_shared,
+                           tiled_min_tokens)
 from tests.helpers import TOL, TORCH_TO_ORACLE, f32_of, make_pool, max_rel_err, parity, to_oracle
 
 pytestmark = pytest.mark.gpu
@@ -264,3 +266,88 @@ def test_shared_block_token_chunks():
     pool, slots = make_pool(E, H, I, torch.bfloat16, seed=95)
     page = _shared_page(H, Is, torch.bfloat16, seed=96)
     _check(x, logits, pool, slots, k, False, page, None, 2.5)
+
+
+# ------------------------------------------------------- the block on the caller's routing
+def _stack_shared(x, pool, slots, w, ids, page, sgate, scale):
+    return stack_fused_moe_shared(x.clone(), pool, slots, w, ids, page, sgate, scale, inplace=False)
+
+
+def _oracle_stack_shared(x, pool, slots, w, ids, page, sgate, scale):
+    return ref.stack_fused_moe_shared(
+        to_oracle(x), to_oracle(pool), slots.cpu().numpy(), w.cpu().numpy(), ids.cpu().numpy(),
+        TORCH_TO_ORACLE[x.dtype], shared_page=None if page is None else to_oracle(page),
+        shared_gate_logits=None if sgate is None else f32_of(sgate), routed_scaling_factor=scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("T,H,I,E,k,Is,gated", [(1, 128, 128, 8, 2, 256, True),
+                                                (33, 256, 128, 16, 4, 384, False),
+                                                (130, 128, 256, 6, 3, 256, True)])
+def test_block_on_given_routing_equals_routed_block(dtype, T, H, I, E, k, Is, gated):
+    """smx_stack_fused_moe_shared on the ids and weights smx_fused_moe_shared_forward chose gives
+    that call's output bit for bit (same kernels), and matches the oracle's block."""
+    x, logits, sgate = _inputs(T, H, E, dtype, seed=T + 3 * E)
+    sgate = sgate if gated else None
+    pool, slots = make_pool(E, H, I, dtype, num_slots=E + 2, seed=E + 1)
+    page = _shared_page(H, Is, dtype, seed=Is)
+    scale = 1.0 if gated else 2.5
+    y, w, ids = fused_moe_shared_forward(x.clone(), logits, pool, slots, k, True, page, sgate,
+                                         scale, inplace=False, return_routing=True)
+    y2 = _stack_shared(x, pool, slots, w, ids, page, sgate, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    y_ref = _oracle_stack_shared(x, pool, slots, w, ids, page, sgate, scale)
+    parity(f32_of(y2), y_ref, TOL[dtype], case=f"block on given routing T={T} E={E} k={k}")
+
+
+def test_block_on_given_routing_token_chunks():
+    """3000 tokens x top-6 = 18000 assignments: two token chunks, the shared gate logits of the
+    second chunk offset with it."""
+    T, H, I, E, k, Is = 3000, 128, 128, 16, 6, 256
+    x, logits, sgate = _inputs(T, H, E, torch.bfloat16, seed=97)
+    pool, slots = make_pool(E, H, I, torch.bfloat16, seed=98)
+    page = _shared_page(H, Is, torch.bfloat16, seed=99)
+    w, ids = ref.grouped_topk(f32_of(logits), k, False, 4, 2)
+    w_t, ids_t = torch.from_numpy(w).to(DEV), torch.from_numpy(ids).to(DEV)
+    y = _stack_shared(x, pool, slots, w_t, ids_t, page, sgate, 1.0)
+    torch.cuda.synchronize()
+    y_ref = _oracle_stack_shared(x, pool, slots, w_t, ids_t, page, sgate, 1.0)
+    parity(f32_of(y), y_ref, TOL[torch.bfloat16], case="block on given routing, token chunks")
+
+
+@pytest.mark.parametrize("method,ng,tg,renorm,scale", [("group_limited_greedy", 8, 3, False, 16.0),
+                                                       ("noaux_tc", 8, 4, True, 2.5),
+                                                       ("noaux_tc", 1, 1, True, 1.0)])
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_deepseek_grouped_routing_blocks(method, ng, tg, renorm, scale, T):
+    """DeepseekV2MoE with DeepSeek-V2's group-limited top-k and DeepSeek-V3's biased sigmoid
+    top-k (reduced sizes: 64 routed experts of ffn 128, hidden 256, top-6 / top-8): the grouped
+    top-k, then the block on that routing, against the oracle's grouped top-k and block."""
+    H, I, E = 256, 128, 64
+    k = 8 if method == "noaux_tc" else 6
+    block = DeepseekV2MoE(n_routed_experts=E, num_experts_per_tok=k, hidden_size=H,
+                          moe_intermediate_size=I, n_shared_experts=2, routed_scaling_factor=scale,
+                          norm_topk_prob=renorm, params_dtype=torch.bfloat16, tp_size=1,
+                          topk_method=method, n_group=ng, topk_group=tg)
+    pool = _load_block(block, E, H, I, 2 * I, seed=71 + T)
+    bias = getattr(block.gate, "e_score_correction_bias", None)
+    if bias is not None:
+        with torch.no_grad():
+            bias.copy_(torch.randn(E, generator=torch.Generator().manual_seed(73)) * 0.05)
+    mapping = torch.randperm(E, generator=torch.Generator().manual_seed(74)).to(DEV)
+    x = torch.randn((T, H), generator=torch.Generator(device=DEV).manual_seed(75 + T),
+                    device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        logits = block.gate(x)
+        y = block(x.clone(), mapping)
+    torch.cuda.synchronize()
+    w_ref, ids_ref = ref.grouped_topk(f32_of(logits), k, renorm, ng, tg,
+                                      None if bias is None else bias.detach().cpu().numpy())
+    y_ref = ref.stack_fused_moe_shared(to_oracle(x), to_oracle(pool), mapping.cpu().numpy(), w_ref,
+                                       ids_ref, ref.BF16, shared_page=to_oracle(block.shared_ws.data),
+                                       routed_scaling_factor=scale)
+    parity(f32_of(y), y_ref, TOL[torch.bfloat16], case=f"DeepseekV2MoE {method} T={T}")
+    if method != "noaux_tc" or ng > 1:
+        # the grouping (or the bias) is in effect: some token's picks differ from plain top-k
+        assert T == 1 or (ids_ref != ref.topk_softmax(f32_of(logits), k, renorm)[1]).any()
