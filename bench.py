@@ -23,8 +23,10 @@ with us per step timed by HIP events around the K steps only; then the roofline 
 dominant kernel (gate/up), timed in a second pass of K steps with HIP events that the
 library records on the launch stream around each kernel; the parity of the layer call against
 the numpy oracle on the same inputs (ids, weight bits, both output error metrics); and the CPU
-baseline: a torch-CPU restatement of the same layer (GEMMs on MKL, weights converted to fp32
-once, outside the timing) on the host cores, median of >= 20 calls after 3 warm-up calls. The
+baseline: the same layer on the host cores through two restatements, C++ (oracle/cpu_moe.cpp,
+cblas_sgemm on MKL under OpenMP) and torch (oracle/torch_cpu.py, GEMMs on MKL), weights
+converted to fp32 once, outside the timing, median of >= 20 calls after 3 warm-up calls each;
+the faster is the baseline, the other reported beside it. The
 default Mixtral run also times 8, 16, 48 and 64 tokens (the rest of the metric's 8-64 range)
 with the same event-timed loop and reports them under "sweep", and under "workloads" the other
 configurations of the benchmark's definition: c1 (fp32, with its gate/up roofline and CPU

@@ -31,7 +31,7 @@ def max_rel_err(y: np.ndarray, want: np.ndarray) -> float:
 
 
 # Output tolerance per activation dtype: max |y - ref| / max |ref|. bf16 carries 8 mantissa
-# bits and four rounding points; the north-star bound is 1e-2.
+# bits and four rounding points; the layer's bf16 parity bound is 1e-2.
 TOL = {torch.bfloat16: 1e-2, torch.float16: 2e-3, torch.float32: 1e-4}
 TOL_BY_NAME = {"bf16": 1e-2, "f16": 2e-3, "f32": 1e-4}
 

@@ -1,6 +1,6 @@
-"""The timed CPU baseline (oracle/torch_cpu.py, torch on MKL) against the numpy oracle: same
-routing ids, weights within fp32 rounding, outputs within the parity tolerance -- so the
-baseline bench.py times computes the same layer."""
+"""The timed CPU baselines (oracle/torch_cpu.py, torch on MKL; oracle/cpu_moe.cpp, cblas_sgemm on
+MKL) against the numpy oracle: same routing ids, weights within fp32 rounding, outputs within
+the parity tolerance -- so the baselines bench.py times compute the same layer."""
 import numpy as np
 import pytest
 import torch
