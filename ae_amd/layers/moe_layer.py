@@ -6,7 +6,9 @@ specmoe/layers/layernorm.py:23-33) then ``hidden = block_sparse_moe(hidden,
 experts_mapping)`` (MixtralMoE.forward, :106-115: router gate, FusedMoE). Here the residual
 add, the norm, the router gate and the top-k run in one kernel, followed by the expert sort,
 the expert kernels and the combine (smx_moe_layer_forward). Blocks with a shared expert
-(SharedExpertMoE) run the same way, their shared-expert gate as one more router row.
+(SharedExpertMoE) run the same way, their shared-expert gate as one more router row. A block
+whose routing is not the plain top-k softmax (grouped top-k, a correction bias, a custom routing
+function) runs as the norm and then the block, two calls.
 """
 from __future__ import annotations
 
@@ -21,6 +23,7 @@ from .fused_moe_kernel import _as_index, _pool_geometry
 from .layernorm import RMSNorm
 from .mixtral_moe import MixtralMoE
 from .shared_moe import SharedExpertMoE
+from .topk import needs_grouped_topk
 
 
 def moe_layer_forward(hidden: torch.Tensor, residual: torch.Tensor, norm_weight: torch.Tensor,
@@ -84,6 +87,16 @@ class PostAttentionMoE(nn.Module):
         self.post_attention_layernorm = layernorm
         self.block_sparse_moe = block
 
+    @staticmethod
+    def _grouped_routing(blk: nn.Module) -> bool:
+        if isinstance(blk, SharedExpertMoE):
+            ng = blk.num_expert_group or 1
+            return needs_grouped_topk(blk.use_grouped_topk, blk.topk_group or ng, ng,
+                                      getattr(blk.gate, "e_score_correction_bias", None))
+        ex = blk.experts
+        return ex.custom_routing_function is not None or needs_grouped_topk(
+            ex.use_grouped_topk, ex.topk_group, ex.num_expert_group, ex.correction_bias)
+
     def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor,
                 experts_mapping: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
         blk = self.block_sparse_moe
@@ -93,6 +106,12 @@ class PostAttentionMoE(nn.Module):
         pool = getattr(blk.experts.ws, "gpu_cache", None)
         if pool is None:
             raise RuntimeError("no expert pool attached: set experts.ws.gpu_cache before forward")
+        if self._grouped_routing(blk):
+            # the fused call's top-k is the plain one: the norm (residual add in place), then
+            # the block with its grouped top-k (select_experts' use_grouped_topk branch)
+            xs, _ = self.post_attention_layernorm(h2, residual.view(-1, H))
+            blk(xs, experts_mapping)
+            return hidden_states, residual
         nw = self.post_attention_layernorm.weight.data
         if nw.dtype != h2.dtype:
             nw = nw.to(h2.dtype)
