@@ -127,3 +127,28 @@ def test_fused_moe_grouped_routing_end_to_end():
         parity(f32_of(out), y_ref, TOL[dtype], case=f"FusedMoE grouped bias={bias is not None}")
         # different picks from the ungrouped top-k on these inputs: the grouping is in effect
         assert (ids_ref != ref.topk_softmax(f32_of(logits), k, True)[1]).any()
+
+
+def test_fused_moe_grouped_routing_tiled_sizes():
+    """A prefill-sized batch (512 tokens, 16 experts, top-4: 128 expected tokens per expert, the
+    MFMA-tiled expert kernels) through FusedMoE with the biased grouped top-k, against the
+    oracle; the plan confirms the tiled kernels run."""
+    from ae_amd import _lib
+    T, H, I, E, k, ng, tg = 512, 256, 256, 16, 4, 4, 2
+    dtype = torch.bfloat16
+    assert _lib.plan_info(T, H, I, E, k, _lib.SMX_BF16)["tiled"] == 1
+    pool, slots = make_pool(E, H, I, dtype, num_slots=E, seed=63)
+    g = torch.Generator(device=DEV).manual_seed(64)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dtype)
+    logits = (torch.randn((T, E), generator=g, device=DEV) * 2.0).to(dtype)
+    bias = torch.randn(E, generator=g, device=DEV) * 0.3
+    moe = FusedMoE(num_experts=E, top_k=k, hidden_size=H, intermediate_size=I, params_dtype=dtype,
+                   tp_size=1, use_grouped_topk=True, topk_group=tg, num_expert_group=ng,
+                   correction_bias=bias)
+    set_weight_attrs(moe.ws, {"gpu_cache": pool})
+    out = moe(x.clone(), logits, slots)
+    torch.cuda.synchronize()
+    w_ref, ids_ref = _oracle(logits, k, True, ng, tg, bias)
+    y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(), w_ref, ids_ref,
+                                TORCH_TO_ORACLE[dtype])
+    parity(f32_of(out), y_ref, TOL[dtype], case="FusedMoE grouped, tiled sizes")
