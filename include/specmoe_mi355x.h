@@ -360,15 +360,20 @@ int smx_set_fp32_gemm_outputs_fp16(int on);
 int smx_fp32_gemm_outputs_fp16(void);
 
 /*
- * Small batches -- T*top_k <= 64 assignments over E <= 64 experts, T <= 32, router logits (when
- * given) in the activation dtype and at most four top-k passes of 64/G tokens -- route inside
- * the gate/up launch on the weight-streaming path: each routed workgroup computes the top-k
- * and the expert sort of the whole batch in one wave into its LDS, and one of them writes the
- * routing records and top-k results for the later kernels; no routing kernel is launched. The
- * records are the routing kernel's, bit for bit. 0 launches the routing kernels instead;
- * default 1. Process-wide. Plays the role of the reference's separate select_experts and
- * moe_align_block_size launches (specmoe/layers/FusedMoE.py:174-185,
- * specmoe/layers/fused_moe_kernel.py:329-330) for such batches.
+ * Batches on the weight-streaming path over E <= 64 experts route inside the gate/up launch:
+ * each routed workgroup computes the routing of the whole batch into its LDS and one of them
+ * writes the routing records and top-k results for the later kernels, bit for bit the routing
+ * kernels' records.
+ *   - one wave: T*top_k <= 64 assignments, every expert's tokens one pass (T <= 16 per token
+ *     tile of the plan, at most two tiles), router logits (when given) in the activation dtype
+ *     in at most four top-k passes of 64/G tokens;
+ *   - four waves (top-k), one of them sorting: router logits for T <= 64 tokens of one pass,
+ *     T*top_k <= 256, T*G <= 512; or given ids (smx_stack_fused_moe and the forward calls
+ *     whose top-k is too large to repeat, which then launch smx_topk_softmax's kernel first)
+ *     up to 768 assignments, experts over several token ranges included.
+ * Larger batches launch the routing kernels. 0 launches them always; default 1. Process-wide.
+ * Plays the role of the reference's separate select_experts and moe_align_block_size launches
+ * (specmoe/layers/FusedMoE.py:174-185, specmoe/layers/fused_moe_kernel.py:329-330).
  */
 int smx_set_routing_in_gateup(int on);
 int smx_routing_in_gateup(void);
