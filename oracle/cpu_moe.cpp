@@ -106,15 +106,20 @@ int cpu_moe_forward(const float* x, int T, int H, int I, int E, int k, const flo
     }
     const float inv = 1.0f / s;
     for (int e = 0; e < E; ++e) p[e] *= inv;
+    // rank: a NaN probability below every number, a picked expert below that (so every round
+    // picks an expert in [0, E))
+    std::vector<float> rank(p);
+    for (int e = 0; e < E; ++e)
+      if (!(rank[e] >= 0.0f)) rank[e] = -0.5f;
     float sum = 0.0f;
     for (int j = 0; j < k; ++j) {
-      int best = -1;
-      for (int e = 0; e < E; ++e)
-        if (p[e] >= 0.0f && (best < 0 || p[e] > p[best])) best = e;
+      int best = 0;
+      for (int e = 1; e < E; ++e)
+        if (rank[e] > rank[best]) best = e;
       topk_ids[static_cast<int64_t>(t) * k + j] = best;
       topk_w[static_cast<int64_t>(t) * k + j] = p[best];
       sum = (j == 0) ? p[best] : sum + p[best];
-      p[best] = -1.0f;
+      rank[best] = -1.0f;
     }
     if (renorm)
       for (int j = 0; j < k; ++j) topk_w[static_cast<int64_t>(t) * k + j] /= sum;
