@@ -50,7 +50,10 @@ __device__ __forceinline__ ChunkOrder rotated_order(int n, int index) {
   return ChunkOrder{n, q - div_small(q, n, 1.0f / static_cast<float>(n)) * n};
 }
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + __expf(-g)); }
+// The library's accurate expf (not the fast __expf): silu's value then differs from a correctly
+// rounded one by about an ulp, so the rounding of act to the activation dtype rarely flips
+// against the reference's arithmetic (one flipped act element moves every output of its term).
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 
 // Rounding of a routed GEMM output (gate/up, and the weighted down output): to the activation
 // dtype; for fp32 runs with f16out set, to fp16 -- the reference's Triton kernel stores fp32

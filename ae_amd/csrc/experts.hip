@@ -194,7 +194,7 @@ __global__ __launch_bounds__(kCombineMaxWaves * kWave) void combine_kernel(Combi
     if (c.part_s) {
       const f32x4 d = terms[c.k][lane];
       float gs = 1.0f;
-      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + __expf(-z)));
+      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + expf(-z)));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float sh = Elem<DT>::round(d[e]);
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(kCombineRowThreads) void combine_rows_kernel(Combin
         d1 += *reinterpret_cast<const f32x4*>(ssrc + sp * sstride + 4);
       }
       float gs = 1.0f;
-      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + __expf(-zs)));
+      if (gated) gs = Elem<DT>::round(1.0f / (1.0f + expf(-zs)));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         float s0 = Elem<DT>::round(d0[e]), s1 = Elem<DT>::round(d1[e]);
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(kRowsWaves * kWave) void down_rows_kernel(RowsArgs 
     if (a.scale != 1.0f) y = Elem<DT>::round(y * a.scale);
     if (shared) {
       float sh = Elem<DT>::round(vals[wave][t]);
-      if (gated) sh = Elem<DT>::round(Elem<DT>::round(1.0f / (1.0f + __expf(-zt))) * sh);
+      if (gated) sh = Elem<DT>::round(Elem<DT>::round(1.0f / (1.0f + expf(-zt))) * sh);
       y += sh;
     }
   }

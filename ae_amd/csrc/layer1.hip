@@ -214,7 +214,7 @@ __device__ void layer_down_role(const ExpertArgs& a, u32x4* stage) {
       float sh = Elem<DT>::round(vals[wave][0]);
       if (gated) {
         const float z = load_scalar(a.lo.sgate, a.lo.sgate_dtype, 0);
-        sh = Elem<DT>::round(Elem<DT>::round(1.0f / (1.0f + __expf(-z))) * sh);
+        sh = Elem<DT>::round(Elem<DT>::round(1.0f / (1.0f + expf(-z))) * sh);
       }
       y += sh;
     }
