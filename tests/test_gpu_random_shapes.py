@@ -135,3 +135,36 @@ def test_random_layer_call_matches_oracle(seed):
         logits=lgf)
     case = f"seed={seed} T={T} H={H} I={I} E={E} k={k} Is={Is} gated={gated} {dtype}"
     parity(f32_of(y), y_ref, TOL[dtype], case=case, elementwise=T * H >= 2048)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_random_prefill_shape_matches_oracle(seed):
+    """Prefill-sized batches (257-2048 tokens over 2-16 experts): the MFMA-tiled kernels, their
+    ragged last token ranges and K splits; the plan is checked to be the tiled one."""
+    from ae_amd import _lib
+    r = np.random.default_rng(7000 + seed)
+    T = int(r.choice([257, 511, 777, 1024, 1500, 2048]))
+    E = int(r.integers(2, 17))
+    k = int(r.integers(1, min(E, 4) + 1))
+    dtype = DTYPES[int(r.integers(0, 3))]
+    unit = 64 if dtype == torch.float32 else 128
+    H, I = unit * int(r.integers(1, 5)), unit * int(r.integers(1, 5))
+    code = {torch.float32: _lib.SMX_F32, torch.float16: _lib.SMX_F16, torch.bfloat16: _lib.SMX_BF16}[dtype]
+    if not _lib.plan_info(T, H, I, E, k, code)["tiled"]:
+        T = 2048  # enough tokens per expert for the tiled kernels at any E <= 16, k >= 1
+    assert _lib.plan_info(T, H, I, E, k, code)["tiled"] == 1
+    g = torch.Generator(device=DEV).manual_seed(4000 + seed)
+    x = torch.randn((T, H), generator=g, device=DEV).to(dtype)
+    logits = (torch.randn((T, E), generator=g, device=DEV) * 2.0).to(dtype)
+    pool = (torch.randn((E, 3 * I * H), generator=g, device=DEV) * 0.02).to(dtype)
+    slots = torch.randperm(E, generator=torch.Generator().manual_seed(seed)).to(DEV)
+    renorm = bool(r.random() < 0.5)
+    y, w, ids = fused_moe_forward(x.clone(), logits, pool, slots, k, renorm, inplace=False,
+                                  return_routing=True)
+    torch.cuda.synchronize()
+    y_ref, w_ref, ids_ref = ref.fused_moe_forward(to_oracle(x), f32_of(logits), to_oracle(pool),
+                                                  slots.cpu().numpy(), k, renorm, TORCH_TO_ORACLE[dtype])
+    case = f"seed={seed} T={T} H={H} I={I} E={E} k={k} renorm={renorm} {dtype}"
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref, err_msg=case)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32), err_msg=case)
+    parity(f32_of(y), y_ref, TOL[dtype], case=case)
