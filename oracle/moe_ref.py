@@ -39,8 +39,9 @@ GEMM accumulation order is not restated; outputs agree to a stated tolerance.
 
 Parity pinning (tests/test_oracle.py): the align docstring example; brute-force sorting;
 top-k against np.argsort/lexsort selection and hand-built tie cases; the grouped top-k against
-a Python sorted() re-derivation, the plain top-k where grouping removes nothing, and
-hand-worked cases (sigmoid_scores within 3 ulp of float64); exp_nonpos against float64
+a Python sorted() re-derivation, the plain top-k where grouping removes nothing, hand-worked
+cases (sigmoid_scores within 3 ulp of float64) and transformers' DeepSeek-V2 / V3 router
+modules (the same picks and weights); exp_nonpos against float64
 exp (<= 2 ulp); the expert math against a float64 textbook SwiGLU MoE built from separate
 gate/up/down matrices through the page packing; the shared-expert block against a float64
 textbook block and its reductions (zero shared page -> routed result, zero routed pages ->

@@ -573,3 +573,54 @@ def test_router_logits_and_layer_composition():
     y2, w2, ids2 = ref.fused_moe_forward(ref.f32_to_bf16_bits(xn), lg, pool, slots, k, True, dt)
     np.testing.assert_array_equal(y, y2)
     np.testing.assert_array_equal(ids, ids2)
+
+
+def _hf_deepseek_router(version, E, k, ng, tg, renorm, bias):
+    """transformers' DeepSeek-V2 / V3 router modules (an independent implementation of the same
+    routing) with an identity gate, so that their logits are the given ones exactly."""
+    pytest.importorskip("transformers")
+    import torch
+    from types import SimpleNamespace
+    if version == 2:
+        from transformers.models.deepseek_v2.modeling_deepseek_v2 import DeepseekV2TopkRouter
+        cfg = SimpleNamespace(num_experts_per_tok=k, num_experts=E, hidden_size=E,
+                              routed_scaling_factor=1.0, topk_method="group_limited_greedy",
+                              n_group=ng, topk_group=tg)
+        r = DeepseekV2TopkRouter(cfg)
+    else:
+        from transformers.models.deepseek_v3.modeling_deepseek_v3 import DeepseekV3TopkRouter
+        cfg = SimpleNamespace(num_experts_per_tok=k, num_local_experts=E, hidden_size=E,
+                              routed_scaling_factor=1.0, n_group=ng, topk_group=tg,
+                              norm_topk_prob=renorm)
+        r = DeepseekV3TopkRouter(cfg)
+        r.e_score_correction_bias.copy_(torch.from_numpy(bias))
+    with torch.no_grad():
+        r.weight.copy_(torch.eye(E))
+    return r
+
+
+@pytest.mark.parametrize("version,E,ng,tg,k,renorm", [(2, 160, 8, 3, 6, False), (2, 64, 8, 2, 6, False),
+                                                      (2, 16, 4, 2, 3, False), (3, 256, 8, 4, 8, True),
+                                                      (3, 64, 8, 2, 6, True), (3, 32, 4, 1, 4, False)])
+def test_grouped_topk_against_transformers_deepseek_routers(version, E, ng, tg, k, renorm):
+    """The grouped top-k against transformers' DeepseekV2TopkRouter (group-limited greedy:
+    softmax, group max) and DeepseekV3TopkRouter (sigmoid + correction bias, top-2 group sums):
+    the same experts for every token (their torch.topk(sorted=False) leaves the order open, so
+    picks are compared as sets) and the same weight per expert, to fp32 rounding (torch's exp
+    and, for V3, its +1e-20 in the renormalising sum)."""
+    import torch
+    rng = np.random.default_rng(E + 10 * version + k)
+    T = 64
+    logits = (rng.standard_normal((T, E)) * 2).astype(np.float32)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32) if version == 3 else None
+    router = _hf_deepseek_router(version, E, k, ng, tg, renorm, bias)
+    with torch.no_grad():
+        hf_logits, w_hf, ids_hf = router(torch.from_numpy(logits))
+    np.testing.assert_array_equal(hf_logits.numpy(), logits)  # the identity gate is exact
+    w, ids = ref.grouped_topk(logits, k, renorm, ng, tg, bias)
+    ids_hf = ids_hf.numpy()
+    w_hf = w_hf.numpy()
+    for t in range(T):
+        assert sorted(ids[t].tolist()) == sorted(ids_hf[t].tolist()), t
+        by_id = dict(zip(ids_hf[t].tolist(), w_hf[t].tolist()))
+        np.testing.assert_allclose(w[t], [by_id[e] for e in ids[t].tolist()], rtol=3e-6, atol=0)
