@@ -48,7 +48,7 @@ textbook block and its reductions (zero shared page -> routed result, zero route
 dense MLP, saturated gate -> ungated / routed only). No reference test vectors exist beyond
 the align docstring example (the reference ships no tests). Parity of the shared-expert block
 with the reference is unpinned: the reference has no such block; it is pinned to the public
-architecture only.
+architectures, in fp32 against transformers' Qwen2MoeSparseMoeBlock and DeepseekV2Moe modules.
 """
 from __future__ import annotations
 

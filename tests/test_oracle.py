@@ -624,3 +624,55 @@ def test_grouped_topk_against_transformers_deepseek_routers(version, E, ng, tg, 
         assert sorted(ids[t].tolist()) == sorted(ids_hf[t].tolist()), t
         by_id = dict(zip(ids_hf[t].tolist(), w_hf[t].tolist()))
         np.testing.assert_allclose(w[t], [by_id[e] for e in ids[t].tolist()], rtol=3e-6, atol=0)
+
+
+@pytest.mark.parametrize("kind", ["qwen2_moe", "deepseek_v2_greedy", "deepseek_v2_grouped"])
+def test_shared_block_against_transformers_modules(kind):
+    """The shared-expert block (and, for DeepSeek-V2, its group-limited routing) against
+    transformers' Qwen2MoeSparseMoeBlock and DeepseekV2Moe in fp32, an independent
+    implementation of the public architectures: the oracle in fp32 (no rounding points) on the
+    same weights, packed into pool pages and a shared page, agrees to fp32 summation order."""
+    pytest.importorskip("transformers")
+    import torch
+    from transformers import DeepseekV2Config, Qwen2MoeConfig
+    torch.manual_seed(3)
+    T, H, I, E, k = 12, 128, 64, 16, 4
+    if kind == "qwen2_moe":
+        from transformers.models.qwen2_moe.modeling_qwen2_moe import Qwen2MoeSparseMoeBlock
+        cfg = Qwen2MoeConfig(hidden_size=H, num_experts=E, num_experts_per_tok=k,
+                             moe_intermediate_size=I, shared_expert_intermediate_size=192,
+                             norm_topk_prob=False)
+        blk = Qwen2MoeSparseMoeBlock(cfg).float()
+        router_w, shared, scale, ng, tg = blk.gate.weight, blk.shared_expert, 1.0, 1, 1
+    else:
+        from transformers.models.deepseek_v2.modeling_deepseek_v2 import DeepseekV2Moe
+        grouped = kind.endswith("grouped")
+        cfg = DeepseekV2Config(hidden_size=H, n_routed_experts=E, num_experts_per_tok=k,
+                               moe_intermediate_size=I, n_shared_experts=2,
+                               n_group=4 if grouped else 1, topk_group=2 if grouped else 1,
+                               topk_method="group_limited_greedy" if grouped else "greedy",
+                               routed_scaling_factor=2.0, hidden_act="silu")
+        blk = DeepseekV2Moe(cfg).float()
+        router_w, shared, scale = blk.gate.weight, blk.shared_experts, 2.0
+        ng, tg = (4, 2) if grouped else (1, 1)
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.copy_(torch.randn(p.shape) * 0.05)
+        x = torch.randn((1, T, H))
+        y_hf = blk(x).reshape(T, H).numpy()
+    xs = x.reshape(T, H).numpy()
+    logits = (xs.astype(np.float64) @ router_w.detach().numpy().T.astype(np.float64)).astype(np.float32)
+    gu = blk.experts.gate_up_proj.detach().numpy()   # [E, 2I, H]: gate rows, then up rows
+    dn = blk.experts.down_proj.detach().numpy()      # [E, H, I]
+    pool = np.concatenate([gu.reshape(E, -1), dn.reshape(E, -1)], axis=1)  # [W1 | W3 | W2]
+    page_s = np.concatenate([shared.gate_proj.weight.detach().numpy().reshape(-1),
+                             shared.up_proj.weight.detach().numpy().reshape(-1),
+                             shared.down_proj.weight.detach().numpy().reshape(-1)])
+    sgl = None
+    if kind == "qwen2_moe":
+        sgl = (xs.astype(np.float64) @ blk.shared_expert_gate.weight.detach().numpy().T).astype(np.float32)
+    w, ids = ref.grouped_topk(logits, k, False, ng, tg)
+    y = ref.stack_fused_moe_shared(xs, pool, np.arange(E), w, ids, ref.F32, shared_page=page_s,
+                                   shared_gate_logits=sgl, routed_scaling_factor=scale)
+    err = np.abs(y - y_hf).max() / np.abs(y_hf).max()
+    assert err < 2e-5, err
