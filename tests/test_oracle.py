@@ -676,3 +676,31 @@ def test_shared_block_against_transformers_modules(kind):
                                    shared_gate_logits=sgl, routed_scaling_factor=scale)
     err = np.abs(y - y_hf).max() / np.abs(y_hf).max()
     assert err < 2e-5, err
+
+
+def test_routed_layer_against_transformers_mixtral_block():
+    """The routed layer (FusedMoE's math: softmax top-2, renormalised, SwiGLU experts over pool
+    pages) against transformers' MixtralSparseMoeBlock in fp32 -- the public implementation of
+    the reference's model (specmoe/models/mixtral.py:59-115) -- on the same weights."""
+    pytest.importorskip("transformers")
+    import torch
+    from transformers import MixtralConfig
+    from transformers.models.mixtral.modeling_mixtral import MixtralSparseMoeBlock
+    torch.manual_seed(4)
+    T, H, I, E, k = 20, 128, 96 * 2, 8, 2
+    cfg = MixtralConfig(hidden_size=H, intermediate_size=I, num_local_experts=E, num_experts_per_tok=k)
+    blk = MixtralSparseMoeBlock(cfg).float().eval()
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.copy_(torch.randn(p.shape) * 0.05)
+        x = torch.randn((1, T, H))
+        y_hf = blk(x).reshape(T, H).numpy()
+    xs = x.reshape(T, H).numpy()
+    logits = (xs.astype(np.float64) @ blk.gate.weight.detach().numpy().T.astype(np.float64)).astype(np.float32)
+    gu = blk.experts.gate_up_proj.detach().numpy()
+    dn = blk.experts.down_proj.detach().numpy()
+    pool = np.concatenate([gu.reshape(E, -1), dn.reshape(E, -1)], axis=1)
+    slots = np.array([3, 0, 7, 1, 6, 2, 5, 4])  # through a permuted slot map
+    y, _, _ = ref.fused_moe_forward(xs, logits, pool[np.argsort(slots)], slots, k, True, ref.F32)
+    err = np.abs(y - y_hf).max() / np.abs(y_hf).max()
+    assert err < 2e-5, err
