@@ -1077,10 +1077,10 @@ int smx_add_rmsnorm_gate(const void* hidden, void* residual, void* normed_out, i
   if (T < 0 || !std::isfinite(eps) || eps < 0.0f) return SMX_ERR_INVALID_ARG;
   int rc = check_norm(H, dtype);
   if (rc != SMX_OK) return rc;
-  if (gate_weight && (E <= 0 || !router_logits)) return SMX_ERR_INVALID_ARG;
+  if (gate_weight && E <= 0) return SMX_ERR_INVALID_ARG;
   if (gate_weight && E > kMaxExperts) return SMX_ERR_UNSUPPORTED;
-  if (T == 0) return SMX_OK;
-  if (!hidden || !normed_out || !norm_weight) return SMX_ERR_INVALID_ARG;
+  if (T == 0) return SMX_OK;  // empty batch: tensors may have null data pointers
+  if (!hidden || !normed_out || !norm_weight || (gate_weight && !router_logits)) return SMX_ERR_INVALID_ARG;
   if (!aligned16(hidden) || !aligned16(normed_out) || !aligned16(norm_weight) ||
       (residual && !aligned16(residual)) || (gate_weight && !aligned16(gate_weight)))
     return SMX_ERR_MISALIGNED;

@@ -325,6 +325,8 @@ def test_norm_gate_rejects_before_launch():
     assert call(a0=VP(0x10008)) == _lib.SMX_ERR_MISALIGNED
     assert call(a0=VP(0)) == _lib.SMX_ERR_INVALID_ARG
     assert call(a4=0) == _lib.SMX_OK
+    # an empty batch's tensors may have null data pointers (torch's [0, n] tensors do)
+    assert call(a4=0, a0=VP(0), a1=VP(0), a2=VP(0), a10=VP(0)) == _lib.SMX_OK
 
 
 def test_layer_forward_rejects_before_launch():
