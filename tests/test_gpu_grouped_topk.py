@@ -152,3 +152,38 @@ def test_fused_moe_grouped_routing_tiled_sizes():
     y_ref = ref.stack_fused_moe(to_oracle(x), to_oracle(pool), slots.cpu().numpy(), w_ref, ids_ref,
                                 TORCH_TO_ORACLE[dtype])
     parity(f32_of(out), y_ref, TOL[dtype], case="FusedMoE grouped, tiled sizes")
+
+
+@pytest.mark.parametrize("T", [1, 8, 32])
+def test_deepseek_v3_full_size_block(T):
+    """The DeepSeek-V3 MoE block at full size: 256 routed experts (the library's maximum) of ffn
+    2048, hidden 7168, the sigmoid top-8 with correction bias over 8 groups of which 4 stay
+    selectable, renormalised, routed scaling 2.5, one shared expert of ffn 2048 -- the grouped
+    top-k, then stack_fused_moe_shared on that routing. The 22.5 GB pool stays on the GPU; the
+    oracle gets the picked experts' pages only (a compact pool and slot map)."""
+    from ae_amd.layers import grouped_topk, stack_fused_moe_shared
+    H, I, E, k, ng, tg, Is, scale = 7168, 2048, 256, 8, 8, 4, 2048, 2.5
+    g = torch.Generator(device=DEV).manual_seed(500 + T)
+    pool = torch.empty((E, 3 * I * H), dtype=torch.bfloat16, device=DEV)
+    for e in range(E):
+        pool[e].normal_(0.0, 0.02, generator=g)
+    slots = torch.randperm(E, generator=torch.Generator().manual_seed(501)).to(DEV)
+    page = (torch.randn((3 * Is * H,), generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    x = torch.randn((T, H), generator=g, device=DEV).to(torch.bfloat16)
+    logits = (torch.randn((T, E), generator=g, device=DEV) * 2.0).to(torch.bfloat16)
+    bias = torch.randn((E,), generator=g, device=DEV) * 0.1
+    w, ids = grouped_topk(logits, k, True, ng, tg, bias)
+    y = stack_fused_moe_shared(x.clone(), pool, slots, w, ids, page, None, scale, inplace=False)
+    torch.cuda.synchronize()
+    w_ref, ids_ref = ref.grouped_topk(f32_of(logits), k, True, ng, tg, bias.cpu().numpy())
+    np.testing.assert_array_equal(ids.cpu().numpy(), ids_ref)
+    np.testing.assert_array_equal(w.cpu().numpy().view(np.uint32), w_ref.view(np.uint32))
+    picked = np.unique(ids_ref)
+    compact = to_oracle(pool[slots[torch.from_numpy(picked).to(DEV)]])
+    cslots = np.full(E, -1, dtype=np.int64)
+    cslots[picked] = np.arange(picked.size)
+    del pool
+    torch.cuda.empty_cache()
+    y_ref = ref.stack_fused_moe_shared(to_oracle(x), compact, cslots, w_ref, ids_ref, ref.BF16,
+                                       shared_page=to_oracle(page), routed_scaling_factor=scale)
+    parity(f32_of(y), y_ref, TOL[torch.bfloat16], case=f"DeepSeek-V3 block T={T}")
