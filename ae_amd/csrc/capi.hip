@@ -353,6 +353,16 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
       p.down_rows = 1;
       down_split(1);
     } else if (b2 > kDownFillBlocks && last > 0 && 2 * last <= kDownFillBlocks) {
+      // Up to four residencies where every active expert is expected to hold at most two
+      // assignments (its down items are then plain weight streams, whose time follows their
+      // bytes) and a W2 row is not a power-of-two number of bytes. Measured, us per layer, two ->
+      // four residencies: Mixtral-8x7B 4 tokens 269.1 -> 265.4 (4 -> 8 splits), DBRX 1 token
+      // 249.1 -> 243.6, 4 tokens 584.8 -> 582.5, Qwen1.5-MoE 12 tokens 110.4 -> 108.6,
+      // DeepSeek-V2-Lite 12 tokens 150.0 -> 147.0; Mixtral-8x22B (ffn 16384: 32 KB rows) 2 tokens
+      // 367.5 -> 381.6 with 8 splits of 4 KB, hence the pitch condition.
+      const int64_t w2_row = I * eb;
+      const bool wide = static_cast<double>(p.N) <= 2.0 * active && (w2_row & (w2_row - 1)) != 0;
+      const int64_t cap = (wide ? 4 : 2) * kDownFillBlocks;
       double best = rounds_per_byte(b2) * (1.0 - 1e-9);
       int best_r = kDownRows;
       int64_t best_s = s;
@@ -361,7 +371,7 @@ Plan make_plan(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k, int dtype,
           if (nchunks % d != 0) continue;
           const int64_t b = down_grid(R, d, nullptr);
           const double c = rounds_per_byte(b);
-          if (b <= 2 * kDownFillBlocks && c < best) {
+          if (b <= cap && c < best) {
             best = c;
             best_r = R;
             best_s = d;
